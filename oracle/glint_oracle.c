@@ -1,0 +1,246 @@
+/* TEST INFRASTRUCTURE ONLY — the CPU oracle for GLINT's hot path.
+ *
+ * Plain-C restatement of the reference's arithmetic, used by tests/, by
+ * __graft_entry__.smoke() and by bench.py's cpu_baseline leg as the checker. Nothing
+ * in glint_amd/ links, loads or calls it. Every function cites the reference file:line
+ * whose semantics it restates. Build: oracle/Makefile -> oracle/liboracle.so.
+ *
+ * Pinning (what checks each function, see tests/test_oracle.py):
+ *   oracle_encode_*    known answers (gpu_ok vector, zero block, NaN, odd pad), the numpy
+ *                      searchsorted restatement on the reference's own edge corpus, and a
+ *                      pure-Python f64 restatement of glint_codec.encode on the
+ *                      reference's seeded data;
+ *   oracle_expand_*    a single f32 multiply; BF16 RNE known answers from
+ *                      test_glint_tools.py:31-37; the -0.0 zero-block answer;
+ *   oracle_htile_*     float64 brute force and the Python tile simulator order;
+ *   oracle_quant_act / oracle_int8_*   exact integer brute force (numpy int64 matmul)
+ *                      and rint ties-to-even known answers.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "../include/glint_cells.h"
+
+#define EXPORT __attribute__((visibility("default")))
+
+static float bf16_to_f32(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* f32 -> bf16 bits, round to nearest even, NaN -> (u >> 16) | 0x40
+ * (glint_np.py:25-31, dtype_io.py:32-42). */
+EXPORT uint16_t oracle_f32_to_bf16_one(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if (isnan(f))
+        return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+EXPORT void oracle_f32_to_bf16(const float *in, int64_t n, uint16_t *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = oracle_f32_to_bf16_one(in[i]);
+}
+
+/* nearest16(): first index of the minimum |v - tab[k]|, strict '<'
+ * (glint_encode.cu:67-79). */
+static int nearest16(const float *tab, float v) {
+    int best = 0;
+    float bd = fabsf(v - tab[0]);
+    for (int k = 1; k < 16; ++k) {
+        const float d = fabsf(v - tab[k]);
+        if (d < bd) {
+            bd = d;
+            best = k;
+        }
+    }
+    return best;
+}
+
+/* Block absmax: max |w| over the block, NaN skipped because fabsf(NaN) > m is false
+ * (glint_encode.cu:41-66, glint_np.py:32-40). */
+static void block_absmax(const float *w, int64_t n, int bs, float *absmax) {
+    const int64_t nb = (n + bs - 1) / bs;
+#pragma omp parallel for schedule(static)
+    for (int64_t b = 0; b < nb; ++b) {
+        float m = 0.f;
+        const int64_t e = (b + 1) * bs < n ? (b + 1) * bs : n;
+        for (int64_t i = b * bs; i < e; ++i) {
+            const float a = fabsf(w[i]);
+            if (a > m)
+                m = a;
+        }
+        absmax[b] = m;
+    }
+}
+
+/* Encode (glint_encode.cu:80-102): v = (s == 0) ? 0 : w / s in f32; hole = nearest
+ * parent, plug = nearest child of that parent; element 2e in the low nibble of byte e,
+ * 2e+1 in the high nibble, high pad nibble 0 for odd n. Returns 0, or -1 for bs <= 0. */
+EXPORT int oracle_encode_f32(const float *w, int64_t n, int bs, uint8_t *hole, uint8_t *plug, float *absmax) {
+    if (bs <= 0 || n < 0)
+        return -1;
+    block_absmax(w, n, bs, absmax);
+    const int64_t npack = (n + 1) / 2;
+#pragma omp parallel for schedule(static)
+    for (int64_t e = 0; e < npack; ++e) {
+        int h[2] = {0, 0}, p[2] = {0, 0};
+        for (int t = 0; t < 2; ++t) {
+            const int64_t i = 2 * e + t;
+            if (i >= n)
+                break;
+            const float s = absmax[i / bs];
+            const float v = (s == 0.f) ? 0.f : (w[i] / s);
+            h[t] = nearest16(GLINT_PARENT, v);
+            p[t] = nearest16(GLINT_CELLS[h[t]], v);
+        }
+        hole[e] = (uint8_t)((h[0] & 15) | ((h[1] & 15) << 4));
+        plug[e] = (uint8_t)((p[0] & 15) | ((p[1] & 15) << 4));
+    }
+    return 0;
+}
+
+/* BF16 input: widen (exact) then encode (glint_encode.cu:35-40, 182-204). `scratch`
+ * holds n floats. */
+EXPORT int oracle_encode_bf16(const uint16_t *w, int64_t n, int bs, uint8_t *hole, uint8_t *plug, float *absmax,
+                              float *scratch) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        scratch[i] = bf16_to_f32(w[i]);
+    return oracle_encode_f32(scratch, n, bs, hole, plug, absmax);
+}
+
+static inline int nib(const uint8_t *pk, int64_t i) { return (pk[i >> 1] >> (4 * (int)(i & 1))) & 15; }
+
+/* out[i] = CELLS[h][p] * absmax[i / bs] (glint_encode.cu:103-114, glint_np.py:84-92). */
+EXPORT void oracle_expand_f32(const uint8_t *hole, const uint8_t *plug, const float *absmax, int64_t n, int bs,
+                              float *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = GLINT_CELLS[nib(hole, i)][nib(plug, i)] * absmax[i / bs];
+}
+
+/* Unpin to BF16: RNE of the f32 expand (glint_unpin.py:25-32). */
+EXPORT void oracle_expand_bf16(const uint8_t *hole, const uint8_t *plug, const float *absmax, int64_t n, int bs,
+                               uint16_t *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = oracle_f32_to_bf16_one(GLINT_CELLS[nib(hole, i)][nib(plug, i)] * absmax[i / bs]);
+}
+
+/* H-TILE, f32 in the reference kernel's order (glint_htile.cu:142-163,
+ * glint_htile_sim.py:22-50): acc += (cell * absmax) * x for k ascending. */
+EXPORT void oracle_htile_f32(const uint8_t *hole, const uint8_t *plug, const float *absmax, const uint16_t *x,
+                             float *y, int M, int N, int K, int bs) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            float acc = 0.f;
+            for (int k = 0; k < K; ++k) {
+                const int64_t i = (int64_t)n * K + k;
+                const float wv = GLINT_CELLS[nib(hole, i)][nib(plug, i)] * absmax[i / bs];
+                acc += wv * bf16_to_f32(x[(int64_t)m * K + k]);
+            }
+            y[(int64_t)m * N + n] = acc;
+        }
+}
+
+/* Same sum in double (test_htile_k_bounds_device.cu:90-98); also returns
+ * sum |terms| per output in `abs_sum` (may be NULL) for error bounds. */
+EXPORT void oracle_htile_f64(const uint8_t *hole, const uint8_t *plug, const float *absmax, const uint16_t *x,
+                             double *y, double *abs_sum, int M, int N, int K, int bs) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            double acc = 0, aacc = 0;
+            for (int k = 0; k < K; ++k) {
+                const int64_t i = (int64_t)n * K + k;
+                const double t = (double)(GLINT_CELLS[nib(hole, i)][nib(plug, i)] * absmax[i / bs]) *
+                                 (double)bf16_to_f32(x[(int64_t)m * K + k]);
+                acc += t;
+                aacc += fabs(t);
+            }
+            y[(int64_t)m * N + n] = acc;
+            if (abs_sum)
+                abs_sum[(int64_t)m * N + n] = aacc;
+        }
+}
+
+/* Activation quantization per (row, 64-block): s = amax > 0 ? amax / 127 : 1,
+ * q = clamp(rint(x / s), -127, 127) (int8_mma_gemm.cu:11-29). k % 64 == 0. */
+EXPORT void oracle_quant_act(const uint16_t *x, int m, int k, int8_t *xq, float *sx) {
+    const int nkb = k / 64;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int r = 0; r < m; ++r)
+        for (int kb = 0; kb < nkb; ++kb) {
+            const int64_t base = (int64_t)r * k + (int64_t)kb * 64;
+            float am = 0.f;
+            for (int t = 0; t < 64; ++t)
+                am = fmaxf(am, fabsf(bf16_to_f32(x[base + t])));
+            const float s = (am > 0.f) ? (am / 127.f) : 1.f;
+            sx[(int64_t)r * nkb + kb] = s;
+            for (int t = 0; t < 64; ++t) {
+                int v = (int)rintf(bf16_to_f32(x[base + t]) / s);
+                v = v > 127 ? 127 : (v < -127 ? -127 : v);
+                xq[base + t] = (int8_t)v;
+            }
+        }
+}
+
+/* W8A8 per-64-slice arithmetic (test_int8_mma_gemm.cu:89-112, p7_abi_selftest.cu:118-125):
+ * ic = exact int32 sum over the slice; acc += ((float)ic * sx) * sw, kb ascending. */
+EXPORT void oracle_int8_mma_emu(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw, int m, int n,
+                                int k, float *y) {
+    const int nkb = k / 64;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j) {
+            float acc = 0.f;
+            for (int kb = 0; kb < nkb; ++kb) {
+                int ic = 0;
+                for (int t = 0; t < 64; ++t)
+                    ic += (int)xq[(int64_t)i * k + kb * 64 + t] * (int)wq[(int64_t)j * k + kb * 64 + t];
+                const float a = (float)ic * sx[(int64_t)i * nkb + kb];
+                acc += a * sw[(int64_t)j * nkb + kb];
+            }
+            y[(int64_t)i * n + j] = acc;
+        }
+}
+
+/* Raw INT8 GEMM: C[m,n] = sum_k A[m,k] * B[n,k] in int32 (exact: |C| <= K*127^2).
+ * Only rows [row0, row1) are computed (a bounded sample for timing). */
+EXPORT void oracle_int8_gemm_i32(const int8_t *A, const int8_t *B, int M, int N, int K, int row0, int row1,
+                                 int32_t *C) {
+    (void)M;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int i = row0; i < row1; ++i)
+        for (int j = 0; j < N; ++j) {
+            int32_t acc = 0;
+            const int8_t *a = A + (int64_t)i * K, *b = B + (int64_t)j * K;
+            for (int t = 0; t < K; ++t)
+                acc += (int32_t)a[t] * (int32_t)b[t];
+            C[(int64_t)i * N + j] = acc;
+        }
+}
+
+/* Scaled output of the raw GEMM: bf16 RNE of ((float)C * sa[m]) * sb[n]. */
+EXPORT void oracle_int8_scale_bf16(const int32_t *C, const float *sa, const float *sb, int M, int N, uint16_t *out) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j)
+            out[(int64_t)i * N + j] = oracle_f32_to_bf16_one(((float)C[(int64_t)i * N + j] * sa[i]) * sb[j]);
+}
+
+EXPORT int oracle_threads(void) {
+#ifdef _OPENMP
+    extern int omp_get_max_threads(void);
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,301 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+Each test checks the oracle against something other than its own formula: published
+hashes, known answers derived by hand from the table, the reference's own seeded
+test data and edge corpus, brute force, or an independent restatement.
+"""
+import hashlib
+import math
+import random
+import struct
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import glint_oracle as G
+from glint_amd import codebook
+
+ROOT = Path(__file__).resolve().parent.parent
+REF_BUILT = ROOT / "oracle" / "_ref"
+
+
+def _gauss(n, seed, scale=0.02):
+    """random.Random(seed).gauss(0, scale): the reference tests' generator
+    (test_glint_tools.py:28-30), reproducible from the standard library."""
+    rng = random.Random(seed)
+    return [rng.gauss(0.0, scale) for _ in range(n)]
+
+
+# ------------------------------------------------------------------- tables
+def test_cells_hash_matches_published_codebook():
+    assert codebook.cells_sha256() == codebook.CELLS_SHA256
+    assert hashlib.sha256(G.CELLS_F32.astype("<f4").tobytes()).hexdigest() == codebook.CELLS_SHA256
+
+
+def test_committed_header_is_generated_from_definition():
+    assert (ROOT / "include" / "glint_cells.h").read_text() == codebook.header_text()
+
+
+def test_parent_table_is_nf4_in_f32():
+    assert [float(x) for x in G.PARENT_F32] == [codebook.f32(x) for x in codebook.PARENT]
+
+
+def test_table_structure():
+    flat = G.CELLS_FLAT
+    assert np.all(np.diff(flat) > 0), "flattened table must be strictly ascending"
+    edges = codebook.voronoi_edges()
+    for k in range(16):  # each row lies inside its parent's Voronoi cell
+        assert edges[k] <= G.CELLS_F32[k, 0] and G.CELLS_F32[k, 15] <= edges[k + 1]
+
+
+@pytest.mark.skipif(not (REF_BUILT / "ref_cells.bin").is_file(), reason="oracle/_ref not built (no /root/reference)")
+def test_cells_equal_reference_header_bytes():
+    assert (REF_BUILT / "ref_cells.bin").read_bytes() == G.CELLS_F32.astype("<f4").tobytes()
+
+
+@pytest.mark.skipif(not (REF_BUILT / "test_cells").is_file(), reason="oracle/_ref not built")
+def test_reference_host_tests_pass():
+    for exe, marker in (("test_cells", "TEST_CELLS_OK"), ("test_htile_k_bounds", "PASS 5 K-tail")):
+        out = subprocess.run([str(REF_BUILT / exe)], capture_output=True, text=True, timeout=120)
+        assert out.returncode == 0 and marker in out.stdout, out.stdout + out.stderr
+
+
+# ------------------------------------------------------------------- encode KATs
+def test_kat_gpu_ok_vector(oracle):
+    """glint_cuda.py:79-85 encodes b"\\x80\\x3f\\x00\\x00" = [1.0, 0.0]: 1.0 is parent 15 /
+    child 15 (CELLS[15][15]=0.992 is the largest); 0.0 is parent 7 / child 8
+    (|0 - (-1.85e-4)| < |0 - 5.13e-3|)."""
+    u16 = np.frombuffer(b"\x80\x3f\x00\x00", dtype="<u2")
+    for hole, plug, am in (oracle.encode_bf16(u16, 64), G.encode_bf16(u16, 64)):
+        assert bytes(hole) == b"\x7f" and bytes(plug) == b"\x8f"
+        assert am.tolist() == [1.0]
+
+
+def test_kat_zero_block_and_negative_zero(oracle):
+    u16 = np.zeros(64, np.uint16)
+    hole, plug, am = oracle.encode_bf16(u16, 64)
+    assert set(hole.tolist()) == {0x77} and set(plug.tolist()) == {0x88} and am.tolist() == [0.0]
+    out = oracle.expand_bf16(hole, plug, am, 64, 64)
+    assert set(out.tolist()) == {0x8000}, "CELLS[7][8] < 0 times 0 is -0.0"
+
+
+def test_kat_nan_inf_handling(oracle):
+    w = np.full(128, 0.5, np.float32)
+    w[3] = np.nan          # block 0: NaN skipped by absmax, encodes as (0, 0)
+    w[64:128] = 0.0
+    w[70] = np.nan         # block 1: absmax 0 -> v = 0 for every element, NaN too
+    hole, plug, am = oracle.encode_f32(w, 64)
+    assert am.tolist() == [0.5, 0.0]
+    h = G.unpack_nibbles(hole, 128)
+    p = G.unpack_nibbles(plug, 128)
+    assert (h[3], p[3]) == (0, 0)
+    assert (h[70], p[70]) == (7, 8)
+    assert (h[0], p[0]) == (15, 15)
+    w2 = np.array([np.inf, 1.0, -2.0, 0.0], np.float32)   # absmax inf: inf/inf = NaN -> (0,0), finite/inf = 0
+    hole2, plug2, am2 = oracle.encode_f32(w2, 64)
+    assert math.isinf(am2[0])
+    assert G.unpack_nibbles(hole2, 4).tolist() == [0, 7, 7, 7] and G.unpack_nibbles(plug2, 4).tolist() == [0, 8, 8, 8]
+    for impl in (oracle.encode_f32, G.encode_f32):
+        a = impl(w, 64)
+        assert bytes(a[0]) == bytes(hole) and bytes(a[1]) == bytes(plug)
+
+
+def test_kat_odd_n_pad_nibble(oracle):
+    u16 = G.f32_to_bf16_bits(np.float32([0.1, -0.3, 0.7]))
+    hole, plug, _ = oracle.encode_bf16(u16, 64)
+    assert hole.size == 2 and (hole[-1] >> 4) == 0 and (plug[-1] >> 4) == 0
+
+
+# --------------------------------------------------------- encode vs reference data
+def test_numpy_nearest_equals_linear_scan_on_reference_edge_corpus(oracle):
+    """The reference's own corpus (test_glint_tools.py:186-213): table points,
+    midpoints, their f32 neighbours, +-0, +-1 and 50k uniform values (default_rng(0)).
+    The C oracle is a literal linear scan; the numpy path is searchsorted."""
+    f, par = G.CELLS_FLAT, G.PARENT_F32
+    mids = ((f[1:] + f[:-1]) / 2).astype(np.float32)
+    pmid = ((par[1:] + par[:-1]) / 2).astype(np.float32)
+    up = lambda a: np.nextafter(a, np.float32(2))
+    dn = lambda a: np.nextafter(a, np.float32(-2))
+    rng = np.random.default_rng(0)
+    v = np.concatenate([f, mids, pmid, par, up(mids), dn(mids), up(pmid), dn(pmid), up(f), dn(f),
+                        np.float32([1, -1, 0, -0.0]), rng.uniform(-1, 1, 50000).astype(np.float32)]).astype(np.float32)
+    # absmax 1.0 in every block makes v = w exactly; put a 1.0 at each block start.
+    bs = 64
+    n = v.size
+    blocks = (n + bs - 2) // (bs - 1)
+    w = np.zeros(blocks * bs, np.float32)
+    idx = np.arange(blocks * bs)
+    data_pos = idx[(idx % bs) != 0][:n]
+    w[idx % bs == 0] = 1.0
+    w[data_pos] = v
+    h1, p1, _ = oracle.encode_f32(w, bs)
+    h2, p2, _ = G.encode_f32(w, bs)
+    assert bytes(h1) == bytes(h2) and bytes(p1) == bytes(p2)
+    hv = G.unpack_nibbles(h1, w.size)[data_pos]
+    pv = G.unpack_nibbles(p1, w.size)[data_pos]
+    # direct scan in numpy (reference test's scan(), restated) on the same values
+    def scan(vals, tab):
+        best = np.zeros(vals.shape, np.uint8)
+        bd = np.abs(vals - tab[:, 0])
+        for k in range(1, 16):
+            d = np.abs(vals - tab[:, k])
+            t = d < bd
+            best[t] = k
+            bd = np.where(t, d, bd)
+        return best
+    h_ref = scan(v, np.broadcast_to(par, (v.size, 16)))
+    p_ref = scan(v, G.CELLS_F32[h_ref])
+    assert (hv == h_ref).all() and (pv == p_ref).all()
+
+
+def test_f32_encode_equals_f64_codec_on_reference_seeded_data(oracle):
+    """test_glint_tools.py:108-119: numpy f32 encode == pure-Python encode on
+    _gauss(64*41+7, 5) with a zero block at [128:192]."""
+    w = _gauss(64 * 41 + 7, 5)
+    w[128:192] = [0.0] * 64
+    wf = np.array(w, dtype=np.float32)
+    hole, plug, am = oracle.encode_f32(wf, 64)
+    hi, pi, ai = G.codec_encode_f64([G.f32(x) for x in w], 64)
+    assert bytes(hole) == G.pack_indices(hi)
+    assert bytes(plug) == G.pack_indices(pi)
+    assert am.tolist() == [G.f32(x) for x in ai]
+    h2, p2, a2 = G.encode_f32(wf, 64)
+    assert bytes(h2) == bytes(hole) and bytes(p2) == bytes(plug) and a2.tobytes() == am.tobytes()
+
+
+def test_toy_shards_encode_agree(oracle):
+    """The reference's toy shards (test_glint_tools.py:61-76): 16x64, odd 8x63
+    (blocks straddle rows), 4x128 with an all-zero block."""
+    a = _gauss(16 * 64, 1)
+    b = _gauss(8 * 63, 2)
+    c = _gauss(4 * 128, 3)
+    c[:64] = [0.0] * 64
+    for vals in (a, b, c):
+        u16 = G.f32_to_bf16_bits(np.array(vals, np.float32))
+        r1 = oracle.encode_bf16(u16, 64)
+        r2 = G.encode_bf16(u16, 64)
+        for x, y in zip(r1, r2):
+            assert x.tobytes() == y.tobytes()
+        hi, pi, _ = G.codec_encode_f64([float(x) for x in G.bf16_bits_to_f32(u16)], 64)
+        assert bytes(r1[0]) == G.pack_indices(hi) and bytes(r1[1]) == G.pack_indices(pi)
+
+
+def test_generic_blocksizes_agree(oracle):
+    rng = np.random.default_rng(7)
+    for bs in (1, 2, 23, 63, 64, 100, 256, 1000):
+        w = (rng.standard_normal(3001) * 0.02).astype(np.float32)
+        r1 = oracle.encode_f32(w, bs)
+        r2 = G.encode_f32(w, bs)
+        for x, y in zip(r1, r2):
+            assert x.tobytes() == y.tobytes(), bs
+
+
+# ------------------------------------------------------------------- expand / RNE
+def test_rne_known_answers(oracle):
+    """test_glint_tools.py:31-37: 1+ulp/2 -> 1, 1+1.5ulp -> 1+2ulp, 1+0.75ulp -> 1+ulp,
+    -(1+ulp/2) -> -1; NaN stays NaN."""
+    ulp = 2.0 ** -7
+    vals = np.float32([1 + ulp / 2, 1 + 1.5 * ulp, 1 + 0.75 * ulp, -(1 + ulp / 2), np.nan])
+    got = G.bf16_bits_to_f32(G.f32_to_bf16_bits(vals))
+    assert got[:4].tolist() == [1.0, 1 + 2 * ulp, 1 + ulp, -1.0]
+    assert math.isnan(got[4])
+    out = np.empty(5, np.uint16)
+    oracle.lib.oracle_f32_to_bf16(G._ptr(vals), 5, G._ptr(out))
+    assert out.tolist() == G.f32_to_bf16_bits(vals).tolist()
+    # overflow rounds to inf; inf stays inf
+    big = np.float32([np.finfo(np.float32).max, np.inf, -np.inf])
+    assert G.f32_to_bf16_bits(big).tolist() == [0x7F80, 0x7F80, 0xFF80]
+
+
+def test_expand_is_table_times_absmax(oracle):
+    rng = np.random.default_rng(3)
+    n, bs = 1001, 23
+    hole = rng.integers(0, 256, (n + 1) // 2, dtype=np.uint8)
+    plug = rng.integers(0, 256, (n + 1) // 2, dtype=np.uint8)
+    am = rng.uniform(0.5, 2.0, (n + bs - 1) // bs).astype(np.float32)
+    got = oracle.expand_f32(hole, plug, am, n, bs)
+    for i in (0, 1, 2, 22, 23, 500, 1000):
+        hb, pb = hole[i // 2], plug[i // 2]
+        h = (hb >> 4) if i & 1 else (hb & 15)
+        p = (pb >> 4) if i & 1 else (pb & 15)
+        assert got[i] == np.float32(G.CELLS_F32[h, p] * am[i // bs])
+    assert got.tobytes() == G.expand(hole, plug, am, n, bs).tobytes()
+    assert oracle.expand_bf16(hole, plug, am, n, bs).tobytes() == G.expand_bf16(hole, plug, am, n, bs).tobytes()
+
+
+# ------------------------------------------------------------------- H-TILE
+def test_htile_oracle_against_f64_brute_force(oracle):
+    rng = np.random.default_rng(11)
+    for (M, N, K, bs) in ((1, 1, 1, 1), (3, 5, 65, 23), (4, 17, 199, 64), (2, 8, 256, 64)):
+        hole = rng.integers(0, 256, (N * K + 1) // 2, dtype=np.uint8)
+        plug = rng.integers(0, 256, (N * K + 1) // 2, dtype=np.uint8)
+        am = rng.uniform(0.25, 1.0, (N * K + bs - 1) // bs).astype(np.float32)
+        x = G.f32_to_bf16_bits(rng.standard_normal(M * K).astype(np.float32))
+        y32 = oracle.htile_f32(hole, plug, am, x, M, N, K, bs)
+        y64, asum = oracle.htile_f64(hole, plug, am, x, M, N, K, bs)
+        ynp = G.htile_ref_f64(hole, plug, am, x, M, N, K, bs)
+        assert np.allclose(y64, ynp, rtol=1e-12, atol=1e-12)
+        bound = (K + 2) * 2.0 ** -23 * asum
+        assert np.all(np.abs(y32 - y64) <= bound)
+
+
+def test_htile_single_term_known_answer(oracle):
+    # K=1: y = CELLS[h][p] * absmax * x exactly; hole nibble 15, plug 15 -> 0.992...
+    hole = np.array([0x0F], np.uint8)
+    plug = np.array([0x0F], np.uint8)
+    am = np.float32([2.0])
+    x = G.f32_to_bf16_bits(np.float32([0.5]))
+    y = oracle.htile_f32(hole, plug, am, x, 1, 1, 1, 64)
+    assert y[0, 0] == np.float32(G.CELLS_F32[15, 15])
+
+
+# ------------------------------------------------------------------- INT8
+def test_quant_act_known_answers(oracle):
+    # a block with amax 127 -> s = 1 exactly; rint ties to even on 2.5 and 3.5
+    vals = np.zeros(64, np.float32)
+    vals[0], vals[1], vals[2], vals[3] = 127.0, 2.5, 3.5, -2.5
+    x = G.f32_to_bf16_bits(vals)
+    xq, sx = oracle.quant_act(x, 1, 64)
+    assert sx.tolist() == [1.0]
+    assert xq[:4].tolist() == [127, 2, 4, -2]
+    xq0, sx0 = oracle.quant_act(np.zeros(64, np.uint16), 1, 64)
+    assert sx0.tolist() == [1.0] and not xq0.any()
+
+
+def test_int8_integer_parts_are_exact(oracle):
+    rng = np.random.default_rng(5)
+    M, N, K = 7, 9, 192
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    C = oracle.int8_gemm_i32(A, B, M, N, K)
+    assert np.array_equal(C, A.astype(np.int64) @ B.astype(np.int64).T)
+    # emulation with unit scales is the exact integer sum converted per slice
+    sx = np.ones(M * (K // 64), np.float32)
+    sw = np.ones(N * (K // 64), np.float32)
+    y = oracle.int8_mma_emu(A.reshape(-1), sx, B.reshape(-1), sw, M, N, K)
+    assert np.array_equal(y.astype(np.int64), C.astype(np.int64))
+    sa = rng.uniform(1e-3, 2e-2, M).astype(np.float32)
+    sb = rng.uniform(1e-3, 2e-2, N).astype(np.float32)
+    out = oracle.int8_scale_bf16(C, sa, sb, M, N)
+    ref = G.f32_to_bf16_bits((C.astype(np.float32) * sa[:, None]) * sb[None, :])
+    assert np.array_equal(out, ref)
+
+
+# ------------------------------------------------------- the pins catch planted mistakes
+def test_planted_mistakes_are_caught():
+    """Mutations of the numpy oracle that a plausible bug would introduce must fail
+    the known answers above: hi-then-lo nibbles, '<=' instead of '<', parent-only."""
+    u16 = np.frombuffer(b"\x80\x3f\x00\x00", dtype="<u2")
+    w = G.bf16_bits_to_f32(u16)
+    h = G.nearest(w, G.PARENT_F32, 0)
+    p = G.nearest(w, G.CELLS_FLAT, h.astype(np.int64) * 16)
+    swapped = ((h[1] & 15) | (h[0] << 4), (p[1] & 15) | (p[0] << 4))
+    assert swapped != (0x7F, 0x8F)
+    # '<=' (last minimum) differs on the reference edge corpus's exact midpoints
+    par = G.PARENT_F32
+    mids = ((par[1:] + par[:-1]) / 2).astype(np.float32)
+    first = G.nearest(mids, par, 0)
+    last = np.array([max(range(16), key=lambda k: (-abs(float(np.float32(m - par[k]))), k)) for m in mids])
+    assert (first != last).any()
