@@ -1,0 +1,105 @@
+"""Build the GLINT HIP libraries in-tree for gfx950.
+
+    python -m glint_amd.build            # libraries + oracle
+    python -m glint_amd.build --only-libs
+
+Outputs (git-ignored, shipped with the tree):
+    glint_amd/lib/libglint_encode.so   encode / expand / H-TILE (include/glint_encode.h, glint_htile.h)
+    glint_amd/lib/libp7_kernels.so     attach ABI: INT8 GEMM (include/int8_mma_gemm.h, p7_attach.h)
+    oracle/liboracle.so                CPU oracle (tests only)
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "lib"
+BUILD = ROOT / "_build"
+ARCH = os.environ.get("GLINT_OFFLOAD_ARCH", "gfx950")
+
+HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
+    "-ffp-contract=off",  # every fused multiply-add in the kernels is an explicit fmaf
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-command-line-argument",
+    f"-I{ROOT / 'include'}", f"-I{CSRC}",
+]
+
+LIBS = {
+    "libglint_encode.so": ["glint_encode.hip", "glint_htile.hip"],
+    "libp7_kernels.so": ["int8_mma_gemm.hip", "p7_abi.cpp"],
+}
+
+
+def _run(cmd, **kw):
+    r = subprocess.run(cmd, capture_output=True, text=True, **kw)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(map(str, cmd))}\n{r.stdout}\n{r.stderr}")
+    return r
+
+
+def gen_code_table() -> None:
+    """Regenerate glint_code_table.inc from the codebook (deterministic)."""
+    BUILD.mkdir(exist_ok=True)
+    exe = BUILD / "gen_code_table"
+    _run(["gcc", "-O2", "-ffp-contract=off", "-fopenmp", f"-I{ROOT / 'include'}", f"-I{CSRC}",
+          str(CSRC / "gen_code_table.c"), "-lm", "-o", str(exe)])
+    tmp = BUILD / "glint_code_table.inc"
+    _run([str(exe), str(tmp)])
+    dst = CSRC / "glint_code_table.inc"
+    if not dst.is_file() or dst.read_bytes() != tmp.read_bytes():
+        shutil.copyfile(tmp, dst)
+
+
+def _compile(src: str) -> Path:
+    obj = BUILD / (src + ".o")
+    lang = ["-x", "hip"] if src.endswith(".hip") else []
+    _run([HIPCC, *HIP_FLAGS, *lang, "-c", str(CSRC / src), "-o", str(obj)])
+    return obj
+
+
+def build_libs() -> None:
+    BUILD.mkdir(exist_ok=True)
+    LIB.mkdir(exist_ok=True)
+    srcs = [s for files in LIBS.values() for s in files if (CSRC / s).is_file()]
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = dict(zip(srcs, ex.map(_compile, srcs)))
+    for lib, files in LIBS.items():
+        present = [objs[f] for f in files if f in objs]
+        if not present:
+            continue
+        out = LIB / lib
+        tmp = LIB / (lib + ".tmp")
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, present)])
+        os.replace(tmp, out)
+
+
+def build_oracle() -> None:
+    _run(["make", "-C", str(ROOT / "oracle"), "-j4"])
+    if Path("/root/reference").is_dir():
+        _run(["make", "-C", str(ROOT / "oracle"), "ref"])
+
+
+def build(only_libs: bool = False) -> None:
+    gen_code_table()
+    build_libs()
+    if not only_libs:
+        build_oracle()
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only-libs", action="store_true")
+    args = ap.parse_args()
+    build(args.only_libs)
+    print("built:", ", ".join(sorted(p.name for p in LIB.glob("*.so"))))
+    sys.exit(0)

@@ -1,0 +1,433 @@
+/* GLINT encode (BF16/F32 -> hole/plug nibble planes + f32 absmax) and expand
+ * (planes -> f32 / BF16) for gfx950.
+ *
+ * Semantics: reference cuda/glint_encode.cu:41-114 and glint_np.py:25-92 (absmax skips
+ * NaN; v = (s == 0) ? 0 : w / s in f32; first-minimum nearest parent, then nearest
+ * child of that parent; element 2e in the low nibble; BF16 = RNE with the NaN rule).
+ *
+ * Fast encode (bs = 64, BF16, aligned): one pass, one 16-byte load per lane per
+ * 512-element wave chunk. Lane l of the chunk owns elements [8l, 8l+8), so a 64-block is
+ * 8 lanes: absmax is a packed-i16 max over BF16 magnitudes plus a 3-step DPP max. The
+ * divide is a per-block correctly rounded reciprocal and Markstein's one-fma correction
+ * (exact for every bf16 pair with 2^-90 <= absmax < 2^90; tests/native/check_markstein.c),
+ * other blocks take the IEEE divide. The nearest-code search is one LDS bucket lookup and
+ * one compare (glint_codebook.h, verified against the scan for every float in [-1, 1]).
+ * Everything else (any bs, F32 input, tails, unaligned pointers) runs the generic pair.
+ */
+#include "glint_common.h"
+#include "glint_codebook.h"
+#include "glint_cells.h"
+#include "glint_encode.h"
+
+#include <stdio.h>
+
+__constant__ GlintCodeEntry kCodeTable[GLINT_CODE_BUCKETS] = {
+#include "glint_code_table.inc"
+};
+
+/* code(v) = base + (v > thr) from an entry table in LDS or constant memory.
+ * v is an f32 divide or fma result, so at worst a quiet NaN; v_med3_f32 returns
+ * min3(v, -1, 1) = -1 for a NaN input, which selects bucket 0 like the host's
+ * fminf(fmaxf(v, -1), 1) in glint_codebook.h. */
+template <typename Tab>
+__device__ __forceinline__ uint32_t glint_code_of(float v, const Tab *tab) {
+    const float c = __builtin_amdgcn_fmed3f(v, -1.0f, 1.0f);
+    const uint32_t b = min(__float_as_uint(fmaf(c, 256.0f, GLINT_CODE_MAGIC)) - GLINT_CODE_MAGIC_BITS,
+                           (uint32_t)(GLINT_CODE_BUCKETS - 1)); /* never out of the table */
+    const GlintCodeEntry e = tab[b];
+    return e.base + (v > __uint_as_float(e.thr) ? 1u : 0u);
+}
+
+/* ------------------------------------------------------------------ fast encode */
+typedef unsigned short glint_u16x2 __attribute__((ext_vector_type(2)));
+typedef short glint_i16x2 __attribute__((ext_vector_type(2)));
+
+/* Max BF16 magnitude of the two halves of d, NaN skipped, as (mag + 0x7F) in i16 lanes:
+ * a NaN magnitude (0x7F81..0x7FFF) becomes negative and never wins; inf (0x7F80)
+ * becomes 0x7FFF. */
+__device__ __forceinline__ glint_i16x2 glint_mag_key(uint32_t d) {
+    const glint_u16x2 m = __builtin_bit_cast(glint_u16x2, d & 0x7FFF7FFFu) + (glint_u16x2)(0x7F);
+    return __builtin_bit_cast(glint_i16x2, m);
+}
+
+__device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const GlintCodeEntry *tab, int64_t chunk, int lane,
+                                                   uint32_t *__restrict__ hole, uint32_t *__restrict__ plug,
+                                                   float *__restrict__ absmax) {
+    /* absmax of this lane's 8 values, then of the 8 lanes that share the block */
+    glint_i16x2 k = __builtin_elementwise_max(glint_mag_key(d.x), glint_mag_key(d.y));
+    k = __builtin_elementwise_max(k, __builtin_elementwise_max(glint_mag_key(d.z), glint_mag_key(d.w)));
+    int m16 = max((int)k.x, (int)k.y) - 0x7F;
+    m16 = glint_max8(m16);
+    const uint32_t sbits = (uint32_t)m16 << 16;
+    const float s = __uint_as_float(sbits);
+
+    const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
+    float w[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        w[2 * j] = glint_bf16lo(dw[j]);
+        w[2 * j + 1] = glint_bf16hi(dw[j]);
+    }
+    float v[8];
+    if (sbits - 0x12800000u < 0x6C800000u - 0x12800000u) { /* 2^-90 <= s < 2^90 */
+        const float y = 1.0f / s;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float q = w[j] * y;
+            const float r = fmaf(-q, s, w[j]);
+            v[j] = fmaf(r, y, q);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            v[j] = (s == 0.0f) ? 0.0f : w[j] / s;
+    }
+    uint32_t c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        c[j] = glint_code_of(v[j], tab);
+    /* bytes c0..c3 / c4..c7 -> nibble planes: plug = low nibbles, hole = high nibbles */
+    const uint32_t a = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+    const uint32_t b = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+    uint32_t pa = a & 0x0F0F0F0Fu, pb = b & 0x0F0F0F0Fu;
+    uint32_t ha = (a >> 4) & 0x0F0F0F0Fu, hb = (b >> 4) & 0x0F0F0F0Fu;
+    pa |= pa >> 4;
+    pb |= pb >> 4;
+    ha |= ha >> 4;
+    hb |= hb >> 4;
+    hole[chunk * 64 + lane] = __builtin_amdgcn_perm(hb, ha, 0x06040200u);
+    plug[chunk * 64 + lane] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
+    if ((lane & 7) == 0)
+        absmax[chunk * 8 + (lane >> 3)] = s;
+}
+
+template <int UNROLL>
+__global__ __launch_bounds__(256) void k_encode_bf16_b64(const glint_u32x4 *__restrict__ w, uint32_t *__restrict__ hole,
+                                                         uint32_t *__restrict__ plug, float *__restrict__ absmax,
+                                                         int64_t nchunks) {
+    __shared__ GlintCodeEntry tab[GLINT_CODE_BUCKETS];
+    for (int i = threadIdx.x; i < GLINT_CODE_BUCKETS; i += blockDim.x)
+        tab[i] = kCodeTable[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+    int64_t c0 = wave * UNROLL;
+    for (; c0 + UNROLL <= nchunks; c0 += nwaves * UNROLL) {
+        glint_u32x4 d[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+            d[u] = __builtin_nontemporal_load(&w[(c0 + u) * 64 + lane]);
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+            glint_encode_chunk(d[u], tab, c0 + u, lane, hole, plug, absmax);
+    }
+    for (int64_t c = c0; c < nchunks && c < c0 + UNROLL; ++c)
+        glint_encode_chunk(w[c * 64 + lane], tab, c, lane, hole, plug, absmax);
+}
+
+/* ---------------------------------------------------------------- generic encode */
+__device__ __forceinline__ float glint_load_w(const uint16_t *w, int64_t i) { return __uint_as_float((uint32_t)w[i] << 16); }
+__device__ __forceinline__ float glint_load_w(const float *w, int64_t i) { return w[i]; }
+
+/* absmax of blocks [b0, b1): one wave per block, NaN skipped (fabsf(NaN) > m is false). */
+template <typename T>
+__global__ __launch_bounds__(256) void k_absmax_generic(const T *__restrict__ w, int64_t n, int bs, int64_t b0,
+                                                        int64_t b1, float *__restrict__ absmax) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+    for (int64_t b = b0 + (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); b < b1; b += nwaves) {
+        const int64_t i0 = b * bs;
+        const int64_t i1 = min(i0 + bs, n);
+        float m = 0.0f;
+        for (int64_t i = i0 + lane; i < i1; i += 64) {
+            const float a = fabsf(glint_load_w(w, i));
+            if (a > m)
+                m = a;
+        }
+        m = glint_wave_max(m); /* no NaN left among the partial maxima */
+        if (lane == 0)
+            absmax[b] = m;
+    }
+}
+
+/* packed bytes [e0, e1): v = (s == 0) ? 0 : w / s (IEEE divide), code lookup, pack. */
+template <typename T>
+__global__ __launch_bounds__(256) void k_encode_generic(const T *__restrict__ w, const float *__restrict__ absmax,
+                                                        int64_t n, int bs, int64_t e0, int64_t e1,
+                                                        uint8_t *__restrict__ hole, uint8_t *__restrict__ plug) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = e0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < e1; e += stride) {
+        uint32_t c[2] = {0u, 0u};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int64_t i = 2 * e + t;
+            if (i < n) {
+                const float s = absmax[i / bs];
+                const float v = (s == 0.0f) ? 0.0f : glint_load_w(w, i) / s;
+                c[t] = glint_code_of(v, kCodeTable);
+            }
+        }
+        hole[e] = (uint8_t)((c[0] >> 4) | (c[1] & 0xF0u));
+        plug[e] = (uint8_t)((c[0] & 15u) | ((c[1] & 15u) << 4));
+    }
+}
+
+static int glint_num_cus() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 256;
+    if (!cached[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
+static unsigned glint_grid(int64_t work_items, int per_block, int max_blocks) {
+    int64_t g = (work_items + per_block - 1) / per_block;
+    if (g > max_blocks)
+        g = max_blocks;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+template <typename T>
+static int encode_device(const T *d_w, int64_t n, int bs, uint8_t *d_hole, uint8_t *d_plug, float *d_am,
+                         hipStream_t st) {
+    if (n < 0 || bs <= 0)
+        return -1;
+    if (n == 0)
+        return 0;
+    if (!d_w || !d_hole || !d_plug || !d_am)
+        return -1;
+    const int cus = glint_num_cus();
+    int64_t n_fast = 0;
+    if (sizeof(T) == 2 && bs == 64 && glint_aligned(d_w, 16) && glint_aligned(d_hole, 4) && glint_aligned(d_plug, 4) &&
+        glint_aligned(d_am, 4))
+        n_fast = (n / 512) * 512;
+    if (n_fast) {
+        constexpr int U = 4;
+        const int64_t nchunks = n_fast / 512;
+        const unsigned grid = glint_grid(nchunks, 4 * U, cus * 8);
+        k_encode_bf16_b64<U><<<grid, 256, 0, st>>>((const glint_u32x4 *)d_w, (uint32_t *)d_hole, (uint32_t *)d_plug, d_am,
+                                                   nchunks);
+    }
+    if (n_fast < n) {
+        const int64_t b0 = n_fast / bs, b1 = (n + bs - 1) / bs;
+        k_absmax_generic<T><<<glint_grid(b1 - b0, 4, cus * 16), 256, 0, st>>>(d_w, n, bs, b0, b1, d_am);
+        const int64_t e0 = n_fast / 2, e1 = (n + 1) / 2;
+        k_encode_generic<T><<<glint_grid(e1 - e0, 256, cus * 16), 256, 0, st>>>(d_w, d_am, n, bs, e0, e1, d_hole,
+                                                                                 d_plug);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* ------------------------------------------------------------------ expand */
+/* Per lane: 32 consecutive elements (16 B of each plane), all inside one absmax block
+ * (bs % 32 == 0), looked up in the bank-private LDS cell table. */
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_expand_fast(const glint_u32x4 *__restrict__ hole, const glint_u32x4 *__restrict__ plug,
+                                                     const float *__restrict__ absmax, void *__restrict__ out,
+                                                     int64_t ngroups, int bs) {
+    __shared__ float ltab[GLINT_LDS_CELLS_WORDS];
+    __shared__ float stage[256];
+    glint_fill_cells_lds(ltab, stage);
+    const uint32_t lb = threadIdx.x & 31;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
+        const glint_u32x4 hv = __builtin_nontemporal_load(&hole[g]);
+        const glint_u32x4 pv = __builtin_nontemporal_load(&plug[g]);
+        const float a = absmax[(g * 32) / bs];
+        const uint32_t H[4] = {hv.x, hv.y, hv.z, hv.w}, P[4] = {pv.x, pv.y, pv.z, pv.w};
+        float r[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t E = ((H[q] << 4) & 0xF0F0F0F0u) | (P[q] & 0x0F0F0F0Fu);
+            const uint32_t O = (H[q] & 0xF0F0F0F0u) | ((P[q] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                r[8 * q + 2 * j] = ltab[(((E >> (8 * j)) & 0xFFu) << 5) | lb] * a;
+                r[8 * q + 2 * j + 1] = ltab[(((O >> (8 * j)) & 0xFFu) << 5) | lb] * a;
+            }
+        }
+        if (BF16) {
+            glint_u32x4 *o = (glint_u32x4 *)out + g * 4;
+            if (a == a) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    __builtin_nontemporal_store(
+                        glint_u32x4{glint_pack_bf16x2(r[8 * q], r[8 * q + 1]), glint_pack_bf16x2(r[8 * q + 2], r[8 * q + 3]),
+                                    glint_pack_bf16x2(r[8 * q + 4], r[8 * q + 5]), glint_pack_bf16x2(r[8 * q + 6], r[8 * q + 7])},
+                        &o[q]);
+            } else { /* NaN absmax: the reference NaN rule for every element */
+                uint16_t *o16 = (uint16_t *)out + g * 32;
+                for (int j = 0; j < 32; ++j)
+                    o16[j] = glint_f32_to_bf16(r[j]);
+            }
+        } else {
+            glint_f32x4 *o = (glint_f32x4 *)out + g * 8;
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                __builtin_nontemporal_store(glint_f32x4{r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]}, &o[q]);
+        }
+    }
+}
+
+/* One element per thread over [i0, n): any bs, any alignment. */
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_expand_generic(const uint8_t *__restrict__ hole, const uint8_t *__restrict__ plug,
+                                                        const float *__restrict__ absmax, void *__restrict__ out,
+                                                        int64_t i0, int64_t n, int bs) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = i0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int sh = (int)(i & 1) * 4;
+        const float r = kCells[(hole[i >> 1] >> sh) & 15][(plug[i >> 1] >> sh) & 15] * absmax[i / bs];
+        if (BF16)
+            ((uint16_t *)out)[i] = glint_f32_to_bf16(r);
+        else
+            ((float *)out)[i] = r;
+    }
+}
+
+template <bool BF16>
+static int expand_device(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_am, int64_t n, int bs, void *d_out,
+                         hipStream_t st) {
+    if (!d_hole || !d_plug || !d_am || !d_out || bs <= 0)
+        return -1;
+    if (n <= 0)
+        return 0;
+    const int cus = glint_num_cus();
+    int64_t n_fast = 0;
+    if (bs % 32 == 0 && glint_aligned(d_hole, 16) && glint_aligned(d_plug, 16) && glint_aligned(d_am, 4) &&
+        glint_aligned(d_out, 16))
+        n_fast = (n / 32) * 32;
+    if (n_fast) {
+        const int64_t ngroups = n_fast / 32;
+        k_expand_fast<BF16><<<glint_grid(ngroups, 256, cus * 4), 256, 0, st>>>((const glint_u32x4 *)d_hole,
+                                                                               (const glint_u32x4 *)d_plug, d_am, d_out,
+                                                                               ngroups, bs);
+    }
+    if (n_fast < n)
+        k_expand_generic<BF16><<<glint_grid(n - n_fast, 256, cus * 16), 256, 0, st>>>(d_hole, d_plug, d_am, d_out,
+                                                                                      n_fast, n, bs);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+/* ------------------------------------------------------------------ C ABI */
+GLINT_API int glint_encode_n_absmax(int64_t n, int blocksize) {
+    if (blocksize <= 0)
+        return 0;
+    return (int)((n + blocksize - 1) / blocksize);
+}
+
+GLINT_API int glint_encode_n_packed(int64_t n) { return (int)((n + 1) / 2); }
+
+GLINT_API int glint_encode_bf16_device(const uint16_t *d_w, int64_t n, int bs, uint8_t *d_hole, uint8_t *d_plug,
+                                       float *d_absmax, struct ihipStream_t *stream) {
+    return encode_device<uint16_t>(d_w, n, bs, d_hole, d_plug, d_absmax, (hipStream_t)stream);
+}
+
+GLINT_API int glint_encode_f32_device(const float *d_w, int64_t n, int bs, uint8_t *d_hole, uint8_t *d_plug,
+                                      float *d_absmax, struct ihipStream_t *stream) {
+    return encode_device<float>(d_w, n, bs, d_hole, d_plug, d_absmax, (hipStream_t)stream);
+}
+
+/* Host-pointer encode: allocate, copy in, encode, copy out, free (synchronous). */
+template <typename T>
+static int encode_host(const T *w, int64_t n, int bs, uint8_t *hole, uint8_t *plug, float *absmax) {
+    if (n < 0 || bs <= 0)
+        return -1;
+    if (n == 0)
+        return 0;
+    if (!w || !hole || !plug || !absmax)
+        return -1;
+    const size_t npack = (size_t)((n + 1) / 2), nam = (size_t)((n + bs - 1) / bs);
+    T *d_w = nullptr;
+    uint8_t *d_h = nullptr, *d_p = nullptr;
+    float *d_a = nullptr;
+    int rc = -1;
+    if (hipMalloc((void **)&d_w, (size_t)n * sizeof(T)) != hipSuccess || hipMalloc((void **)&d_h, npack) != hipSuccess ||
+        hipMalloc((void **)&d_p, npack) != hipSuccess || hipMalloc((void **)&d_a, nam * sizeof(float)) != hipSuccess)
+        goto done;
+    if (hipMemcpy(d_w, w, (size_t)n * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+        goto done;
+    rc = -3;
+    if (encode_device<T>(d_w, n, bs, d_h, d_p, d_a, 0) != 0 || hipDeviceSynchronize() != hipSuccess)
+        goto done;
+    if (hipMemcpy(hole, d_h, npack, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(plug, d_p, npack, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(absmax, d_a, nam * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess)
+        goto done;
+    rc = 0;
+done:
+    (void)hipFree(d_w);
+    (void)hipFree(d_h);
+    (void)hipFree(d_p);
+    (void)hipFree(d_a);
+    return rc;
+}
+
+GLINT_API int glint_encode_bf16_host(const uint16_t *w, int64_t n, int bs, uint8_t *hole, uint8_t *plug, float *absmax) {
+    return encode_host<uint16_t>(w, n, bs, hole, plug, absmax);
+}
+
+GLINT_API int glint_encode_f32_host(const float *w, int64_t n, int bs, uint8_t *hole, uint8_t *plug, float *absmax) {
+    return encode_host<float>(w, n, bs, hole, plug, absmax);
+}
+
+template <bool BF16>
+static int expand_host(const uint8_t *hole, const uint8_t *plug, const float *absmax, int64_t n, int bs, void *out) {
+    if (bs <= 0 || n < 0)
+        return -1;
+    if (n == 0)
+        return 0;
+    if (!hole || !plug || !absmax || !out)
+        return -1;
+    const size_t npack = (size_t)((n + 1) / 2), nam = (size_t)((n + bs - 1) / bs);
+    const size_t out_bytes = (size_t)n * (BF16 ? 2 : 4);
+    uint8_t *d_h = nullptr, *d_p = nullptr;
+    float *d_a = nullptr;
+    void *d_o = nullptr;
+    int rc = -3;
+    if (hipMalloc((void **)&d_h, npack) != hipSuccess || hipMalloc((void **)&d_p, npack) != hipSuccess ||
+        hipMalloc((void **)&d_a, nam * sizeof(float)) != hipSuccess || hipMalloc(&d_o, out_bytes) != hipSuccess)
+        goto done;
+    if (hipMemcpy(d_h, hole, npack, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d_p, plug, npack, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d_a, absmax, nam * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+        goto done;
+    if (expand_device<BF16>(d_h, d_p, d_a, n, bs, d_o, 0) != 0 || hipDeviceSynchronize() != hipSuccess)
+        goto done;
+    if (hipMemcpy(out, d_o, out_bytes, hipMemcpyDeviceToHost) != hipSuccess)
+        goto done;
+    rc = 0;
+done:
+    (void)hipFree(d_h);
+    (void)hipFree(d_p);
+    (void)hipFree(d_a);
+    (void)hipFree(d_o);
+    return rc;
+}
+
+GLINT_API int glint_expand_packed_to_f32_host(const uint8_t *hole, const uint8_t *plug, const float *absmax, int64_t n,
+                                              int bs, float *out) {
+    return expand_host<false>(hole, plug, absmax, n, bs, out);
+}
+
+GLINT_API int glint_expand_packed_to_bf16_host(const uint8_t *hole, const uint8_t *plug, const float *absmax, int64_t n,
+                                               int bs, uint16_t *out) {
+    return expand_host<true>(hole, plug, absmax, n, bs, out);
+}
+
+GLINT_API int glint_expand_packed_to_f32_device(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax,
+                                                int64_t n, int bs, float *d_out, struct ihipStream_t *stream) {
+    return expand_device<false>(d_hole, d_plug, d_absmax, n, bs, d_out, (hipStream_t)stream);
+}
+
+GLINT_API int glint_expand_packed_to_bf16_device(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax,
+                                                 int64_t n, int bs, uint16_t *d_out, struct ihipStream_t *stream) {
+    return expand_device<true>(d_hole, d_plug, d_absmax, n, bs, d_out, (hipStream_t)stream);
+}

@@ -1,0 +1,280 @@
+"""ctypes bindings to the GLINT C ABI (libglint_encode.so, libp7_kernels.so).
+
+Two layers:
+
+* ``EncodeLib`` / ``P7Lib``: the raw C entry points with their argtypes, as a caller of
+  the reference's ``glint_cuda.py`` would bind them (the host-pointer ABI takes bytes);
+* tensor helpers (``encode_bf16`` ... ``int8_gemm_i32``) that pass torch device tensors
+  and torch's current stream straight to the device entry points. torch is only the
+  allocator and stream here; every result is computed by the HIP kernels.
+
+A missing library raises RuntimeError: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional, Tuple
+
+PKG = Path(__file__).resolve().parent
+LIB_DIR = PKG / "lib"
+
+_c = ctypes
+VP, I64, I32 = _c.c_void_p, _c.c_int64, _c.c_int
+
+
+def encode_lib_path() -> Optional[Path]:
+    """$GLINT_ENCODE_SO, else glint_amd/lib/libglint_encode.so (reference glint_cuda.py:9-18)."""
+    env = os.environ.get("GLINT_ENCODE_SO")
+    if env:
+        p = Path(env)
+        return p if p.is_file() else None
+    p = LIB_DIR / "libglint_encode.so"
+    return p if p.is_file() else None
+
+
+def p7_lib_path() -> Optional[Path]:
+    env = os.environ.get("GLINT_P7_SO")
+    if env:
+        p = Path(env)
+        return p if p.is_file() else None
+    p = LIB_DIR / "libp7_kernels.so"
+    return p if p.is_file() else None
+
+
+_ENCODE_SIGS = {
+    "glint_encode_n_absmax": ([I64, I32], I32),
+    "glint_encode_n_packed": ([I64], I32),
+    "glint_encode_bf16_host": ([VP, I64, I32, VP, VP, VP], I32),
+    "glint_encode_f32_host": ([VP, I64, I32, VP, VP, VP], I32),
+    "glint_expand_packed_to_f32_host": ([VP, VP, VP, I64, I32, VP], I32),
+    "glint_expand_packed_to_bf16_host": ([VP, VP, VP, I64, I32, VP], I32),
+    "glint_expand_packed_to_f32_device": ([VP, VP, VP, I64, I32, VP, VP], I32),
+    "glint_expand_packed_to_bf16_device": ([VP, VP, VP, I64, I32, VP, VP], I32),
+    "glint_encode_bf16_device": ([VP, I64, I32, VP, VP, VP, VP], I32),
+    "glint_encode_f32_device": ([VP, I64, I32, VP, VP, VP, VP], I32),
+    "launch_glint_htile_s3_f32_stream": ([VP, VP, VP, VP, VP, I32, I32, I32, I32, VP], I32),
+    "launch_glint_htile_s3_f32": ([VP, VP, VP, VP, VP, I32, I32, I32, I32], I32),
+    "launch_glint_htile_bf16_stream": ([VP, VP, VP, VP, VP, I32, I32, I32, I32, VP], I32),
+}
+
+
+class Int8MmaLinear(_c.Structure):
+    """include/int8_mma_gemm.h Int8MmaLinear, passed by value."""
+    _fields_ = [("q", VP), ("scale", VP), ("n_out", I32), ("k_in", I32)]
+
+
+_P7_SIGS = {
+    "p7_abi_version": ([], _c.c_char_p),
+    "int8_mma_gemm": ([VP, Int8MmaLinear, VP, I32, VP, VP, VP], I32),
+    "p7_int8_gemm_flat": ([VP, VP, VP, I32, I32, VP, I32, VP, VP, VP], I32),
+    "glint_int8_gemm_i32": ([VP, VP, VP, I32, I32, I32, VP], I32),
+    "glint_int8_gemm_scaled_bf16": ([VP, VP, VP, VP, VP, I32, I32, I32, VP], I32),
+}
+
+ENCODE_SYMBOLS = tuple(_ENCODE_SIGS)
+P7_SYMBOLS = tuple(_P7_SIGS)
+
+
+def _bind(path: Path, sigs: dict) -> ctypes.CDLL:
+    lib = ctypes.CDLL(str(path))
+    for name, (args, res) in sigs.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = res
+    return lib
+
+
+_ENC: Optional[ctypes.CDLL] = None
+_P7: Optional[ctypes.CDLL] = None
+
+
+def encode_lib() -> ctypes.CDLL:
+    global _ENC
+    if _ENC is None:
+        p = encode_lib_path()
+        if p is None:
+            raise RuntimeError("libglint_encode.so not built: run `python -m glint_amd.build`")
+        _ENC = _bind(p, _ENCODE_SIGS)
+    return _ENC
+
+
+def p7_lib() -> ctypes.CDLL:
+    global _P7
+    if _P7 is None:
+        p = p7_lib_path()
+        if p is None:
+            raise RuntimeError("libp7_kernels.so not built: run `python -m glint_amd.build`")
+        _P7 = _bind(p, _P7_SIGS)
+    return _P7
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} rc={rc}")
+
+
+# ------------------------------------------------------------ tensor helpers (device)
+def _torch():
+    import torch
+    return torch
+
+
+def _stream(stream=None) -> ctypes.c_void_p:
+    torch = _torch()
+    s = torch.cuda.current_stream() if stream is None else stream
+    return VP(s.cuda_stream)
+
+
+def _p(t) -> ctypes.c_void_p:
+    return VP(t.data_ptr())
+
+
+def _as_u16(t):
+    torch = _torch()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16)
+    if t.dtype in (torch.int16, torch.uint16):
+        return t
+    raise TypeError(f"expected bf16 bits, got {t.dtype}")
+
+
+def encode_bf16(w, blocksize: int = 64, out=None, stream=None):
+    """GPU encode of a BF16 device tensor -> (hole u8, plug u8, absmax f32) device tensors."""
+    torch = _torch()
+    w = _as_u16(w).contiguous()
+    n = w.numel()
+    if out is None:
+        npk, nam = (n + 1) // 2, (n + blocksize - 1) // blocksize
+        out = (torch.empty(npk, dtype=torch.uint8, device=w.device), torch.empty(npk, dtype=torch.uint8, device=w.device),
+               torch.empty(nam, dtype=torch.float32, device=w.device))
+    hole, plug, am = out
+    _check(encode_lib().glint_encode_bf16_device(_p(w), n, blocksize, _p(hole), _p(plug), _p(am), _stream(stream)),
+           "glint_encode_bf16_device")
+    return hole, plug, am
+
+
+def encode_f32(w, blocksize: int = 64, stream=None):
+    torch = _torch()
+    w = w.contiguous()
+    assert w.dtype == torch.float32
+    n = w.numel()
+    npk, nam = (n + 1) // 2, (n + blocksize - 1) // blocksize
+    hole = torch.empty(npk, dtype=torch.uint8, device=w.device)
+    plug = torch.empty(npk, dtype=torch.uint8, device=w.device)
+    am = torch.empty(nam, dtype=torch.float32, device=w.device)
+    _check(encode_lib().glint_encode_f32_device(_p(w), n, blocksize, _p(hole), _p(plug), _p(am), _stream(stream)),
+           "glint_encode_f32_device")
+    return hole, plug, am
+
+
+def expand_f32(hole, plug, absmax, n: int, blocksize: int = 64, out=None, stream=None):
+    torch = _torch()
+    out = torch.empty(n, dtype=torch.float32, device=hole.device) if out is None else out
+    _check(encode_lib().glint_expand_packed_to_f32_device(_p(hole), _p(plug), _p(absmax), n, blocksize, _p(out),
+                                                          _stream(stream)), "glint_expand_packed_to_f32_device")
+    return out
+
+
+def expand_bf16(hole, plug, absmax, n: int, blocksize: int = 64, out=None, stream=None):
+    torch = _torch()
+    out = torch.empty(n, dtype=torch.bfloat16, device=hole.device) if out is None else out
+    _check(encode_lib().glint_expand_packed_to_bf16_device(_p(hole), _p(plug), _p(absmax), n, blocksize, _p(out),
+                                                           _stream(stream)), "glint_expand_packed_to_bf16_device")
+    return out
+
+
+def htile_f32(hole, plug, absmax, x, N: int, K: int, blocksize: int = 64, out=None, stream=None):
+    """y[M, N] f32 = x[M, K] (bf16) @ W^T via launch_glint_htile_s3_f32_stream."""
+    torch = _torch()
+    x = _as_u16(x)
+    M = x.numel() // K
+    y = torch.empty((M, N), dtype=torch.float32, device=x.device) if out is None else out
+    _check(encode_lib().launch_glint_htile_s3_f32_stream(_p(hole), _p(plug), _p(absmax), _p(x), _p(y), M, N, K,
+                                                         blocksize, _stream(stream)), "launch_glint_htile_s3_f32_stream")
+    return y
+
+
+def htile_bf16(hole, plug, absmax, x, N: int, K: int, blocksize: int = 64, out=None, stream=None):
+    """y[M, N] bf16 (f32 accumulation) via launch_glint_htile_bf16_stream."""
+    torch = _torch()
+    x = _as_u16(x)
+    M = x.numel() // K
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if out is None else out
+    _check(encode_lib().launch_glint_htile_bf16_stream(_p(hole), _p(plug), _p(absmax), _p(x), _p(y), M, N, K,
+                                                       blocksize, _stream(stream)), "launch_glint_htile_bf16_stream")
+    return y
+
+
+def int8_mma_gemm(x, q, scale, n_out: int, k_in: int, xq=None, sx=None, stream=None):
+    """The attach ABI's W8A8 GEMM: x bf16 [m, k_in] -> y f32 [m, n_out] (also returns xq, sx)."""
+    torch = _torch()
+    x = _as_u16(x)
+    m = x.numel() // k_in
+    y = torch.empty((m, n_out), dtype=torch.float32, device=x.device)
+    xq = torch.empty(m * k_in, dtype=torch.int8, device=x.device) if xq is None else xq
+    sx = torch.empty(m * (k_in // 64), dtype=torch.float32, device=x.device) if sx is None else sx
+    lin = Int8MmaLinear(q.data_ptr(), scale.data_ptr(), n_out, k_in)
+    _check(p7_lib().int8_mma_gemm(_p(x), lin, _p(y), m, _p(xq), _p(sx), _stream(stream)), "int8_mma_gemm")
+    return y, xq, sx
+
+
+def int8_gemm_i32(A, B, stream=None):
+    torch = _torch()
+    M, K = A.shape
+    N = B.shape[0]
+    C = torch.empty((M, N), dtype=torch.int32, device=A.device)
+    _check(p7_lib().glint_int8_gemm_i32(_p(A), _p(B), _p(C), M, N, K, _stream(stream)), "glint_int8_gemm_i32")
+    return C
+
+
+def int8_gemm_scaled_bf16(A, B, sa, sb, out=None, stream=None):
+    torch = _torch()
+    M, K = A.shape
+    N = B.shape[0]
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=A.device) if out is None else out
+    _check(p7_lib().glint_int8_gemm_scaled_bf16(_p(A), _p(B), _p(sa), _p(sb), _p(out), M, N, K, _stream(stream)),
+           "glint_int8_gemm_scaled_bf16")
+    return out
+
+
+# ------------------------------------------------------------- host-pointer wrappers
+def encode_bf16_host(raw_bf16: bytes, n: int, blocksize: int = 64) -> Tuple[bytes, bytes, bytes]:
+    """Same contract as the reference's glint_cuda.encode_bf16_cuda (glint_cuda.py:52-65)."""
+    lib = encode_lib()
+    n_am = lib.glint_encode_n_absmax(n, blocksize)
+    n_pk = lib.glint_encode_n_packed(n)
+    hole = (_c.c_uint8 * n_pk)()
+    plug = (_c.c_uint8 * n_pk)()
+    am = (_c.c_float * n_am)()
+    buf = (_c.c_uint16 * n).from_buffer_copy(raw_bf16[: n * 2])
+    rc = lib.glint_encode_bf16_host(_c.byref(buf), n, blocksize, hole, plug, am)
+    if rc != 0:
+        raise RuntimeError(f"glint_encode_bf16_host rc={rc}")
+    return bytes(hole), bytes(plug), bytes(_c.string_at(_c.addressof(am), n_am * 4))
+
+
+def expand_host(hole: bytes, plug: bytes, absmax_f32: bytes, n: int, blocksize: int = 64) -> bytes:
+    """Same contract as the reference's glint_cuda.expand_cuda (glint_cuda.py:66-78)."""
+    lib = encode_lib()
+    out = (_c.c_float * n)()
+    h = _c.create_string_buffer(bytes(hole), len(hole))
+    p = _c.create_string_buffer(bytes(plug), len(plug))
+    a = _c.create_string_buffer(bytes(absmax_f32), len(absmax_f32))
+    rc = lib.glint_expand_packed_to_f32_host(h, p, a, n, blocksize, out)
+    if rc != 0:
+        raise RuntimeError(f"glint_expand_packed_to_f32_host rc={rc}")
+    return bytes(_c.string_at(_c.addressof(out), n * 4))
+
+
+def expand_bf16_host(hole: bytes, plug: bytes, absmax_f32: bytes, n: int, blocksize: int = 64) -> bytes:
+    lib = encode_lib()
+    out = (_c.c_uint16 * n)()
+    h = _c.create_string_buffer(bytes(hole), len(hole))
+    p = _c.create_string_buffer(bytes(plug), len(plug))
+    a = _c.create_string_buffer(bytes(absmax_f32), len(absmax_f32))
+    rc = lib.glint_expand_packed_to_bf16_host(h, p, a, n, blocksize, out)
+    if rc != 0:
+        raise RuntimeError(f"glint_expand_packed_to_bf16_host rc={rc}")
+    return bytes(_c.string_at(_c.addressof(out), n * 2))

@@ -1,0 +1,114 @@
+"""GPU H-TILE parity.
+
+f32 ABI (launch_glint_htile_s3_f32[_stream]): the reference's device tests restated —
+  K-bounds test (test_htile_k_bounds_device.cu:44-118: shift 0/1 misaligned pointers,
+  K in {1..256}, 5 shapes, bs=23, canaries, 3 repetitions, |err| <= 1e-5 (1 + |ref|) vs
+  float64) and the 10-shape test (test_glint_htile.cu:63-153: max_diff < 1e-3 vs f32);
+  plus the M=1 fast GEMV at the BASELINE shapes vs float64 within the f32 summation
+  bound (K + 2) 2^-23 sum|terms| (test_streamer_real_weights.cu:130-133).
+bf16 path (launch_glint_htile_bf16_stream): rel Frobenius <= 1e-2 vs an f32 GEMM on
+  the expanded weights, and far tighter in practice.
+"""
+import numpy as np
+import pytest
+
+from glint_amd import glint_hip as H
+from oracle import glint_oracle as G
+from tests.gpu_util import dev, host, bf16_bits, torch_cuda
+
+pytestmark = pytest.mark.gpu
+
+
+def _kbounds_inputs(M, N, K, bs):
+    i = np.arange(N * K, dtype=np.int64)
+    h = ((i * 7 + i // 17 + 3) % 16).astype(np.uint8)
+    p = ((i * 11 + i // 13 + 5) % 16).astype(np.uint8)
+    hole = G.pack_nibbles(h)
+    plug = G.pack_nibbles(p)
+    nb = (N * K + bs - 1) // bs
+    scales = (0.25 + (np.arange(nb) % 7) * 0.125).astype(np.float32)
+    j = np.arange(M * K, dtype=np.int64)
+    x = bf16_bits((((j * 3 + j // 19) % 17) - 8).astype(np.float32) * 0.0625)
+    return hole, plug, scales, x
+
+
+@pytest.mark.parametrize("shift", [0, 1])
+def test_reference_k_bounds_device_cases(oracle, shift):
+    torch = torch_cuda()
+    bs, guard, canary = 23, 16, 123456.0
+    worst = 0.0
+    for K in (1, 32, 40, 48, 63, 64, 65, 192, 199, 256):
+        for M, N in ((1, 1), (15, 15), (16, 16), (17, 19), (33, 31)):
+            hole, plug, scales, x = _kbounds_inputs(M, N, K, bs)
+            dh, dp, dx = dev(hole, shift), dev(plug, shift), dev(x, shift)
+            da = dev(scales)
+            y = torch.full((M * N + 2 * guard,), canary, dtype=torch.float32, device="cuda")
+            ref, _ = oracle.htile_f64(hole, plug, scales, x, M, N, K, bs)
+            for _rep in range(3):
+                rc = H.encode_lib().launch_glint_htile_s3_f32(
+                    H._p(dh), H._p(dp), H._p(da), H._p(dx), H.VP(y.data_ptr() + 4 * guard), M, N, K, bs)
+                assert rc == 0
+                got = host(y)
+                assert (got[:guard] == canary).all() and (got[guard + M * N:] == canary).all(), (M, N, K)
+                out = got[guard:guard + M * N].reshape(M, N).astype(np.float64)
+                err = np.abs(out - ref)
+                assert np.isfinite(out).all()
+                assert (err <= 1e-5 * (1 + np.abs(ref))).all(), (shift, M, N, K, float(err.max()))
+                worst = max(worst, float(err.max()))
+    assert worst < 1e-4
+
+
+def test_reference_ten_shapes(oracle):
+    cases = [(16, 16, 64, 64), (16, 16, 128, 64), (32, 32, 192, 64), (16, 16, 32, 64), (16, 16, 48, 64),
+             (16, 16, 40, 64), (16, 16, 70, 64), (16, 16, 100, 64), (7, 23, 64, 64), (4, 3072, 3072, 64)]
+    for M, N, K, bs in cases:
+        nw, nx = N * K, M * K
+        npk, nam = (nw + 1) // 2, (nw + bs - 1) // bs
+        i = np.arange(npk, dtype=np.int64)
+        hole = ((i * 7 + 1) % 256).astype(np.uint8)
+        plug = ((i * 13 + 5) % 256).astype(np.uint8)
+        am = (0.5 + (np.arange(nam) % 10) * 0.1).astype(np.float32)
+        j = np.arange(nx, dtype=np.int64)
+        x = bf16_bits((((j * 17 + 3) % 100) - 50).astype(np.float32) * 0.01)
+        y = host(H.htile_f32(dev(hole), dev(plug), dev(am), dev(x), N, K, bs)).reshape(M, N)
+        ref = oracle.htile_f32(hole, plug, am, x, M, N, K, bs)
+        assert float(np.abs(y - ref).max()) < 1e-3, (M, N, K)
+
+
+def _encoded_weight(oracle, N, K, seed, bs=64):
+    torch = torch_cuda()
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn(N * K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    return H.encode_bf16(w, bs)
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336), (100, 64), (3, 1088), (129, 2048)])
+def test_gemv_fast_path_vs_float64(oracle, N, K):
+    torch = torch_cuda()
+    hole, plug, am = _encoded_weight(oracle, N, K, 2002)
+    g = torch.Generator(device="cuda").manual_seed(2001)
+    x = torch.randn(K, device="cuda", generator=g).to(torch.bfloat16)
+    y = host(H.htile_f32(hole, plug, am, x, N, K, 64)).reshape(-1).astype(np.float64)
+    yb = host(H.htile_bf16(hole, plug, am, x, N, K, 64), np.uint16).reshape(-1)
+    ref, asum = oracle.htile_f64(host(hole), host(plug), host(am), host(x, np.uint16), 1, N, K, 64)
+    ref, asum = ref.reshape(-1), asum.reshape(-1)
+    bound = (K + 2) * 2.0 ** -23 * asum
+    assert (np.abs(y - ref) <= bound).all(), float((np.abs(y - ref) / bound).max())
+    assert (np.abs(y - ref) <= 1e-5 * (1 + np.abs(ref))).all()
+    yb64 = G.bf16_bits_to_f32(yb).astype(np.float64)
+    assert (np.abs(yb64 - ref) <= np.abs(ref) * 2.0 ** -8 + bound * 1.01).all()
+
+
+@pytest.mark.parametrize("M", [1, 4, 64, 200])
+def test_bf16_path_rel_frobenius(oracle, M):
+    torch = torch_cuda()
+    N, K = 1024, 4096
+    hole, plug, am = _encoded_weight(oracle, N, K, 3002)
+    g = torch.Generator(device="cuda").manual_seed(3001)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    y = H.htile_bf16(hole, plug, am, x, N, K, 64).float()
+    w = H.expand_f32(hole, plug, am, N * K, 64).reshape(N, K)
+    ref = x.float() @ w.T
+    rel = float(torch.linalg.norm(y - ref) / torch.linalg.norm(ref))
+    assert rel <= 1e-2
+    assert rel <= 4e-3  # BF16 rounding of the output alone is ~2^-9

@@ -1,0 +1,91 @@
+"""GPU INT8 parity.
+
+int8_mma_gemm (attach ABI): quantized activation bytes identical to the oracle
+(test_int8_mma_gemm.cu:127-132) and y bit-identical to the oracle's emulation of the
+per-64-slice arithmetic (the reference gates at rel <= 1e-5, :207); k_in % 64 != 0 refused.
+glint_int8_gemm_i32 / _scaled_bf16: int32 results bit-exact vs an exact integer GEMM.
+"""
+import numpy as np
+import pytest
+
+from glint_amd import glint_hip as H
+from oracle import glint_oracle as G
+from tests.gpu_util import dev, host, bf16_bits, first_diff, torch_cuda
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("m,n,k", [(70, 192, 256), (37, 100, 1536), (1, 64, 64), (130, 257, 512)])
+def test_int8_mma_gemm_matches_emulation(oracle, m, n, k):
+    rng = np.random.default_rng(m * 1000 + n)
+    x = bf16_bits(rng.normal(0, 1, m * k).astype(np.float32))
+    wq = rng.integers(-127, 128, n * k, dtype=np.int8)
+    sw = rng.uniform(1e-3, 2e-2, n * (k // 64)).astype(np.float32)
+    y, xq, sx = H.int8_mma_gemm(dev(x), dev(wq), dev(sw), n, k)
+    oxq, osx = oracle.quant_act(x, m, k)
+    gxq, gsx = host(xq), host(sx)
+    assert gxq.tobytes() == oxq.tobytes(), first_diff(gxq, oxq)
+    assert gsx.tobytes() == osx.tobytes()
+    ref = oracle.int8_mma_emu(oxq, osx, wq, sw, m, n, k)
+    got = host(y).reshape(m, n)
+    assert got.tobytes() == ref.tobytes(), first_diff(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_quant_act_special_values(oracle):
+    vals = np.zeros(64 * 4, np.float32)
+    vals[1], vals[2], vals[3] = 127.0, 2.5, -3.5                   # s = 1: ties to even
+    vals[64:128] = np.linspace(-3, 3, 64)
+    vals[130] = np.nan                                              # NaN skipped by the max
+    vals[128:130] = [0.5, -0.25]
+    vals[192:] = 1e-38
+    x = bf16_bits(vals)
+    n, k = 64, 256
+    wq = np.ones(n * k, np.int8)
+    sw = np.ones(n * (k // 64), np.float32)
+    y, xq, sx = H.int8_mma_gemm(dev(x), dev(wq), dev(sw), n, k)
+    oxq, osx = oracle.quant_act(x, 1, k)
+    assert host(xq).tobytes() == oxq.tobytes() and host(sx).tobytes() == osx.tobytes()
+
+
+def test_flat_entry_and_refusal():
+    torch = torch_cuda()
+    p7 = H.p7_lib()
+    rng = np.random.default_rng(1)
+    m, n, k = 8, 64, 128
+    x = dev(bf16_bits(rng.normal(0, 1, m * k)))
+    q = dev(rng.integers(-127, 128, n * k, dtype=np.int8))
+    s = dev(rng.uniform(1e-3, 1e-2, n * 2).astype(np.float32))
+    y1 = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    xq = torch.empty(m * k, dtype=torch.int8, device="cuda")
+    sx = torch.empty(m * 2, dtype=torch.float32, device="cuda")
+    rc = p7.p7_int8_gemm_flat(H._p(x), H._p(q), H._p(s), n, k, H._p(y1), m, H._p(xq), H._p(sx), H._stream())
+    assert rc == 0
+    y2, _, _ = H.int8_mma_gemm(x, q, s, n, k)
+    assert torch.equal(y1.reshape(m, n), y2)
+    rc = p7.p7_int8_gemm_flat(H._p(x), H._p(q), H._p(s), n, 96, H._p(y1), m, H._p(xq), H._p(sx), H._stream())
+    assert rc == 1
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 130, 192), (256, 512, 1024), (2048, 256, 8192)])
+def test_int8_gemm_exact(oracle, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = rng.uniform(1e-3, 2e-2, M).astype(np.float32)
+    sb = rng.uniform(1e-3, 2e-2, N).astype(np.float32)
+    dA, dB = dev(A).reshape(M, K), dev(B).reshape(N, K)
+    C = host(H.int8_gemm_i32(dA, dB))
+    ref = oracle.int8_gemm_i32(A, B, M, N, K)
+    assert np.array_equal(C, ref), first_diff(C, ref)
+    out = host(H.int8_gemm_scaled_bf16(dA, dB, dev(sa), dev(sb)), np.uint16)
+    assert np.array_equal(out, oracle.int8_scale_bf16(ref, sa, sb, M, N))
+
+
+def test_int8_gemm_extremes(oracle):
+    """All -127 / all 127 at the largest K of the benchmark: |C| = K * 127^2 = 132 million."""
+    M, N, K = 128, 128, 8192
+    A = np.full((M, K), -127, np.int8)
+    B = np.full((N, K), 127, np.int8)
+    B[1::2] = -127
+    C = host(H.int8_gemm_i32(dev(A).reshape(M, K), dev(B).reshape(N, K)))
+    assert (C[:, 0::2] == -K * 127 * 127).all() and (C[:, 1::2] == K * 127 * 127).all()
