@@ -9,6 +9,8 @@
  *   workgroup in LDS (bf16); the cell table sits in LDS as 32 bank-private copies, so the
  *   per-element lookups never conflict. Per row: 16 f32 FMAs per lane per step, then one
  *   FMA by the block absmax, then a wave reduction.
+ * k_htile_mfma_b64 — prefill (M > 1, bf16 out, bs = 64): BF16 MFMA on LDS-dequantized
+ *   weight tiles, f32 accumulation.
  * k_htile_generic — every other shape (any M, K, bs, alignment): 64x32 output tiles,
  *   weights decoded to f32 in LDS per 32-wide K step, f32 FMAs in k order.
  */
@@ -188,6 +190,134 @@ __global__ __launch_bounds__(256) void k_htile_generic(const uint8_t *__restrict
         }
 }
 
+/* ---------------------------------------------------- prefill GEMM on BF16 MFMA */
+/* y[M, N] (bf16) = x[M, K] W^T for bs = 64, K % 64 == 0. Block tile BM x 128 x 64 (K);
+ * 4 waves in 2 x 2, wave tile (BM/2) x 64 = (BM/32) x 4 MFMA tiles of 16x16
+ * (v_mfma_f32_16x16x32_bf16, two K halves per step). Per K step each thread turns 32
+ * packed weights of one row (16 B of each plane) into BF16 RNE(cell * absmax) through
+ * the bank-private LDS table and writes them to the W tile; the next step's planes and
+ * x tile are loaded from HBM while the MFMAs run. LDS rows are padded by 8 BF16 so the
+ * 16 rows read by one MFMA operand load fall in distinct bank groups. */
+typedef __bf16 glint_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 glint_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float glint_f32x2 __attribute__((ext_vector_type(2)));
+
+#define MF_BN 128
+#define MF_LDW 72 /* 64 + 8 bf16 per LDS row */
+
+__device__ __forceinline__ uint32_t glint_cvt_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(glint_f32x2{lo, hi}, glint_bf16x2));
+}
+
+template <int BM>
+__global__ __launch_bounds__(256) void k_htile_mfma_b64(const glint_u32x4 *__restrict__ hole,
+                                                        const glint_u32x4 *__restrict__ plug,
+                                                        const float *__restrict__ absmax, const uint16_t *__restrict__ x,
+                                                        uint16_t *__restrict__ y, int M, int N, int K) {
+    constexpr int WM = BM / 2, TM = WM / 16, XV = BM / 32; /* x u32x4 loads per thread */
+    __shared__ float ltab[GLINT_LDS_CELLS_WORDS];
+    __shared__ float stage[256];
+    __shared__ __attribute__((aligned(16))) uint16_t sX[BM * MF_LDW];
+    __shared__ __attribute__((aligned(16))) uint16_t sW[MF_BN * MF_LDW];
+    glint_fill_cells_lds(ltab, stage);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * MF_BN;
+    const uint32_t lb = lane & 31;
+    const int nK = K >> 6;
+    /* staging roles: weights row wr = tid >> 1, K half wh = tid & 1 (32 elements) */
+    const int wr = tid >> 1, wh = tid & 1;
+    const int wn_row = n0 + wr;
+    glint_f32x4 acc[TM][4];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
+
+    glint_u32x4 hv, pv, xv[XV];
+    float av;
+    auto gload = [&](int kb) {
+        if (wn_row < N) {
+            const int64_t q = (int64_t)wn_row * (K >> 5) + kb * 2 + wh; /* 32-element groups */
+            hv = __builtin_nontemporal_load(&hole[q]);
+            pv = __builtin_nontemporal_load(&plug[q]);
+            av = absmax[(int64_t)wn_row * (K >> 6) + kb];
+        } else {
+            hv = pv = glint_u32x4{0u, 0u, 0u, 0u};
+            av = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int idx = tid + 256 * i, xr = idx >> 3, xc = idx & 7;
+            const int m = m0 + xr;
+            xv[i] = (m < M) ? *(const glint_u32x4 *)(x + (int64_t)m * K + (int64_t)kb * 64 + xc * 8)
+                            : glint_u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    gload(0);
+    for (int kb = 0; kb < nK; ++kb) {
+        /* dequantize this thread's 32 weights and stage x */
+        {
+            const uint32_t H[4] = {hv.x, hv.y, hv.z, hv.w}, P[4] = {pv.x, pv.y, pv.z, pv.w};
+            uint32_t packed[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t E = ((H[q] << 4) & 0xF0F0F0F0u) | (P[q] & 0x0F0F0F0Fu);
+                const uint32_t O = (H[q] & 0xF0F0F0F0u) | ((P[q] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const float ve = ltab[(((E >> (8 * b)) & 0xFFu) << 5) | lb] * av;
+                    const float vo = ltab[(((O >> (8 * b)) & 0xFFu) << 5) | lb] * av;
+                    packed[4 * q + b] = glint_cvt_bf16x2(ve, vo);
+                }
+            }
+            glint_u32x4 *dst = (glint_u32x4 *)(sW + wr * MF_LDW + wh * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                dst[i] = glint_u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
+#pragma unroll
+            for (int i = 0; i < XV; ++i) {
+                const int idx = tid + 256 * i, xr = idx >> 3, xc = idx & 7;
+                *(glint_u32x4 *)(sX + xr * MF_LDW + xc * 8) = xv[i];
+            }
+        }
+        __syncthreads();
+        if (kb + 1 < nK)
+            gload(kb + 1);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int kofs = ks * 32 + (lane >> 4) * 8;
+            glint_bf16x8 af[TM], bfr[4];
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+                af[a] = __builtin_bit_cast(glint_bf16x8,
+                                           *(const glint_u32x4 *)(sX + (wm * WM + a * 16 + (lane & 15)) * MF_LDW + kofs));
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                bfr[b] = __builtin_bit_cast(glint_bf16x8,
+                                            *(const glint_u32x4 *)(sW + (wn * 64 + b * 16 + (lane & 15)) * MF_LDW + kofs));
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm * WM + a * 16 + (lane >> 4) * 4 + i;
+                const int n = n0 + wn * 64 + b * 16 + (lane & 15);
+                if (m < M && n < N)
+                    y[(int64_t)m * N + n] = glint_f32_to_bf16(acc[a][b][i]);
+            }
+}
+
 /* ------------------------------------------------------------------ dispatch */
 template <bool OUT_BF16>
 static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y, int M,
@@ -201,7 +331,18 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
     const bool gemv_ok = M == 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 8) && glint_aligned(plug, 8) &&
                          glint_aligned(absmax, 4) && glint_aligned(x, 16) &&
                          K <= GEMV_MAX_K;
-    if (gemv_ok) {
+    const bool mfma_ok = OUT_BF16 && M > 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) &&
+                         glint_aligned(plug, 16) && glint_aligned(absmax, 4) && glint_aligned(x, 16);
+    if (mfma_ok) {
+        const unsigned gx = (unsigned)((N + MF_BN - 1) / MF_BN);
+        if (M <= 64) {
+            k_htile_mfma_b64<64><<<dim3(gx, (M + 63) / 64), 256, 0, st>>>(
+                (const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
+        } else {
+            k_htile_mfma_b64<128><<<dim3(gx, (M + 127) / 128), 256, 0, st>>>(
+                (const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
+        }
+    } else if (gemv_ok) {
         constexpr int R = 4;
         const int64_t groups = ((int64_t)N + R - 1) / R;
         const int waves = GEMV_THREADS / 64;

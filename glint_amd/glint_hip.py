@@ -78,6 +78,13 @@ P7_SYMBOLS = tuple(_P7_SIGS)
 
 
 def _bind(path: Path, sigs: dict) -> ctypes.CDLL:
+    # One HIP runtime per process: torch's wheel ships its own libamdhip64.so.7. If torch
+    # is importable, load it first so our library binds to that already-loaded runtime
+    # (same SONAME) instead of pulling in a second copy from /opt/rocm.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(path))
     for name, (args, res) in sigs.items():
         f = getattr(lib, name)
