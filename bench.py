@@ -220,6 +220,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline GEMV only")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run 10 plain 256 MiB device copies (the reference kernel for scaling PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the GLINT hot path has no multi-GPU mode in this build "
@@ -233,6 +235,13 @@ def main() -> int:
     H.encode_lib()
     H.p7_lib()
     log(f"device {torch.cuda.get_device_name(0)}")
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     gemv, pins, x = bench_gemv(torch, H, args.steps, args.warmup)
     log(f"gemv {gemv['ms'] * 1e3:.2f} us {gemv['gbs']:.0f} GB/s")
     del pins

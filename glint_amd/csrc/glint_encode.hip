@@ -56,7 +56,8 @@ __device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const Gl
     /* absmax of this lane's 8 values, then of the 8 lanes that share the block */
     glint_i16x2 k = __builtin_elementwise_max(glint_mag_key(d.x), glint_mag_key(d.y));
     k = __builtin_elementwise_max(k, __builtin_elementwise_max(glint_mag_key(d.z), glint_mag_key(d.w)));
-    int m16 = max((int)k.x, (int)k.y) - 0x7F;
+    /* floor at key 0x7F (magnitude 0): a lane whose values are all NaN contributes 0 */
+    int m16 = max(max((int)k.x, (int)k.y), 0x7F) - 0x7F;
     m16 = glint_max8(m16);
     const uint32_t sbits = (uint32_t)m16 << 16;
     const float s = __uint_as_float(sbits);

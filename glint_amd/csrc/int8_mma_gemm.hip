@@ -43,7 +43,8 @@ __global__ __launch_bounds__(256) void k_quant_act(const glint_u32x4 *__restrict
         const glint_u32x4 d = x[t];
         glint_i16x2 k = __builtin_elementwise_max(q_mag_key(d.x), q_mag_key(d.y));
         k = __builtin_elementwise_max(k, __builtin_elementwise_max(q_mag_key(d.z), q_mag_key(d.w)));
-        const int m16 = glint_max8(max((int)k.x, (int)k.y) - 0x7F);
+        /* floor at key 0x7F (magnitude 0) so an all-NaN lane contributes 0 */
+        const int m16 = glint_max8(max(max((int)k.x, (int)k.y), 0x7F) - 0x7F);
         const float am = __uint_as_float((uint32_t)m16 << 16);
         const float s = (am > 0.0f) ? (am / 127.0f) : 1.0f;
         const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
@@ -51,6 +52,7 @@ __global__ __launch_bounds__(256) void k_quant_act(const glint_u32x4 *__restrict
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const float w = (j & 1) ? glint_bf16hi(dw[j >> 1]) : glint_bf16lo(dw[j >> 1]);
+            /* float -> int as the reference's CUDA cast: NaN -> 0, saturating */
             int v = (int)rintf(w / s);
             v = v > 127 ? 127 : (v < -127 ? -127 : v);
             packed[j >> 2] |= ((uint32_t)v & 0xFFu) << (8 * (j & 3));

@@ -171,6 +171,18 @@ EXPORT void oracle_htile_f64(const uint8_t *hole, const uint8_t *plug, const flo
         }
 }
 
+/* float -> int32 the way the reference's CUDA `(int)` cast converts (PTX cvt.rzi.s32.f32:
+ * NaN -> 0, out-of-range values saturate); a plain C cast of NaN is undefined. */
+static int cvt_s32(float f) {
+    if (f != f)
+        return 0;
+    if (f >= 2147483648.0f)
+        return 2147483647;
+    if (f <= -2147483648.0f)
+        return (int)0x80000000u;
+    return (int)f;
+}
+
 /* Activation quantization per (row, 64-block): s = amax > 0 ? amax / 127 : 1,
  * q = clamp(rint(x / s), -127, 127) (int8_mma_gemm.cu:11-29). k % 64 == 0. */
 EXPORT void oracle_quant_act(const uint16_t *x, int m, int k, int8_t *xq, float *sx) {
@@ -185,7 +197,7 @@ EXPORT void oracle_quant_act(const uint16_t *x, int m, int k, int8_t *xq, float 
             const float s = (am > 0.f) ? (am / 127.f) : 1.f;
             sx[(int64_t)r * nkb + kb] = s;
             for (int t = 0; t < 64; ++t) {
-                int v = (int)rintf(bf16_to_f32(x[base + t]) / s);
+                int v = cvt_s32(rintf(bf16_to_f32(x[base + t]) / s));
                 v = v > 127 ? 127 : (v < -127 ? -127 : v);
                 xq[base + t] = (int8_t)v;
             }

@@ -264,6 +264,16 @@ def test_quant_act_known_answers(oracle):
     assert sx0.tolist() == [1.0] and not xq0.any()
 
 
+def test_quant_act_nan_converts_like_the_cuda_cast(oracle):
+    """A NaN activation is skipped by the block max and quantizes to 0: the reference's
+    (int)rintf(NaN / s) is a saturating cvt.rzi.s32.f32, which maps NaN to 0."""
+    vals = np.linspace(-2, 2, 64).astype(np.float32)
+    vals[7] = np.nan
+    xq, sx = oracle.quant_act(G.f32_to_bf16_bits(vals), 1, 64)
+    assert sx.tolist() == [np.float32(2.0) / np.float32(127.0)]
+    assert xq[7] == 0 and xq[0] == -127 and xq[63] == 127
+
+
 def test_int8_integer_parts_are_exact(oracle):
     rng = np.random.default_rng(5)
     M, N, K = 7, 9, 192
