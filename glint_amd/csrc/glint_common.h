@@ -39,6 +39,39 @@ __device__ __forceinline__ void glint_fill_cells_lds(float *ltab, float *stage) 
     __syncthreads();
 }
 
+/* 64-copy layout for the streaming kernels: word (c << 6) | lane, i.e. byte address
+ * c * 256 + lane * 4 (64 KiB). Every lane reads its own copy, each copy lives in one
+ * bank, and the byte address of code byte k of a word E is one v_perm_b32 that drops
+ * E's byte k into address byte 1 next to the lane's byte lane*4. */
+#define GLINT_LDS_CELLS64_WORDS (256 * 64)
+
+__device__ __forceinline__ void glint_fill_cells_lds64(float *ltab, float *stage) {
+    for (int i = threadIdx.x; i < 256; i += blockDim.x)
+        stage[i] = (&kCells[0][0])[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < GLINT_LDS_CELLS64_WORDS; i += blockDim.x)
+        ltab[i] = stage[i >> 6];
+    __syncthreads();
+}
+
+/* Byte address of code byte K of E for the lane whose lane*4 is `lane4` (in byte 0). */
+template <int K>
+__device__ __forceinline__ uint32_t glint_cell_addr(uint32_t E, uint32_t lane4) {
+    return __builtin_amdgcn_perm(E, lane4, 0x0C0C0000u | ((4u + K) << 8));
+}
+__device__ __forceinline__ float glint_lds_f32(const float *base, uint32_t byte_addr) {
+    return *(const float *)((const char *)base + byte_addr);
+}
+
+/* Code bytes of 4 consecutive element pairs: byte j of the even word is element 2j's
+ * code (hole << 4 | plug), byte j of the odd word element 2j+1's. */
+__device__ __forceinline__ uint32_t glint_codes_even(uint32_t H, uint32_t P) {
+    return ((H << 4) & 0xF0F0F0F0u) | (P & 0x0F0F0F0Fu);
+}
+__device__ __forceinline__ uint32_t glint_codes_odd(uint32_t H, uint32_t P) {
+    return (H & 0xF0F0F0F0u) | ((P >> 4) & 0x0F0F0F0Fu);
+}
+
 /* ------------------------------------------------------------- device helpers */
 typedef uint32_t glint_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t glint_u32x2 __attribute__((ext_vector_type(2)));
@@ -99,6 +132,28 @@ __device__ __forceinline__ float glint_wave_max(float v) {
 }
 
 /* ------------------------------------------------------------- host helpers */
+#include <mutex>
+
 static inline bool glint_aligned(const void *p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+/* Raise a kernel's dynamic-LDS limit to `bytes` on the current device (needed above
+ * 64 KiB); remembered per (kernel, device). Returns 0 or -1. */
+static inline int glint_set_lds_limit(const void *kernel, size_t bytes) {
+    static std::mutex mu;
+    static struct { const void *k; int dev; size_t bytes; } seen[64];
+    static int nseen = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return -1;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < nseen; ++i)
+        if (seen[i].k == kernel && seen[i].dev == dev && seen[i].bytes >= bytes)
+            return 0;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess)
+        return -1;
+    if (nseen < 64)
+        seen[nseen++] = {kernel, dev, bytes};
+    return 0;
+}
 
 #endif

@@ -227,52 +227,86 @@ static int encode_device(const T *d_w, int64_t n, int bs, uint8_t *d_hole, uint8
 }
 
 /* ------------------------------------------------------------------ expand */
-/* Per lane: 32 consecutive elements (16 B of each plane), all inside one absmax block
- * (bs % 32 == 0), looked up in the bank-private LDS cell table. */
+/* A group is 32 consecutive elements (16 B of each plane) inside one absmax block
+ * (bs % 32 == 0). Each lane issues the loads of EU groups before converting any, looks
+ * cells up in the 64-copy LDS table (one v_perm_b32 per address) and writes 64 B (BF16)
+ * or 128 B (f32) per group. */
+#define EXPAND_THREADS 1024
+#define EXPAND_U 4
+
 template <bool BF16>
-__global__ __launch_bounds__(256) void k_expand_fast(const glint_u32x4 *__restrict__ hole, const glint_u32x4 *__restrict__ plug,
-                                                     const float *__restrict__ absmax, void *__restrict__ out,
-                                                     int64_t ngroups, int bs) {
-    __shared__ float ltab[GLINT_LDS_CELLS_WORDS];
-    __shared__ float stage[256];
-    glint_fill_cells_lds(ltab, stage);
-    const uint32_t lb = threadIdx.x & 31;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
-        const glint_u32x4 hv = __builtin_nontemporal_load(&hole[g]);
-        const glint_u32x4 pv = __builtin_nontemporal_load(&plug[g]);
-        const float a = absmax[(g * 32) / bs];
-        const uint32_t H[4] = {hv.x, hv.y, hv.z, hv.w}, P[4] = {pv.x, pv.y, pv.z, pv.w};
-        float r[32];
+__device__ __forceinline__ void expand_group(const float *ltab, uint32_t lane4, glint_u32x4 hv, glint_u32x4 pv, float a,
+                                             void *__restrict__ out, int64_t g) {
+    const uint32_t H[4] = {hv.x, hv.y, hv.z, hv.w}, P[4] = {pv.x, pv.y, pv.z, pv.w};
+    float r[32];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t E = ((H[q] << 4) & 0xF0F0F0F0u) | (P[q] & 0x0F0F0F0Fu);
-            const uint32_t O = (H[q] & 0xF0F0F0F0u) | ((P[q] >> 4) & 0x0F0F0F0Fu);
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t E = glint_codes_even(H[q], P[q]);
+        const uint32_t O = glint_codes_odd(H[q], P[q]);
+        r[8 * q + 0] = glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)) * a;
+        r[8 * q + 1] = glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)) * a;
+        r[8 * q + 2] = glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)) * a;
+        r[8 * q + 3] = glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)) * a;
+        r[8 * q + 4] = glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)) * a;
+        r[8 * q + 5] = glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)) * a;
+        r[8 * q + 6] = glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)) * a;
+        r[8 * q + 7] = glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)) * a;
+    }
+    if (BF16) {
+        glint_u32x4 *o = (glint_u32x4 *)out + g * 4;
+        if (a == a) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                r[8 * q + 2 * j] = ltab[(((E >> (8 * j)) & 0xFFu) << 5) | lb] * a;
-                r[8 * q + 2 * j + 1] = ltab[(((O >> (8 * j)) & 0xFFu) << 5) | lb] * a;
-            }
+            for (int q = 0; q < 4; ++q)
+                __builtin_nontemporal_store(
+                    glint_u32x4{glint_pack_bf16x2(r[8 * q], r[8 * q + 1]), glint_pack_bf16x2(r[8 * q + 2], r[8 * q + 3]),
+                                glint_pack_bf16x2(r[8 * q + 4], r[8 * q + 5]), glint_pack_bf16x2(r[8 * q + 6], r[8 * q + 7])},
+                    &o[q]);
+        } else { /* NaN absmax: the reference NaN rule for every element */
+            uint16_t *o16 = (uint16_t *)out + g * 32;
+            for (int j = 0; j < 32; ++j)
+                o16[j] = glint_f32_to_bf16(r[j]);
         }
-        if (BF16) {
-            glint_u32x4 *o = (glint_u32x4 *)out + g * 4;
-            if (a == a) {
+    } else {
+        glint_f32x4 *o = (glint_f32x4 *)out + g * 8;
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    __builtin_nontemporal_store(
-                        glint_u32x4{glint_pack_bf16x2(r[8 * q], r[8 * q + 1]), glint_pack_bf16x2(r[8 * q + 2], r[8 * q + 3]),
-                                    glint_pack_bf16x2(r[8 * q + 4], r[8 * q + 5]), glint_pack_bf16x2(r[8 * q + 6], r[8 * q + 7])},
-                        &o[q]);
-            } else { /* NaN absmax: the reference NaN rule for every element */
-                uint16_t *o16 = (uint16_t *)out + g * 32;
-                for (int j = 0; j < 32; ++j)
-                    o16[j] = glint_f32_to_bf16(r[j]);
-            }
-        } else {
-            glint_f32x4 *o = (glint_f32x4 *)out + g * 8;
+        for (int q = 0; q < 8; ++q)
+            __builtin_nontemporal_store(glint_f32x4{r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]}, &o[q]);
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(EXPAND_THREADS) void k_expand_fast(const glint_u32x4 *__restrict__ hole,
+                                                                const glint_u32x4 *__restrict__ plug,
+                                                                const float *__restrict__ absmax, void *__restrict__ out,
+                                                                int64_t ngroups, int bs) {
+    __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS];
+    __shared__ float stage[256];
+    const uint32_t lane4 = (threadIdx.x & 63) * 4u;
+    const int64_t nthreads = (int64_t)gridDim.x * EXPAND_THREADS;
+    const int64_t t0 = (int64_t)blockIdx.x * EXPAND_THREADS + threadIdx.x;
+    const int gpb = bs >> 5; /* groups per absmax block */
+    /* first batch of loads goes out before the table fill */
+    glint_u32x4 hv[EXPAND_U], pv[EXPAND_U];
+    float av[EXPAND_U];
+    int64_t g = t0;
 #pragma unroll
-            for (int q = 0; q < 8; ++q)
-                __builtin_nontemporal_store(glint_f32x4{r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]}, &o[q]);
+    for (int u = 0; u < EXPAND_U; ++u) {
+        const int64_t gu = min(g + u * nthreads, ngroups - 1);
+        hv[u] = __builtin_nontemporal_load(&hole[gu]);
+        pv[u] = __builtin_nontemporal_load(&plug[gu]);
+        av[u] = absmax[gu / gpb];
+    }
+    glint_fill_cells_lds64(ltab, stage);
+    for (; g < ngroups; g += EXPAND_U * nthreads) {
+#pragma unroll
+        for (int u = 0; u < EXPAND_U; ++u) {
+            const int64_t gu = g + u * nthreads;
+            if (gu < ngroups)
+                expand_group<BF16>(ltab, lane4, hv[u], pv[u], av[u], out, gu);
+            const int64_t gn = min(gu + EXPAND_U * nthreads, ngroups - 1);
+            hv[u] = __builtin_nontemporal_load(&hole[gn]);
+            pv[u] = __builtin_nontemporal_load(&plug[gn]);
+            av[u] = absmax[gn / gpb];
         }
     }
 }
@@ -307,9 +341,8 @@ static int expand_device(const uint8_t *d_hole, const uint8_t *d_plug, const flo
         n_fast = (n / 32) * 32;
     if (n_fast) {
         const int64_t ngroups = n_fast / 32;
-        k_expand_fast<BF16><<<glint_grid(ngroups, 256, cus * 4), 256, 0, st>>>((const glint_u32x4 *)d_hole,
-                                                                               (const glint_u32x4 *)d_plug, d_am, d_out,
-                                                                               ngroups, bs);
+        k_expand_fast<BF16><<<glint_grid(ngroups, EXPAND_THREADS * EXPAND_U, cus * 2), EXPAND_THREADS, 0, st>>>(
+            (const glint_u32x4 *)d_hole, (const glint_u32x4 *)d_plug, d_am, d_out, ngroups, bs);
     }
     if (n_fast < n)
         k_expand_generic<BF16><<<glint_grid(n - n_fast, 256, cus * 16), 256, 0, st>>>(d_hole, d_plug, d_am, d_out,

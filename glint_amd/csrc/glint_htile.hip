@@ -5,10 +5,11 @@
  *
  * k_htile_gemv_b64 — decode (M = 1), bs = 64, K % 64 == 0: HBM-bound. A wave owns R
  *   weight rows; lane l reads 8 B of each plane per row per step (16 consecutive k inside
- *   one absmax block), so one wave load is 512 contiguous bytes. x is staged once per
- *   workgroup in LDS (bf16); the cell table sits in LDS as 32 bank-private copies, so the
- *   per-element lookups never conflict. Per row: 16 f32 FMAs per lane per step, then one
- *   FMA by the block absmax, then a wave reduction.
+ *   one absmax block), so one wave load is 512 contiguous bytes, and keeps D steps of
+ *   loads in flight. x is staged once per workgroup in LDS (bf16); the cell table sits in
+ *   LDS as 64 lane-private copies, so lookups never conflict and each lookup address is
+ *   one v_perm_b32. Per element: 0.5 op to form code bytes, 1 perm, 1 LDS read, 1 f32
+ *   FMA; then one FMA by the block absmax per 16 elements and a wave reduction.
  * k_htile_mfma_b64 — prefill (M > 1, bf16 out, bs = 64): BF16 MFMA on LDS-dequantized
  *   weight tiles, f32 accumulation.
  * k_htile_generic — every other shape (any M, K, bs, alignment): 64x32 output tiles,
@@ -18,97 +19,127 @@
 #include "glint_htile.h"
 
 /* ---------------------------------------------------------------- GEMV (M = 1) */
-#define GEMV_THREADS 512
-/* x (K bf16) + the 33 KiB tables stay within the default 64 KiB of LDS per block */
-#define GEMV_MAX_K 15360
+#ifndef GEMV_R
+#define GEMV_R 2 /* weight rows per wave */
+#endif
+#ifndef GEMV_D
+#define GEMV_D 2 /* row-steps of loads in flight per wave */
+#endif
+#ifndef GEMV_T
+#define GEMV_T 512 /* threads per workgroup for K <= 8192 */
+#endif
+/* x (K f32) + the 65 KiB of tables fit in the 160 KiB of LDS */
+#define GEMV_MAX_K 16384
+#define GEMV_LDS_BYTES(K) ((size_t)(K) * 4 + 64) /* dynamic part: x as f32 + one zero chunk */
 
+/* Wave task: rows [n0, n0 + R). Step i covers 16-element chunk j = 64 i + lane of every
+ * row (8 B of each plane, inside one absmax block). Loads run D steps ahead in a ring of
+ * registers (slot d holds steps d, d + D, ...), issued for the first task before the
+ * LDS tables are filled. */
 template <int R>
-struct GemvRows {
-    glint_u32x2 h[R], p[R];
-    float a[R];
-};
-
-template <int R>
-__device__ __forceinline__ void gemv_load(GemvRows<R> &s, const glint_u32x2 *__restrict__ hole,
-                                          const glint_u32x2 *__restrict__ plug, const float *__restrict__ absmax,
-                                          int n0, int N, int K, int j, bool ok) {
+__device__ __forceinline__ void gemv_load_step(const glint_u32x2 *__restrict__ hole, const glint_u32x2 *__restrict__ plug,
+                                               const float *__restrict__ absmax, int n0, int N, int nch, int it,
+                                               int lane, glint_u32x2 (&h)[R], glint_u32x2 (&p)[R], float (&a)[R]) {
+    /* unconditional loads: a lane past the row end reads the row's last chunk, gets
+     * absmax 0 and x = 0, so it adds exactly 0 */
+    const int jr = it * 64 + lane;
+    const bool ok = jr < nch;
+    const uint32_t j = (uint32_t)min(jr, nch - 1);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int n = n0 + r;
-        if (ok && n < N) {
-            const int64_t cj = (int64_t)n * (K >> 4) + j; /* 16-element chunk index */
-            s.h[r] = __builtin_nontemporal_load(&hole[cj]);
-            s.p[r] = __builtin_nontemporal_load(&plug[cj]);
-            s.a[r] = absmax[cj >> 2];
-        } else {
-            s.h[r] = glint_u32x2{0u, 0u};
-            s.p[r] = glint_u32x2{0u, 0u};
-            s.a[r] = 0.0f;
-        }
+        /* row base: wave-uniform (scalar) arithmetic; rows past N reuse row N-1 */
+        const int64_t n = min(n0 + r, N - 1);
+        h[r] = __builtin_nontemporal_load(hole + n * nch + j);
+        p[r] = __builtin_nontemporal_load(plug + n * nch + j);
+        const float av = absmax[n * (nch >> 2) + (j >> 2)];
+        a[r] = ok ? av : 0.0f;
     }
 }
 
-template <int R, bool OUT_BF16>
-__global__ __launch_bounds__(GEMV_THREADS) void k_htile_gemv_b64(const glint_u32x2 *__restrict__ hole,
-                                                                 const glint_u32x2 *__restrict__ plug,
-                                                                 const float *__restrict__ absmax,
-                                                                 const glint_u32x4 *__restrict__ x, void *__restrict__ y,
-                                                                 int N, int K) {
-    __shared__ float ltab[GLINT_LDS_CELLS_WORDS];
+template <int R, int D, int THREADS, bool OUT_BF16>
+__global__ __launch_bounds__(THREADS, 4) void k_htile_gemv_b64(const glint_u32x2 *__restrict__ hole,
+                                                               const glint_u32x2 *__restrict__ plug,
+                                                               const float *__restrict__ absmax,
+                                                               const glint_u32x4 *__restrict__ x, void *__restrict__ y,
+                                                               int N, int K) {
+    __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS]; /* 64 KiB at LDS offset 0 */
     __shared__ float stage[256];
-    extern __shared__ glint_u32x4 xs[]; /* K bf16 */
-    for (int i = threadIdx.x; i < (K >> 3); i += blockDim.x)
-        xs[i] = x[i];
-    glint_fill_cells_lds(ltab, stage);
+    extern __shared__ __attribute__((aligned(16))) glint_f32x4 xs[]; /* K f32 */
 
     const int lane = threadIdx.x & 63;
-    const uint32_t lb = lane & 31;
-    const int nchunk = K >> 4;
-    const int iters = (nchunk + 63) >> 6;
-    const int waves_per_block = blockDim.x >> 6;
-    const int64_t nwaves = (int64_t)gridDim.x * waves_per_block;
-    for (int64_t g = (int64_t)blockIdx.x * waves_per_block + (threadIdx.x >> 6); g * R < N; g += nwaves) {
-        const int n0 = (int)(g * R);
+    const uint32_t lane4 = (uint32_t)lane * 4u;
+    const int nch = K >> 4;
+    const int iters = (nch + 63) >> 6;
+    const int wpb = THREADS / 64;
+    const int nwaves = gridDim.x * wpb;
+    /* wave-uniform task index, so row arithmetic stays in scalar registers */
+    int g = blockIdx.x * wpb + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ntasks = (N + R - 1) / R;
+
+    glint_u32x2 rh[D][R], rp[D][R];
+    float ra[D][R];
+    if (g < ntasks) {
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (d < iters)
+                gemv_load_step<R>(hole, plug, absmax, g * R, N, nch, d, lane, rh[d], rp[d], ra[d]);
+    }
+    for (int i = threadIdx.x; i < (K >> 3); i += THREADS) {
+        const glint_u32x4 v = x[i];
+        xs[2 * i] = glint_f32x4{glint_bf16lo(v.x), glint_bf16hi(v.x), glint_bf16lo(v.y), glint_bf16hi(v.y)};
+        xs[2 * i + 1] = glint_f32x4{glint_bf16lo(v.z), glint_bf16hi(v.z), glint_bf16lo(v.w), glint_bf16hi(v.w)};
+    }
+    if (threadIdx.x < 4)
+        xs[(K >> 2) + threadIdx.x] = glint_f32x4{0.f, 0.f, 0.f, 0.f}; /* chunk nch: zeros */
+    glint_fill_cells_lds64(ltab, stage);
+
+    for (; g < ntasks; g += nwaves) {
+        const int n0 = g * R;
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r)
             acc[r] = 0.0f;
-        GemvRows<R> cur, nxt;
-        gemv_load<R>(cur, hole, plug, absmax, n0, N, K, lane, lane < nchunk);
-        for (int it = 0; it < iters; ++it) {
-            const int j = it * 64 + lane;
-            const bool ok = j < nchunk;
-            if (it + 1 < iters)
-                gemv_load<R>(nxt, hole, plug, absmax, n0, N, K, j + 64, j + 64 < nchunk);
-            glint_u32x4 xa = glint_u32x4{0u, 0u, 0u, 0u}, xb = xa;
-            if (ok) {
-                xa = xs[2 * j];
-                xb = xs[2 * j + 1];
-            }
-            const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-            float xf[16];
+        for (int base = 0; base < iters; base += D) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                xf[2 * q] = glint_bf16lo(xw[q]);
-                xf[2 * q + 1] = glint_bf16hi(xw[q]);
-            }
+            for (int d = 0; d < D; ++d) {
+                const int it = base + d;
+                if (it < iters) {
+                    /* x of chunk j; lanes past the row end read the zero chunk */
+                    const int jc = min(it * 64 + lane, nch);
+                    float xf[16];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float part = 0.0f;
-                const uint32_t H[2] = {cur.h[r].x, cur.h[r].y}, P[2] = {cur.p[r].x, cur.p[r].y};
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    const uint32_t E = ((H[q] << 4) & 0xF0F0F0F0u) | (P[q] & 0x0F0F0F0Fu);
-                    const uint32_t O = (H[q] & 0xF0F0F0F0u) | ((P[q] >> 4) & 0x0F0F0F0Fu);
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        part = fmaf(ltab[(((E >> (8 * b)) & 0xFFu) << 5) | lb], xf[8 * q + 2 * b], part);
-                        part = fmaf(ltab[(((O >> (8 * b)) & 0xFFu) << 5) | lb], xf[8 * q + 2 * b + 1], part);
+                    for (int q = 0; q < 4; ++q) {
+                        const glint_f32x4 v = xs[4 * jc + q];
+                        xf[4 * q] = v.x;
+                        xf[4 * q + 1] = v.y;
+                        xf[4 * q + 2] = v.z;
+                        xf[4 * q + 3] = v.w;
                     }
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float part = 0.0f;
+                        const uint32_t H[2] = {rh[d][r].x, rh[d][r].y}, P[2] = {rp[d][r].x, rp[d][r].y};
+#pragma unroll
+                        for (int q = 0; q < 2; ++q) {
+                            const uint32_t E = glint_codes_even(H[q], P[q]);
+                            const uint32_t O = glint_codes_odd(H[q], P[q]);
+                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)), xf[8 * q + 0], part);
+                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)), xf[8 * q + 1], part);
+                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)), xf[8 * q + 2], part);
+                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)), xf[8 * q + 3], part);
+                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)), xf[8 * q + 4], part);
+                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)), xf[8 * q + 5], part);
+                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)), xf[8 * q + 6], part);
+                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)), xf[8 * q + 7], part);
+                        }
+                        acc[r] = fmaf(ra[d][r], part, acc[r]);
+                        /* keep the next row's lookups after this row's FMAs: bounds live registers */
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    if (it + D < iters)
+                        gemv_load_step<R>(hole, plug, absmax, n0, N, nch, it + D, lane, rh[d], rp[d], ra[d]);
                 }
-                acc[r] = fmaf(cur.a[r], part, acc[r]);
             }
-            cur = nxt;
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -119,6 +150,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_htile_gemv_b64(const glint_u32
                 else
                     ((float *)y)[n0 + r] = t;
             }
+        }
+        if (g + nwaves < ntasks) {
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+                if (d < iters)
+                    gemv_load_step<R>(hole, plug, absmax, (g + nwaves) * R, N, nch, d, lane, rh[d], rp[d], ra[d]);
         }
     }
 }
@@ -343,12 +380,26 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
                 (const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
         }
     } else if (gemv_ok) {
-        constexpr int R = 4;
-        const int64_t groups = ((int64_t)N + R - 1) / R;
-        const int waves = GEMV_THREADS / 64;
-        const unsigned grid = (unsigned)((groups + waves - 1) / waves);
-        k_htile_gemv_b64<R, OUT_BF16><<<grid, GEMV_THREADS, (size_t)K * 2, st>>>(
-            (const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, (const glint_u32x4 *)x, y, N, K);
+        constexpr int R = GEMV_R, D = GEMV_D;
+        const size_t lds = GEMV_LDS_BYTES(K);
+        const int64_t tasks = ((int64_t)N + R - 1) / R;
+        if (K <= 8192) {
+            constexpr int T = GEMV_T;
+            auto kern = k_htile_gemv_b64<R, D, T, OUT_BF16>;
+            if (glint_set_lds_limit((const void *)kern, lds) != 0)
+                return -3;
+            const unsigned grid = (unsigned)((tasks + T / 64 - 1) / (T / 64));
+            kern<<<grid, T, lds, st>>>((const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax,
+                                      (const glint_u32x4 *)x, y, N, K);
+        } else {
+            constexpr int T = 1024;
+            auto kern = k_htile_gemv_b64<R, D, T, OUT_BF16>;
+            if (glint_set_lds_limit((const void *)kern, lds) != 0)
+                return -3;
+            const unsigned grid = (unsigned)((tasks + T / 64 - 1) / (T / 64));
+            kern<<<grid, T, lds, st>>>((const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax,
+                                      (const glint_u32x4 *)x, y, N, K);
+        }
     } else {
         dim3 grid((N + GT_N - 1) / GT_N, (M + GT_M - 1) / GT_M);
         k_htile_generic<OUT_BF16><<<grid, 256, 0, st>>>(hole, plug, absmax, (const uint16_t *)x, y, M, N, K, bs);
