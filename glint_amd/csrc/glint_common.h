@@ -136,6 +136,15 @@ __device__ __forceinline__ float glint_wave_max(float v) {
 
 static inline bool glint_aligned(const void *p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+/* Workgroups of `kernel` (block size `threads`, `dyn_lds` bytes of dynamic LDS) that fit
+ * on one CU at once; 1 if the runtime cannot say. Sizes persistent grids. */
+static inline int glint_resident_blocks(const void *kernel, int threads, size_t dyn_lds = 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, dyn_lds) != hipSuccess || n < 1)
+        n = 1;
+    return n;
+}
+
 /* Raise a kernel's dynamic-LDS limit to `bytes` on the current device (needed above
  * 64 KiB); remembered per (kernel, device). Returns 0 or -1. */
 static inline int glint_set_lds_limit(const void *kernel, size_t bytes) {

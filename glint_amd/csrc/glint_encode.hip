@@ -50,15 +50,52 @@ __device__ __forceinline__ glint_i16x2 glint_mag_key(uint32_t d) {
     return __builtin_bit_cast(glint_i16x2, m);
 }
 
-__device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const GlintCodeEntry *tab, int64_t chunk, int lane,
-                                                   uint32_t *__restrict__ hole, uint32_t *__restrict__ plug,
-                                                   float *__restrict__ absmax) {
-    /* absmax of this lane's 8 values, then of the 8 lanes that share the block */
+/* LDS form of the bucket table: entry b = {threshold bits, S(base), S(base + 1), 0} with
+ * the "spread" code S(c) = hole | plug << 16 = (c >> 4) | (c & 15) << 16, so a lane folds
+ * its 4 codes into hole nibbles (bits 0..15) and plug nibbles (bits 16..31) with one
+ * shift-or each. 8 copies, entry b of copy j at byte (b * 8 + j) * 16: the 8 lanes that
+ * one ds_read_b128 pass serves (lane % 8 = j) read 8 disjoint 16-byte bank groups. */
+#define ENC_COPIES 8
+#define ENC_LDS_WORDS (GLINT_CODE_BUCKETS * ENC_COPIES * 4)
+#define ENC_THREADS 1024
+#define ENC_UNROLL 4
+
+__device__ __forceinline__ uint32_t glint_spread_code(uint32_t c) { return (c >> 4) | ((c & 15u) << 16); }
+
+__device__ __forceinline__ void glint_fill_code_lds(glint_u32x4 *tab) {
+    for (int i = threadIdx.x; i < GLINT_CODE_BUCKETS * ENC_COPIES; i += blockDim.x) {
+        const GlintCodeEntry e = kCodeTable[i / ENC_COPIES];
+        tab[i] = glint_u32x4{e.thr, glint_spread_code(e.base), glint_spread_code(e.base + 1), 0u};
+    }
+    __syncthreads();
+}
+
+/* Spread code of v (|v| <= 1 or a quiet NaN; see glint_code_of). `lane_k` is this lane's
+ * constant making the byte address (bucket << 7) + lane_k land on its own copy. */
+__device__ __forceinline__ uint32_t glint_spread_of(float v, const glint_u32x4 *tab, uint32_t lane_k) {
+    const float c = __builtin_amdgcn_fmed3f(v, -1.0f, 1.0f);
+    const uint32_t addr = (__float_as_uint(fmaf(c, 256.0f, GLINT_CODE_MAGIC)) << 7) + lane_k;
+    const glint_u32x4 e = *(const glint_u32x4 *)((const char *)tab + addr);
+    return v > __uint_as_float(e.x) ? e.z : e.y;
+}
+
+template <int CTRL>
+__device__ __forceinline__ int glint_max_dpp(int v) {
+    /* bound_ctrl with full masks lets the DPP move fold into v_max_i32_dpp */
+    return max(v, __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const glint_u32x4 *tab, uint32_t lane_k,
+                                                   int64_t chunk, int lane, uint32_t *__restrict__ hole,
+                                                   uint32_t *__restrict__ plug, float *__restrict__ absmax) {
+    /* absmax of this lane's 8 values, then of the 8 lanes that share the block; the
+     * floor at key 0x7F (magnitude 0) makes an all-NaN lane contribute 0 */
     glint_i16x2 k = __builtin_elementwise_max(glint_mag_key(d.x), glint_mag_key(d.y));
     k = __builtin_elementwise_max(k, __builtin_elementwise_max(glint_mag_key(d.z), glint_mag_key(d.w)));
-    /* floor at key 0x7F (magnitude 0): a lane whose values are all NaN contributes 0 */
     int m16 = max(max((int)k.x, (int)k.y), 0x7F) - 0x7F;
-    m16 = glint_max8(m16);
+    m16 = glint_max_dpp<GLINT_DPP_QUAD_1032>(m16);
+    m16 = glint_max_dpp<GLINT_DPP_QUAD_2301>(m16);
+    m16 = glint_max_dpp<GLINT_DPP_ROW_HALF_MIRROR>(m16);
     const uint32_t sbits = (uint32_t)m16 << 16;
     const float s = __uint_as_float(sbits);
 
@@ -83,48 +120,59 @@ __device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const Gl
         for (int j = 0; j < 8; ++j)
             v[j] = (s == 0.0f) ? 0.0f : w[j] / s;
     }
-    uint32_t c[8];
+    /* element 4h + i contributes its hole nibble at bit 4i and plug nibble at 16 + 4i */
+    uint32_t acc[2];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-        c[j] = glint_code_of(v[j], tab);
-    /* bytes c0..c3 / c4..c7 -> nibble planes: plug = low nibbles, hole = high nibbles */
-    const uint32_t a = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-    const uint32_t b = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-    uint32_t pa = a & 0x0F0F0F0Fu, pb = b & 0x0F0F0F0Fu;
-    uint32_t ha = (a >> 4) & 0x0F0F0F0Fu, hb = (b >> 4) & 0x0F0F0F0Fu;
-    pa |= pa >> 4;
-    pb |= pb >> 4;
-    ha |= ha >> 4;
-    hb |= hb >> 4;
-    hole[chunk * 64 + lane] = __builtin_amdgcn_perm(hb, ha, 0x06040200u);
-    plug[chunk * 64 + lane] = __builtin_amdgcn_perm(pb, pa, 0x06040200u);
+    for (int h = 0; h < 2; ++h) {
+        uint32_t a = glint_spread_of(v[4 * h], tab, lane_k);
+#pragma unroll
+        for (int i = 1; i < 4; ++i)
+            a |= glint_spread_of(v[4 * h + i], tab, lane_k) << (4 * i);
+        acc[h] = a;
+    }
+    hole[chunk * 64 + lane] = __builtin_amdgcn_perm(acc[1], acc[0], 0x05040100u);
+    plug[chunk * 64 + lane] = __builtin_amdgcn_perm(acc[1], acc[0], 0x07060302u);
     if ((lane & 7) == 0)
         absmax[chunk * 8 + (lane >> 3)] = s;
 }
 
-template <int UNROLL>
-__global__ __launch_bounds__(256) void k_encode_bf16_b64(const glint_u32x4 *__restrict__ w, uint32_t *__restrict__ hole,
-                                                         uint32_t *__restrict__ plug, float *__restrict__ absmax,
-                                                         int64_t nchunks) {
-    __shared__ GlintCodeEntry tab[GLINT_CODE_BUCKETS];
-    for (int i = threadIdx.x; i < GLINT_CODE_BUCKETS; i += blockDim.x)
-        tab[i] = kCodeTable[i];
-    __syncthreads();
+__global__ __launch_bounds__(ENC_THREADS) void k_encode_bf16_b64(const glint_u32x4 *__restrict__ w,
+                                                                 uint32_t *__restrict__ hole,
+                                                                 uint32_t *__restrict__ plug,
+                                                                 float *__restrict__ absmax, int64_t nchunks) {
+    __shared__ __attribute__((aligned(16))) glint_u32x4 tab[GLINT_CODE_BUCKETS * ENC_COPIES];
     const int lane = threadIdx.x & 63;
-    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
-    int64_t c0 = wave * UNROLL;
-    for (; c0 + UNROLL <= nchunks; c0 += nwaves * UNROLL) {
-        glint_u32x4 d[UNROLL];
+    /* (bucket << 7) + lane_k == byte offset of entry (bucket, lane % 8): the fma result's
+     * bits are 2^23's plus the bucket, so subtract 2^23's bits << 7 (mod 2^32) */
+    const uint32_t lane_k = (uint32_t)(lane & 7) * 16u - (GLINT_CODE_MAGIC_BITS << 7);
+    const int64_t wave = (int64_t)blockIdx.x * (ENC_THREADS / 64) + (threadIdx.x >> 6);
+    const int64_t nwaves = (int64_t)gridDim.x * (ENC_THREADS / 64);
+    int64_t c0 = wave * ENC_UNROLL;
+    glint_u32x4 d[ENC_UNROLL];
+    /* first loads go out before the table fill */
+    if (c0 + ENC_UNROLL <= nchunks) {
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u)
+        for (int u = 0; u < ENC_UNROLL; ++u)
             d[u] = __builtin_nontemporal_load(&w[(c0 + u) * 64 + lane]);
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u)
-            glint_encode_chunk(d[u], tab, c0 + u, lane, hole, plug, absmax);
     }
-    for (int64_t c = c0; c < nchunks && c < c0 + UNROLL; ++c)
-        glint_encode_chunk(w[c * 64 + lane], tab, c, lane, hole, plug, absmax);
+    glint_fill_code_lds(tab);
+    for (; c0 + ENC_UNROLL <= nchunks; c0 += nwaves * ENC_UNROLL) {
+        glint_u32x4 cur[ENC_UNROLL];
+#pragma unroll
+        for (int u = 0; u < ENC_UNROLL; ++u)
+            cur[u] = d[u];
+        const int64_t cn = c0 + nwaves * ENC_UNROLL;
+        if (cn + ENC_UNROLL <= nchunks) {
+#pragma unroll
+            for (int u = 0; u < ENC_UNROLL; ++u)
+                d[u] = __builtin_nontemporal_load(&w[(cn + u) * 64 + lane]);
+        }
+#pragma unroll
+        for (int u = 0; u < ENC_UNROLL; ++u)
+            glint_encode_chunk(cur[u], tab, lane_k, c0 + u, lane, hole, plug, absmax);
+    }
+    for (int64_t c = c0; c < nchunks && c < c0 + ENC_UNROLL; ++c)
+        glint_encode_chunk(w[c * 64 + lane], tab, lane_k, c, lane, hole, plug, absmax);
 }
 
 /* ---------------------------------------------------------------- generic encode */
@@ -210,11 +258,11 @@ static int encode_device(const T *d_w, int64_t n, int bs, uint8_t *d_hole, uint8
         glint_aligned(d_am, 4))
         n_fast = (n / 512) * 512;
     if (n_fast) {
-        constexpr int U = 4;
         const int64_t nchunks = n_fast / 512;
-        const unsigned grid = glint_grid(nchunks, 4 * U, cus * 8);
-        k_encode_bf16_b64<U><<<grid, 256, 0, st>>>((const glint_u32x4 *)d_w, (uint32_t *)d_hole, (uint32_t *)d_plug, d_am,
-                                                   nchunks);
+        const unsigned grid =
+            glint_grid(nchunks, (ENC_THREADS / 64) * ENC_UNROLL, cus * glint_resident_blocks((const void *)k_encode_bf16_b64, ENC_THREADS));
+        k_encode_bf16_b64<<<grid, ENC_THREADS, 0, st>>>((const glint_u32x4 *)d_w, (uint32_t *)d_hole,
+                                                        (uint32_t *)d_plug, d_am, nchunks);
     }
     if (n_fast < n) {
         const int64_t b0 = n_fast / bs, b1 = (n + bs - 1) / bs;
@@ -341,7 +389,8 @@ static int expand_device(const uint8_t *d_hole, const uint8_t *d_plug, const flo
         n_fast = (n / 32) * 32;
     if (n_fast) {
         const int64_t ngroups = n_fast / 32;
-        k_expand_fast<BF16><<<glint_grid(ngroups, EXPAND_THREADS * EXPAND_U, cus * 2), EXPAND_THREADS, 0, st>>>(
+        const int per_cu = glint_resident_blocks((const void *)k_expand_fast<BF16>, EXPAND_THREADS);
+        k_expand_fast<BF16><<<glint_grid(ngroups, EXPAND_THREADS * EXPAND_U, cus * per_cu), EXPAND_THREADS, 0, st>>>(
             (const glint_u32x4 *)d_hole, (const glint_u32x4 *)d_plug, d_am, d_out, ngroups, bs);
     }
     if (n_fast < n)

@@ -26,11 +26,13 @@
 #define GEMV_D 2 /* row-steps of loads in flight per wave */
 #endif
 #ifndef GEMV_T
-#define GEMV_T 512 /* threads per workgroup for K <= 8192 */
+#define GEMV_T 1024 /* threads per workgroup for K <= 8192 */
 #endif
 /* x (K f32) + the 65 KiB of tables fit in the 160 KiB of LDS */
 #define GEMV_MAX_K 16384
 #define GEMV_LDS_BYTES(K) ((size_t)(K) * 4 + 64) /* dynamic part: x as f32 + one zero chunk */
+/* x is stored as 4 planes of (K/16 + 1) float4: plane q holds floats 4q..4q+3 of every
+ * 16-element chunk, so the 64 lanes of one ds_read_b128 read 64 consecutive float4. */
 
 /* Wave task: rows [n0, n0 + R). Step i covers 16-element chunk j = 64 i + lane of every
  * row (8 B of each plane, inside one absmax block). Loads run D steps ahead in a ring of
@@ -84,13 +86,15 @@ __global__ __launch_bounds__(THREADS, 4) void k_htile_gemv_b64(const glint_u32x2
             if (d < iters)
                 gemv_load_step<R>(hole, plug, absmax, g * R, N, nch, d, lane, rh[d], rp[d], ra[d]);
     }
-    for (int i = threadIdx.x; i < (K >> 3); i += THREADS) {
+    const int xplane = nch + 1;
+    for (int i = threadIdx.x; i < (K >> 3); i += THREADS) { /* i: 8 bf16 = half a chunk */
         const glint_u32x4 v = x[i];
-        xs[2 * i] = glint_f32x4{glint_bf16lo(v.x), glint_bf16hi(v.x), glint_bf16lo(v.y), glint_bf16hi(v.y)};
-        xs[2 * i + 1] = glint_f32x4{glint_bf16lo(v.z), glint_bf16hi(v.z), glint_bf16lo(v.w), glint_bf16hi(v.w)};
+        const int jj = i >> 1, q0 = (i & 1) * 2;
+        xs[q0 * xplane + jj] = glint_f32x4{glint_bf16lo(v.x), glint_bf16hi(v.x), glint_bf16lo(v.y), glint_bf16hi(v.y)};
+        xs[(q0 + 1) * xplane + jj] = glint_f32x4{glint_bf16lo(v.z), glint_bf16hi(v.z), glint_bf16lo(v.w), glint_bf16hi(v.w)};
     }
     if (threadIdx.x < 4)
-        xs[(K >> 2) + threadIdx.x] = glint_f32x4{0.f, 0.f, 0.f, 0.f}; /* chunk nch: zeros */
+        xs[threadIdx.x * xplane + nch] = glint_f32x4{0.f, 0.f, 0.f, 0.f}; /* chunk nch: zeros */
     glint_fill_cells_lds64(ltab, stage);
 
     for (; g < ntasks; g += nwaves) {
@@ -109,7 +113,7 @@ __global__ __launch_bounds__(THREADS, 4) void k_htile_gemv_b64(const glint_u32x2
                     float xf[16];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const glint_f32x4 v = xs[4 * jc + q];
+                        const glint_f32x4 v = xs[q * xplane + jc];
                         xf[4 * q] = v.x;
                         xf[4 * q + 1] = v.y;
                         xf[4 * q + 2] = v.z;
@@ -356,6 +360,17 @@ __global__ __launch_bounds__(256) void k_htile_mfma_b64(const glint_u32x4 *__res
 }
 
 /* ------------------------------------------------------------------ dispatch */
+/* One resident wave of workgroups (every CU filled to its occupancy limit), or fewer if
+ * there are fewer wave tasks; the waves then loop over their tasks. */
+static unsigned gemv_grid(const void *kern, int threads, size_t lds, int64_t tasks) {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    const int64_t resident = (int64_t)cus * glint_resident_blocks(kern, threads, lds);
+    const int64_t needed = (tasks + threads / 64 - 1) / (threads / 64);
+    return (unsigned)(needed < resident ? needed : resident);
+}
+
 template <bool OUT_BF16>
 static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y, int M,
                         int N, int K, int bs, hipStream_t st) {
@@ -388,7 +403,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             auto kern = k_htile_gemv_b64<R, D, T, OUT_BF16>;
             if (glint_set_lds_limit((const void *)kern, lds) != 0)
                 return -3;
-            const unsigned grid = (unsigned)((tasks + T / 64 - 1) / (T / 64));
+            const unsigned grid = gemv_grid((const void *)kern, T, lds, tasks);
             kern<<<grid, T, lds, st>>>((const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax,
                                       (const glint_u32x4 *)x, y, N, K);
         } else {
@@ -396,7 +411,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             auto kern = k_htile_gemv_b64<R, D, T, OUT_BF16>;
             if (glint_set_lds_limit((const void *)kern, lds) != 0)
                 return -3;
-            const unsigned grid = (unsigned)((tasks + T / 64 - 1) / (T / 64));
+            const unsigned grid = gemv_grid((const void *)kern, T, lds, tasks);
             kern<<<grid, T, lds, st>>>((const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax,
                                       (const glint_u32x4 *)x, y, N, K);
         }
