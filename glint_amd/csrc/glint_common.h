@@ -54,6 +54,18 @@ __device__ __forceinline__ void glint_fill_cells_lds64(float *ltab, float *stage
     __syncthreads();
 }
 
+/* Same table, filled straight from the constant table: thread t writes the 16-B runs
+ * [16 w4, 16 w4 + 16) for w4 = t, t + blockDim.x, ...; a run holds 4 copies of cell
+ * w4 / 16. Ends with a barrier. */
+__device__ __forceinline__ void glint_fill_cells_lds64_direct(float *ltab) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    for (int w4 = threadIdx.x; w4 < GLINT_LDS_CELLS64_WORDS / 4; w4 += blockDim.x) {
+        const float v = (&kCells[0][0])[w4 >> 4];
+        ((f32x4 *)ltab)[w4] = f32x4{v, v, v, v};
+    }
+    __syncthreads();
+}
+
 /* Byte address of code byte K of E for the lane whose lane*4 is `lane4` (in byte 0). */
 template <int K>
 __device__ __forceinline__ uint32_t glint_cell_addr(uint32_t E, uint32_t lane4) {
@@ -118,6 +130,15 @@ __device__ __forceinline__ int glint_max8(int v) {
 }
 
 /* Sum over the 64 lanes of a wave; every lane gets the total. */
+/* Sum over each row of 16 lanes, left in every lane of the row (DPP only, no LDS). */
+__device__ __forceinline__ float glint_row16_sum(float v) {
+    v += __int_as_float(glint_dpp<GLINT_DPP_QUAD_1032>(__float_as_int(v)));
+    v += __int_as_float(glint_dpp<GLINT_DPP_QUAD_2301>(__float_as_int(v)));
+    v += __int_as_float(glint_dpp<GLINT_DPP_ROW_HALF_MIRROR>(__float_as_int(v)));
+    v += __int_as_float(glint_dpp<GLINT_DPP_ROW_MIRROR>(__float_as_int(v)));
+    return v;
+}
+
 __device__ __forceinline__ float glint_wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1)
@@ -143,6 +164,32 @@ static inline int glint_resident_blocks(const void *kernel, int threads, size_t 
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, dyn_lds) != hipSuccess || n < 1)
         n = 1;
     return n;
+}
+
+/* Workgroups of `kernel` resident on the whole current device (CUs x occupancy), computed
+ * once per (kernel, device, block size, dynamic LDS): the occupancy query costs
+ * microseconds, which a microsecond-scale decode launch cannot pay on every call. */
+static inline int64_t glint_resident_grid(const void *kernel, int threads, size_t dyn_lds) {
+    static std::mutex mu;
+    static struct { const void *k; int dev, threads; size_t lds; int64_t blocks; } seen[128];
+    static int nseen = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return 256;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (int i = 0; i < nseen; ++i)
+            if (seen[i].k == kernel && seen[i].dev == dev && seen[i].threads == threads && seen[i].lds == dyn_lds)
+                return seen[i].blocks;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
+    const int64_t blocks = (int64_t)cus * glint_resident_blocks(kernel, threads, dyn_lds);
+    std::lock_guard<std::mutex> lock(mu);
+    if (nseen < 128)
+        seen[nseen++] = {kernel, dev, threads, dyn_lds, blocks};
+    return blocks;
 }
 
 /* Raise a kernel's dynamic-LDS limit to `bytes` on the current device (needed above

@@ -53,12 +53,20 @@ __device__ __forceinline__ glint_i16x2 glint_mag_key(uint32_t d) {
 /* LDS form of the bucket table: entry b = {threshold bits, S(base), S(base + 1), 0} with
  * the "spread" code S(c) = hole | plug << 16 = (c >> 4) | (c & 15) << 16, so a lane folds
  * its 4 codes into hole nibbles (bits 0..15) and plug nibbles (bits 16..31) with one
- * shift-or each. 8 copies, entry b of copy j at byte (b * 8 + j) * 16: the 8 lanes that
- * one ds_read_b128 pass serves (lane % 8 = j) read 8 disjoint 16-byte bank groups. */
+ * shift-or each. ENC_COPIES copies, entry b of copy j at byte (b * ENC_COPIES + j) * 16,
+ * lane l reading copy l % ENC_COPIES, to spread the random lookups over the banks. */
+#ifndef ENC_COPIES
 #define ENC_COPIES 8
-#define ENC_LDS_WORDS (GLINT_CODE_BUCKETS * ENC_COPIES * 4)
+#endif
+#ifndef ENC_THREADS
 #define ENC_THREADS 1024
+#endif
+#ifndef ENC_UNROLL
 #define ENC_UNROLL 4
+#endif
+#ifndef ENC_WPE /* minimum waves per SIMD the register allocation must allow */
+#define ENC_WPE 4
+#endif
 
 __device__ __forceinline__ uint32_t glint_spread_code(uint32_t c) { return (c >> 4) | ((c & 15u) << 16); }
 
@@ -74,7 +82,7 @@ __device__ __forceinline__ void glint_fill_code_lds(glint_u32x4 *tab) {
  * constant making the byte address (bucket << 7) + lane_k land on its own copy. */
 __device__ __forceinline__ uint32_t glint_spread_of(float v, const glint_u32x4 *tab, uint32_t lane_k) {
     const float c = __builtin_amdgcn_fmed3f(v, -1.0f, 1.0f);
-    const uint32_t addr = (__float_as_uint(fmaf(c, 256.0f, GLINT_CODE_MAGIC)) << 7) + lane_k;
+    const uint32_t addr = (__float_as_uint(fmaf(c, 256.0f, GLINT_CODE_MAGIC)) * (ENC_COPIES * 16u)) + lane_k;
     const glint_u32x4 e = *(const glint_u32x4 *)((const char *)tab + addr);
     return v > __uint_as_float(e.x) ? e.z : e.y;
 }
@@ -136,15 +144,17 @@ __device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const gl
         absmax[chunk * 8 + (lane >> 3)] = s;
 }
 
-__global__ __launch_bounds__(ENC_THREADS) void k_encode_bf16_b64(const glint_u32x4 *__restrict__ w,
+__global__ __launch_bounds__(ENC_THREADS, ENC_WPE) void k_encode_bf16_b64(const glint_u32x4 *__restrict__ w,
                                                                  uint32_t *__restrict__ hole,
                                                                  uint32_t *__restrict__ plug,
                                                                  float *__restrict__ absmax, int64_t nchunks) {
     __shared__ __attribute__((aligned(16))) glint_u32x4 tab[GLINT_CODE_BUCKETS * ENC_COPIES];
     const int lane = threadIdx.x & 63;
-    /* (bucket << 7) + lane_k == byte offset of entry (bucket, lane % 8): the fma result's
-     * bits are 2^23's plus the bucket, so subtract 2^23's bits << 7 (mod 2^32) */
-    const uint32_t lane_k = (uint32_t)(lane & 7) * 16u - (GLINT_CODE_MAGIC_BITS << 7);
+    /* bucket * ENC_COPIES * 16 + lane_k == byte offset of entry (bucket, lane % ENC_COPIES):
+     * the fma result's bits are 2^23's plus the bucket, so subtract 2^23's bits times the
+     * entry stride (mod 2^32) */
+    const uint32_t lane_k =
+        (uint32_t)(lane % ENC_COPIES) * 16u - GLINT_CODE_MAGIC_BITS * (uint32_t)(ENC_COPIES * 16);
     const int64_t wave = (int64_t)blockIdx.x * (ENC_THREADS / 64) + (threadIdx.x >> 6);
     const int64_t nwaves = (int64_t)gridDim.x * (ENC_THREADS / 64);
     int64_t c0 = wave * ENC_UNROLL;
@@ -260,7 +270,7 @@ static int encode_device(const T *d_w, int64_t n, int bs, uint8_t *d_hole, uint8
     if (n_fast) {
         const int64_t nchunks = n_fast / 512;
         const unsigned grid =
-            glint_grid(nchunks, (ENC_THREADS / 64) * ENC_UNROLL, cus * glint_resident_blocks((const void *)k_encode_bf16_b64, ENC_THREADS));
+            glint_grid(nchunks, (ENC_THREADS / 64) * ENC_UNROLL, (int)glint_resident_grid((const void *)k_encode_bf16_b64, ENC_THREADS, 0));
         k_encode_bf16_b64<<<grid, ENC_THREADS, 0, st>>>((const glint_u32x4 *)d_w, (uint32_t *)d_hole,
                                                         (uint32_t *)d_plug, d_am, nchunks);
     }
@@ -281,6 +291,17 @@ static int encode_device(const T *d_w, int64_t n, int bs, uint8_t *d_hole, uint8
  * or 128 B (f32) per group. */
 #define EXPAND_THREADS 1024
 #define EXPAND_U 4
+#ifndef EXPAND_NT_STORE
+#define EXPAND_NT_STORE 0 /* 1: nontemporal output stores */
+#endif
+
+template <typename T>
+__device__ __forceinline__ void glint_store_out(T v, T *p) {
+    if (EXPAND_NT_STORE)
+        __builtin_nontemporal_store(v, p);
+    else
+        *p = v;
+}
 
 template <bool BF16>
 __device__ __forceinline__ void expand_group(const float *ltab, uint32_t lane4, glint_u32x4 hv, glint_u32x4 pv, float a,
@@ -305,7 +326,7 @@ __device__ __forceinline__ void expand_group(const float *ltab, uint32_t lane4, 
         if (a == a) {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                __builtin_nontemporal_store(
+                glint_store_out(
                     glint_u32x4{glint_pack_bf16x2(r[8 * q], r[8 * q + 1]), glint_pack_bf16x2(r[8 * q + 2], r[8 * q + 3]),
                                 glint_pack_bf16x2(r[8 * q + 4], r[8 * q + 5]), glint_pack_bf16x2(r[8 * q + 6], r[8 * q + 7])},
                     &o[q]);
@@ -318,7 +339,7 @@ __device__ __forceinline__ void expand_group(const float *ltab, uint32_t lane4, 
         glint_f32x4 *o = (glint_f32x4 *)out + g * 8;
 #pragma unroll
         for (int q = 0; q < 8; ++q)
-            __builtin_nontemporal_store(glint_f32x4{r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]}, &o[q]);
+            glint_store_out(glint_f32x4{r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]}, &o[q]);
     }
 }
 
@@ -389,8 +410,8 @@ static int expand_device(const uint8_t *d_hole, const uint8_t *d_plug, const flo
         n_fast = (n / 32) * 32;
     if (n_fast) {
         const int64_t ngroups = n_fast / 32;
-        const int per_cu = glint_resident_blocks((const void *)k_expand_fast<BF16>, EXPAND_THREADS);
-        k_expand_fast<BF16><<<glint_grid(ngroups, EXPAND_THREADS * EXPAND_U, cus * per_cu), EXPAND_THREADS, 0, st>>>(
+        const int resident = (int)glint_resident_grid((const void *)k_expand_fast<BF16>, EXPAND_THREADS, 0);
+        k_expand_fast<BF16><<<glint_grid(ngroups, EXPAND_THREADS * EXPAND_U, resident), EXPAND_THREADS, 0, st>>>(
             (const glint_u32x4 *)d_hole, (const glint_u32x4 *)d_plug, d_am, d_out, ngroups, bs);
     }
     if (n_fast < n)

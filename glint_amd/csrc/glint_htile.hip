@@ -3,13 +3,15 @@
  * y[m, n] = sum_k CELLS[h][p] * absmax[(n*K + k) / bs] * x[m, k]
  * (reference cuda/glint_htile.cu:124-164 and glint_htile_sim.py:22-50; f32 arithmetic).
  *
- * k_htile_gemv_b64 — decode (M = 1), bs = 64, K % 64 == 0: HBM-bound. A wave owns R
- *   weight rows; lane l reads 8 B of each plane per row per step (16 consecutive k inside
- *   one absmax block), so one wave load is 512 contiguous bytes, and keeps D steps of
- *   loads in flight. x is staged once per workgroup in LDS (bf16); the cell table sits in
- *   LDS as 64 lane-private copies, so lookups never conflict and each lookup address is
- *   one v_perm_b32. Per element: 0.5 op to form code bytes, 1 perm, 1 LDS read, 1 f32
- *   FMA; then one FMA by the block absmax per 16 elements and a wave reduction.
+ * k_htile_gemv_xreg — decode (M = 1), bs = 64, K % 2048 == 0 (the decode shapes): HBM-bound.
+ *   Each wave keeps a 2048-wide slice of x in registers and streams weight rows past it:
+ *   per row, lane l reads 16 B of each nibble plane (32 consecutive k inside one absmax
+ *   block), so a wave load is 1 KiB contiguous; rows are multi-buffered in registers. The
+ *   cell table sits in LDS as 64 lane-private copies, so lookups never conflict and each
+ *   lookup address is one v_perm_b32. Per element: 0.5 op to form code bytes, 1 perm, 1 LDS
+ *   read, 1 f32 FMA; per row one FMA by the block absmax and 4 DPP adds.
+ * k_htile_gemv_b64 — decode for the other K % 64 == 0: x staged in LDS as f32 planes,
+ *   (task, step) items double-buffered in registers.
  * k_htile_mfma_b64 — prefill (M > 1, bf16 out, bs = 64): BF16 MFMA on LDS-dequantized
  *   weight tiles, f32 accumulation.
  * k_htile_generic — every other shape (any M, K, bs, alignment): 64x32 output tiles,
@@ -20,147 +22,313 @@
 
 /* ---------------------------------------------------------------- GEMV (M = 1) */
 #ifndef GEMV_R
-#define GEMV_R 2 /* weight rows per wave */
+#define GEMV_R 1 /* weight rows per wave task */
 #endif
 #ifndef GEMV_D
-#define GEMV_D 2 /* row-steps of loads in flight per wave */
+#define GEMV_D 1 /* groups of (task, step) items per register buffer (two buffers) */
 #endif
 #ifndef GEMV_T
-#define GEMV_T 1024 /* threads per workgroup for K <= 8192 */
+#define GEMV_T 1024 /* threads per workgroup */
+#endif
+#ifndef GEMV_WPE
+#define GEMV_WPE 4 /* minimum waves per SIMD the register allocation must allow */
 #endif
 /* x (K f32) + the 65 KiB of tables fit in the 160 KiB of LDS */
 #define GEMV_MAX_K 16384
-#define GEMV_LDS_BYTES(K) ((size_t)(K) * 4 + 64) /* dynamic part: x as f32 + one zero chunk */
-/* x is stored as 4 planes of (K/16 + 1) float4: plane q holds floats 4q..4q+3 of every
- * 16-element chunk, so the 64 lanes of one ds_read_b128 read 64 consecutive float4. */
+#define GEMV_LDS_BYTES(K) ((size_t)(K) * 4 + 128) /* dynamic part: x as f32 + one zero chunk */
+/* x is stored as 8 planes of (K/32 + 1) float4: plane q holds floats 4q..4q+3 of every
+ * 32-element chunk, so the 64 lanes of one ds_read_b128 read 64 consecutive float4. */
 
-/* Wave task: rows [n0, n0 + R). Step i covers 16-element chunk j = 64 i + lane of every
- * row (8 B of each plane, inside one absmax block). Loads run D steps ahead in a ring of
- * registers (slot d holds steps d, d + D, ...), issued for the first task before the
- * LDS tables are filled. */
+struct GemvItem {
+    glint_u32x4 h, p; /* 32 packed elements of each plane */
+    float a;
+};
+
+/* Loads of work item t of this wave: task g = g0 + (t / steps) * nwaves, step t % steps;
+ * R rows per task. Lanes past the row end read the row's last chunk with absmax 0 and the
+ * zero x chunk; rows past N reuse row N-1 (their sums are not stored). */
 template <int R>
-__device__ __forceinline__ void gemv_load_step(const glint_u32x2 *__restrict__ hole, const glint_u32x2 *__restrict__ plug,
-                                               const float *__restrict__ absmax, int n0, int N, int nch, int it,
-                                               int lane, glint_u32x2 (&h)[R], glint_u32x2 (&p)[R], float (&a)[R]) {
-    /* unconditional loads: a lane past the row end reads the row's last chunk, gets
-     * absmax 0 and x = 0, so it adds exactly 0 */
-    const int jr = it * 64 + lane;
-    const bool ok = jr < nch;
+__device__ __forceinline__ void gemv_load_item(const glint_u32x4 *__restrict__ hole, const glint_u32x4 *__restrict__ plug,
+                                               const float *__restrict__ absmax, int N, int nch, int steps, int g0,
+                                               int nwaves, int nitems_max, int t, int lane, GemvItem (&it)[R]) {
+    t = min(t, nitems_max); /* past the end: reload the last item, whose result is unused */
+    const int task = g0 + (t / steps) * nwaves;
+    const int jr = (t % steps) * 64 + lane;
     const uint32_t j = (uint32_t)min(jr, nch - 1);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        /* row base: wave-uniform (scalar) arithmetic; rows past N reuse row N-1 */
-        const int64_t n = min(n0 + r, N - 1);
-        h[r] = __builtin_nontemporal_load(hole + n * nch + j);
-        p[r] = __builtin_nontemporal_load(plug + n * nch + j);
-        const float av = absmax[n * (nch >> 2) + (j >> 2)];
-        a[r] = ok ? av : 0.0f;
+        const int64_t n = min(task * R + r, N - 1);
+        it[r].h = __builtin_nontemporal_load(hole + n * nch + j);
+        it[r].p = __builtin_nontemporal_load(plug + n * nch + j);
+        it[r].a = absmax[n * (nch >> 1) + (j >> 1)]; /* lanes past the row end: masked at use */
     }
 }
 
+/* One wave runs tasks g0, g0 + nwaves, ...; each task is `steps` items (lane l of step s
+ * covers elements [32 (64 s + l), +32) of each of its R rows). Items are double-buffered
+ * in groups of D across task boundaries; the first group goes out before the LDS fill. */
 template <int R, int D, int THREADS, bool OUT_BF16>
-__global__ __launch_bounds__(THREADS, 4) void k_htile_gemv_b64(const glint_u32x2 *__restrict__ hole,
-                                                               const glint_u32x2 *__restrict__ plug,
-                                                               const float *__restrict__ absmax,
-                                                               const glint_u32x4 *__restrict__ x, void *__restrict__ y,
-                                                               int N, int K) {
+__global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glint_u32x4 *__restrict__ hole,
+                                                                      const glint_u32x4 *__restrict__ plug,
+                                                                      const float *__restrict__ absmax,
+                                                                      const glint_u32x4 *__restrict__ x,
+                                                                      void *__restrict__ y, int N, int K) {
     __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS]; /* 64 KiB at LDS offset 0 */
     __shared__ float stage[256];
-    extern __shared__ __attribute__((aligned(16))) glint_f32x4 xs[]; /* K f32 */
+    extern __shared__ __attribute__((aligned(16))) glint_f32x4 xs[]; /* K f32, 8 planes */
 
     const int lane = threadIdx.x & 63;
     const uint32_t lane4 = (uint32_t)lane * 4u;
-    const int nch = K >> 4;
-    const int iters = (nch + 63) >> 6;
+    const int nch = K >> 5;                 /* 32-element chunks per row */
+    const int steps = (nch + 63) >> 6;
     const int wpb = THREADS / 64;
     const int nwaves = gridDim.x * wpb;
-    /* wave-uniform task index, so row arithmetic stays in scalar registers */
-    int g = blockIdx.x * wpb + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ntasks = (N + R - 1) / R;
+    /* wave-uniform, so task and row arithmetic stays in scalar registers */
+    const int g0 = blockIdx.x * wpb + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int my_tasks = g0 < ntasks ? (ntasks - g0 + nwaves - 1) / nwaves : 0;
+    const int nitems = my_tasks * steps;
 
-    glint_u32x2 rh[D][R], rp[D][R];
-    float ra[D][R];
-    if (g < ntasks) {
+    /* two register buffers of D items: while one is computed, the other's loads are in
+     * flight; the loop is unrolled by 2 so the buffers never move (a loop-carried ring
+     * would make the compiler wait for every outstanding load at the loop head) */
+    GemvItem buf_a[D][R], buf_b[D][R];
+    const int tmax = max(nitems - 1, 0);
 #pragma unroll
-        for (int d = 0; d < D; ++d)
-            if (d < iters)
-                gemv_load_step<R>(hole, plug, absmax, g * R, N, nch, d, lane, rh[d], rp[d], ra[d]);
-    }
+    for (int d = 0; d < D; ++d)
+        gemv_load_item<R>(hole, plug, absmax, N, nch, steps, g0, nwaves, tmax, d, lane, buf_a[d]);
+
     const int xplane = nch + 1;
-    for (int i = threadIdx.x; i < (K >> 3); i += THREADS) { /* i: 8 bf16 = half a chunk */
+    for (int i = threadIdx.x; i < (K >> 3); i += THREADS) { /* i: 8 bf16 = a quarter chunk */
         const glint_u32x4 v = x[i];
-        const int jj = i >> 1, q0 = (i & 1) * 2;
+        const int jj = i >> 2, q0 = (i & 3) * 2;
         xs[q0 * xplane + jj] = glint_f32x4{glint_bf16lo(v.x), glint_bf16hi(v.x), glint_bf16lo(v.y), glint_bf16hi(v.y)};
         xs[(q0 + 1) * xplane + jj] = glint_f32x4{glint_bf16lo(v.z), glint_bf16hi(v.z), glint_bf16lo(v.w), glint_bf16hi(v.w)};
     }
-    if (threadIdx.x < 4)
+    if (threadIdx.x < 8)
         xs[threadIdx.x * xplane + nch] = glint_f32x4{0.f, 0.f, 0.f, 0.f}; /* chunk nch: zeros */
     glint_fill_cells_lds64(ltab, stage);
 
-    for (; g < ntasks; g += nwaves) {
-        const int n0 = g * R;
-        float acc[R];
+    float acc[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            acc[r] = 0.0f;
-        for (int base = 0; base < iters; base += D) {
+    for (int r = 0; r < R; ++r)
+        acc[r] = 0.0f;
+
+    auto compute_item = [&](int t, const GemvItem (&item)[R]) {
+        const int step = t % steps;
+        const int jc = min(step * 64 + lane, nch);
 #pragma unroll
-            for (int d = 0; d < D; ++d) {
-                const int it = base + d;
-                if (it < iters) {
-                    /* x of chunk j; lanes past the row end read the zero chunk */
-                    const int jc = min(it * 64 + lane, nch);
-                    float xf[16];
+        for (int r = 0; r < R; ++r) {
+            float part = 0.0f;
+            const uint32_t H[4] = {item[r].h.x, item[r].h.y, item[r].h.z, item[r].h.w};
+            const uint32_t P[4] = {item[r].p.x, item[r].p.y, item[r].p.z, item[r].p.w};
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const glint_f32x4 v = xs[q * xplane + jc];
-                        xf[4 * q] = v.x;
-                        xf[4 * q + 1] = v.y;
-                        xf[4 * q + 2] = v.z;
-                        xf[4 * q + 3] = v.w;
-                    }
+            for (int q = 0; q < 4; ++q) {
+                const glint_f32x4 xa = xs[(2 * q) * xplane + jc];
+                const glint_f32x4 xb = xs[(2 * q + 1) * xplane + jc];
+                const uint32_t E = glint_codes_even(H[q], P[q]);
+                const uint32_t O = glint_codes_odd(H[q], P[q]);
+                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)), xa.x, part);
+                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)), xa.y, part);
+                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)), xa.z, part);
+                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)), xa.w, part);
+                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)), xb.x, part);
+                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)), xb.y, part);
+                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)), xb.z, part);
+                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)), xb.w, part);
+                /* at most 8 lookups in flight per wave: bounds live registers */
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            acc[r] = fmaf(jc < nch ? item[r].a : 0.0f, part, acc[r]);
+        }
+        if (step == steps - 1) { /* task done: reduce its rows and store */
+            const int n0 = (g0 + (t / steps) * nwaves) * R;
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float part = 0.0f;
-                        const uint32_t H[2] = {rh[d][r].x, rh[d][r].y}, P[2] = {rp[d][r].x, rp[d][r].y};
-#pragma unroll
-                        for (int q = 0; q < 2; ++q) {
-                            const uint32_t E = glint_codes_even(H[q], P[q]);
-                            const uint32_t O = glint_codes_odd(H[q], P[q]);
-                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)), xf[8 * q + 0], part);
-                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)), xf[8 * q + 1], part);
-                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)), xf[8 * q + 2], part);
-                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)), xf[8 * q + 3], part);
-                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)), xf[8 * q + 4], part);
-                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)), xf[8 * q + 5], part);
-                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)), xf[8 * q + 6], part);
-                            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)), xf[8 * q + 7], part);
-                        }
-                        acc[r] = fmaf(ra[d][r], part, acc[r]);
-                        /* keep the next row's lookups after this row's FMAs: bounds live registers */
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                    if (it + D < iters)
-                        gemv_load_step<R>(hole, plug, absmax, n0, N, nch, it + D, lane, rh[d], rp[d], ra[d]);
+            for (int r = 0; r < R; ++r) {
+                const float sum = glint_wave_sum(acc[r]);
+                acc[r] = 0.0f;
+                if (lane == r && n0 + r < N) {
+                    if (OUT_BF16)
+                        ((uint16_t *)y)[n0 + r] = glint_f32_to_bf16(sum);
+                    else
+                        ((float *)y)[n0 + r] = sum;
                 }
             }
         }
+    };
+
+    /* full rounds: every compute is unconditional, so at the loop head the only loads in
+     * flight are the ones the next compute needs last (the wait counter can count them) */
+    int base = 0;
+    for (; base + 2 * D <= nitems; base += 2 * D) {
+        /* loads are unconditional (clamped): no branch hides them from the wait counter */
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float t = glint_wave_sum(acc[r]);
-            if (lane == r && n0 + r < N) {
-                if (OUT_BF16)
-                    ((uint16_t *)y)[n0 + r] = glint_f32_to_bf16(t);
-                else
-                    ((float *)y)[n0 + r] = t;
-            }
-        }
-        if (g + nwaves < ntasks) {
+        for (int d = 0; d < D; ++d)
+            gemv_load_item<R>(hole, plug, absmax, N, nch, steps, g0, nwaves, tmax, base + D + d, lane, buf_b[d]);
 #pragma unroll
-            for (int d = 0; d < D; ++d)
-                if (d < iters)
-                    gemv_load_step<R>(hole, plug, absmax, (g + nwaves) * R, N, nch, d, lane, rh[d], rp[d], ra[d]);
+        for (int d = 0; d < D; ++d)
+            compute_item(base + d, buf_a[d]);
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            gemv_load_item<R>(hole, plug, absmax, N, nch, steps, g0, nwaves, tmax, base + 2 * D + d, lane, buf_a[d]);
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            compute_item(base + D + d, buf_b[d]);
+    }
+    if (base < nitems) { /* fewer than 2 D items left; buf_a holds items base .. base + D - 1 */
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            gemv_load_item<R>(hole, plug, absmax, N, nch, steps, g0, nwaves, tmax, base + D + d, lane, buf_b[d]);
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (base + d < nitems)
+                compute_item(base + d, buf_a[d]);
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (base + D + d < nitems)
+                compute_item(base + D + d, buf_b[d]);
+    }
+}
+
+/* ------------------------------------------------ GEMV with x in registers */
+/* For K a multiple of 2048 (every K of the decode shapes): the row is cut into S = K/2048
+ * slices of 64 chunks of 32 elements. Wave (s, g) of a workgroup holds slice s of x in
+ * registers (lane l: the 32 f32 of chunk 64 s + l) and runs rows r0 + g, r0 + g + G, ...
+ * of the workgroup's row range; LDS then serves only the cell lookups. Per row a wave
+ * loads 1 KiB of each plane (16 B per lane) plus the 32 block scales, rows double-buffered
+ * in registers; its partial sum is folded to 4 row-of-16 sums by DPP and parked in LDS,
+ * and after one barrier the workgroup adds the 4 S partials of each row in a fixed order. */
+#ifndef GEMV_X_THREADS
+#define GEMV_X_THREADS 512 /* most threads per workgroup (whole waves of S slices are used) */
+#endif
+#ifndef GEMV_X_DEPTH
+#define GEMV_X_DEPTH 3 /* rows of loads in flight per wave */
+#endif
+#ifndef GEMV_X_BATCH
+#define GEMV_X_BATCH 2 /* groups of 8 cell lookups a wave may have in flight (1, 2 or 4) */
+#endif
+#define GEMV_X_RED_MAX 4096 /* floats of per-row partials a workgroup may park in LDS */
+
+struct GemvRow {
+    glint_u32x4 h, p;
+    float a;
+};
+
+__device__ __forceinline__ void gemv_x_load(const glint_u32x4 *__restrict__ hole, const glint_u32x4 *__restrict__ plug,
+                                            const float *__restrict__ absmax, int64_t n, int nch, uint32_t j,
+                                            GemvRow &row) {
+    row.h = __builtin_nontemporal_load(hole + n * nch + j);
+    row.p = __builtin_nontemporal_load(plug + n * nch + j);
+    row.a = absmax[n * (nch >> 1) + (j >> 1)];
+}
+
+template <bool OUT_BF16>
+__global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_xreg(
+    const glint_u32x4 *__restrict__ hole, const glint_u32x4 *__restrict__ plug, const float *__restrict__ absmax,
+    const glint_u32x4 *__restrict__ x, void *__restrict__ y, int N, int K, int G, int rows_per_wg) {
+    __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS]; /* 64 KiB at LDS offset 0 */
+    extern __shared__ float red[];                                              /* [rows_per_wg][S][4] */
+
+    const int lane = threadIdx.x & 63;
+    const uint32_t lane4 = (uint32_t)lane * 4u;
+    const int nch = K >> 5, S = nch >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int s = w % S, g = w / S;
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int nrows = max(min(rows_per_wg, N - r0), 0);
+    const int my = g < nrows ? (nrows - g + G - 1) / G : 0; /* rows r0 + g + i G, i < my */
+    const uint32_t j = (uint32_t)(s * 64 + lane);
+    /* row of item i, clamped into the matrix (a clamped reload is never used) */
+    auto row_of = [&](int i) -> int64_t { return (int64_t)min(r0 + g + min(i, max(my - 1, 0)) * G, N - 1); };
+
+    /* Loads go out in the order they are consumed (the wait counter is in order): the
+     * cell table, x, then the first two rows. 8 runs per thread cover the 4096 16-B runs
+     * of the table when blockDim >= 512; a loop after them covers smaller blocks. */
+    /* run indices past 4095 are clamped: those threads rewrite run 4095 with its own value */
+    float cv[8];
+    int w4[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        w4[k] = min((int)threadIdx.x + k * (int)blockDim.x, 4095);
+        cv[k] = (&kCells[0][0])[w4[k] >> 4];
+    }
+    glint_u32x4 xv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        xv[q] = x[j * 4 + q];
+    __builtin_amdgcn_sched_barrier(0);
+    GemvRow buf[GEMV_X_DEPTH];
+#pragma unroll
+    for (int d = 0; d < GEMV_X_DEPTH; ++d)
+        gemv_x_load(hole, plug, absmax, row_of(d), nch, j, buf[d]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        ((glint_f32x4 *)ltab)[w4[k]] = glint_f32x4{cv[k], cv[k], cv[k], cv[k]};
+    for (int r = threadIdx.x + 8 * blockDim.x; r < 4096; r += blockDim.x) { /* blockDim < 512 only */
+        const float v = (&kCells[0][0])[r >> 4];
+        ((glint_f32x4 *)ltab)[r] = glint_f32x4{v, v, v, v};
+    }
+    float xr[32];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const glint_u32x4 v = xv[q];
+        xr[8 * q + 0] = glint_bf16lo(v.x); xr[8 * q + 1] = glint_bf16hi(v.x);
+        xr[8 * q + 2] = glint_bf16lo(v.y); xr[8 * q + 3] = glint_bf16hi(v.y);
+        xr[8 * q + 4] = glint_bf16lo(v.z); xr[8 * q + 5] = glint_bf16hi(v.z);
+        xr[8 * q + 6] = glint_bf16lo(v.w); xr[8 * q + 7] = glint_bf16hi(v.w);
+    }
+    __syncthreads();
+
+    auto compute_row = [&](int i, const GemvRow &row) {
+        float part = 0.0f;
+        const uint32_t H[4] = {row.h.x, row.h.y, row.h.z, row.h.w};
+        const uint32_t P[4] = {row.p.x, row.p.y, row.p.z, row.p.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t E = glint_codes_even(H[q], P[q]);
+            const uint32_t O = glint_codes_odd(H[q], P[q]);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)), xr[8 * q + 0], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)), xr[8 * q + 1], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)), xr[8 * q + 2], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)), xr[8 * q + 3], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)), xr[8 * q + 4], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)), xr[8 * q + 5], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)), xr[8 * q + 6], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)), xr[8 * q + 7], part);
+            /* at most 8 GEMV_X_BATCH lookups in flight per wave: bounds live registers */
+            if ((q + 1) % GEMV_X_BATCH == 0)
+                __builtin_amdgcn_sched_barrier(0);
         }
+        const float v = glint_row16_sum(row.a * part);
+        if ((lane & 15) == 0)
+            red[((g + i * G) * S + s) * 4 + (lane >> 4)] = v;
+    };
+
+    /* rows i .. i + DEPTH - 1 are in flight at the top of each round; full rounds keep
+     * every compute unconditional, so the wait counter can count the loads in flight */
+    int i = 0;
+    for (; i + GEMV_X_DEPTH <= my; i += GEMV_X_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < GEMV_X_DEPTH; ++d) {
+            compute_row(i + d, buf[d]);
+            gemv_x_load(hole, plug, absmax, row_of(i + d + GEMV_X_DEPTH), nch, j, buf[d]);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < GEMV_X_DEPTH - 1; ++d)
+        if (i + d < my)
+            compute_row(i + d, buf[d]);
+    __syncthreads();
+
+    for (int t = threadIdx.x; t < nrows; t += blockDim.x) {
+        float sum = 0.0f;
+        for (int k = 0; k < S * 4; ++k)
+            sum += red[t * S * 4 + k];
+        if (OUT_BF16)
+            ((uint16_t *)y)[r0 + t] = glint_f32_to_bf16(sum);
+        else
+            ((float *)y)[r0 + t] = sum;
     }
 }
 
@@ -363,10 +531,7 @@ __global__ __launch_bounds__(256) void k_htile_mfma_b64(const glint_u32x4 *__res
 /* One resident wave of workgroups (every CU filled to its occupancy limit), or fewer if
  * there are fewer wave tasks; the waves then loop over their tasks. */
 static unsigned gemv_grid(const void *kern, int threads, size_t lds, int64_t tasks) {
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        cus = 256;
-    const int64_t resident = (int64_t)cus * glint_resident_blocks(kern, threads, lds);
+    const int64_t resident = glint_resident_grid(kern, threads, lds);
     const int64_t needed = (tasks + threads / 64 - 1) / (threads / 64);
     return (unsigned)(needed < resident ? needed : resident);
 }
@@ -380,7 +545,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         return -2;
     if (M <= 0 || N <= 0)
         return 0;
-    const bool gemv_ok = M == 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 8) && glint_aligned(plug, 8) &&
+    const bool gemv_ok = M == 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
                          glint_aligned(absmax, 4) && glint_aligned(x, 16) &&
                          K <= GEMV_MAX_K;
     const bool mfma_ok = OUT_BF16 && M > 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) &&
@@ -394,6 +559,21 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             k_htile_mfma_b64<128><<<dim3(gx, (M + 127) / 128), 256, 0, st>>>(
                 (const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
         }
+    } else if (gemv_ok && (K % 2048) == 0 && K / 2048 <= GEMV_X_THREADS / 64) {
+        const int S = K / 2048, G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
+        auto kern = k_htile_gemv_xreg<OUT_BF16>;
+        const int64_t resident = glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4);
+        const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
+        int64_t rows_per_wg = G * per_wave;
+        const int64_t cap = (GEMV_X_RED_MAX / (S * 4)) / G * G;
+        if (rows_per_wg > cap)
+            rows_per_wg = cap;
+        const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
+        const size_t lds = (size_t)rows_per_wg * S * 4 * sizeof(float);
+        if (glint_set_lds_limit((const void *)kern, GEMV_X_RED_MAX * 4) != 0)
+            return -3;
+        kern<<<grid, threads, lds, st>>>((const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax,
+                                         (const glint_u32x4 *)x, y, N, K, G, (int)rows_per_wg);
     } else if (gemv_ok) {
         constexpr int R = GEMV_R, D = GEMV_D;
         const size_t lds = GEMV_LDS_BYTES(K);
@@ -404,7 +584,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             if (glint_set_lds_limit((const void *)kern, lds) != 0)
                 return -3;
             const unsigned grid = gemv_grid((const void *)kern, T, lds, tasks);
-            kern<<<grid, T, lds, st>>>((const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax,
+            kern<<<grid, T, lds, st>>>((const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax,
                                       (const glint_u32x4 *)x, y, N, K);
         } else {
             constexpr int T = 1024;
@@ -412,7 +592,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             if (glint_set_lds_limit((const void *)kern, lds) != 0)
                 return -3;
             const unsigned grid = gemv_grid((const void *)kern, T, lds, tasks);
-            kern<<<grid, T, lds, st>>>((const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax,
+            kern<<<grid, T, lds, st>>>((const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax,
                                       (const glint_u32x4 *)x, y, N, K);
         }
     } else {

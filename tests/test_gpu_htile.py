@@ -82,7 +82,8 @@ def _encoded_weight(oracle, N, K, seed, bs=64):
     return H.encode_bf16(w, bs)
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336), (100, 64), (3, 1088), (129, 2048)])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336), (100, 64), (3, 1088), (129, 2048), (1, 2048),
+                                 (7, 6144), (1000, 12288), (17, 16384), (4097, 8192)])
 def test_gemv_fast_path_vs_float64(oracle, N, K):
     torch = torch_cuda()
     hole, plug, am = _encoded_weight(oracle, N, K, 2002)
