@@ -53,11 +53,38 @@ def timed(torch, fns, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / steps
 
 
+def bound(fn, *args):
+    """A zero-argument call of the C-ABI function `fn` with its arguments converted once
+    (tensors to device pointers, ints to C ints), so the timed loop pays only the ctypes
+    call and the launch, not Python tensor bookkeeping. Raises on a non-zero return."""
+    import ctypes
+    conv = []
+    for a in args:
+        if hasattr(a, "data_ptr"):
+            conv.append(ctypes.c_void_p(a.data_ptr()))
+        elif isinstance(a, ctypes.c_void_p):
+            conv.append(a)
+        else:
+            conv.append(a)
+    conv = tuple(conv)
+
+    def call():
+        rc = fn(*conv)
+        if rc != 0:
+            raise RuntimeError(f"{fn.__name__} rc={rc}")
+    return call
+
+
+def stream_handle(torch):
+    import ctypes
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
 def gemv_bytes(N: int, K: int, out_bytes: int = 2) -> float:
     return N * K * (1 + 4 / 64) + 2 * K + out_bytes * N
 
 
-def bench_gemv(torch, H, steps, warmup):
+def bench_gemv(torch, H, steps, warmup, headline_only=False):
     N, K = GEMV_N, GEMV_K
     per = gemv_bytes(N, K)
     copies = max(17, int(1.05 * 2 ** 30 / per) + 1)
@@ -70,10 +97,13 @@ def bench_gemv(torch, H, steps, warmup):
     gx = torch.Generator(device="cuda").manual_seed(2001)
     x = torch.randn(K, device="cuda", generator=gx).to(torch.bfloat16)
     y = torch.empty(N, dtype=torch.bfloat16, device="cuda")
-    fns = [lambda p=p: H.htile_bf16(p[0], p[1], p[2], x, N, K, 64, out=y) for p in pins]
+    lib, st = H.encode_lib(), stream_handle(torch)
+    fns = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, y, 1, N, K, 64, st) for p in pins]
     ms = timed(torch, fns, steps, warmup)
+    if headline_only:
+        return {"ms": ms, "bytes": per, "gbs": per / ms / 1e6, "copies": copies, "rotation_bytes": copies * per}, pins, x
     yf = torch.empty(N, dtype=torch.float32, device="cuda")
-    fns32 = [lambda p=p: H.htile_f32(p[0], p[1], p[2], x, N, K, 64, out=yf) for p in pins]
+    fns32 = [bound(lib.launch_glint_htile_s3_f32_stream, p[0], p[1], p[2], x, yf, 1, N, K, 64, st) for p in pins]
     ms32 = timed(torch, fns32, steps, warmup)
     # W_down shape: N=4096, K=14336
     pins_d = []
@@ -84,7 +114,7 @@ def bench_gemv(torch, H, steps, warmup):
         del w
     xd = torch.randn(14336, device="cuda", generator=gx).to(torch.bfloat16)
     yd = torch.empty(4096, dtype=torch.bfloat16, device="cuda")
-    fnsd = [lambda p=p: H.htile_bf16(p[0], p[1], p[2], xd, 4096, 14336, 64, out=yd) for p in pins_d]
+    fnsd = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], xd, yd, 1, 4096, 14336, 64, st) for p in pins_d]
     msd = timed(torch, fnsd, steps, warmup)
     del pins_d
     return {
@@ -116,14 +146,20 @@ def bench_model_encode(torch, H, passes: int):
         pins.append((torch.empty((n + 1) // 2, dtype=torch.uint8, device="cuda"),
                      torch.empty((n + 1) // 2, dtype=torch.uint8, device="cuda"),
                      torch.empty((n + 63) // 64, dtype=torch.float32, device="cuda")))
-    enc = lambda: [H.encode_bf16(w, 64, out=p) for w, p in zip(ws, pins)]
+    lib, st = H.encode_lib(), stream_handle(torch)
+    enc_calls = [bound(lib.glint_encode_bf16_device, w, w.numel(), 64, p[0], p[1], p[2], st) for w, p in zip(ws, pins)]
+    enc = lambda: [c() for c in enc_calls]
     ms_enc = timed(torch, [enc], passes, 1)
+    del enc_calls, enc
     del ws
     torch.cuda.empty_cache()
     outs = [torch.empty(p[0].numel() * 2, dtype=torch.bfloat16, device="cuda") for p in pins]
     ns = [a * b for a, b in shapes]
-    exp = lambda: [H.expand_bf16(p[0], p[1], p[2], n, 64, out=o) for p, n, o in zip(pins, ns, outs)]
+    exp_calls = [bound(lib.glint_expand_packed_to_bf16_device, p[0], p[1], p[2], n, 64, o, st)
+                 for p, n, o in zip(pins, ns, outs)]
+    exp = lambda: [c() for c in exp_calls]
     ms_exp = timed(torch, [exp], passes, 1)
+    del exp_calls, exp
     del outs, pins
     torch.cuda.empty_cache()
     b = 3.0625 * total
@@ -132,6 +168,44 @@ def bench_model_encode(torch, H, passes: int):
         "encode_ms": ms_enc, "encode_bf16_in_gbs": 2 * total / ms_enc / 1e6,
         "encode_hbm_gbs": b / ms_enc / 1e6, "encode_frac": b / ms_enc / 1e6 / HBM_PEAK_GBS,
         "expand_bf16_ms": ms_exp, "expand_hbm_gbs": b / ms_exp / 1e6, "expand_frac": b / ms_exp / 1e6 / HBM_PEAK_GBS,
+    }
+
+
+def bench_host_abi(H, reps: int = 5):
+    """The reference's host-pointer ABI (glint_encode_bf16_host, expand to f32 / BF16 host)
+    on the 4096x4096 CPU-reference config: pageable host buffers in and out, so every call
+    pays H2D + kernel + D2H over PCIe. Reported apart from the device-resident rates."""
+    import ctypes
+    import numpy as np
+    lib = H.encode_lib()
+    rng = np.random.default_rng(1001)
+    n = 4096 * 4096
+    w = rng.normal(0.0, 0.02, n).astype(np.float32)
+    w[rng.choice(n, n // 1000, replace=False)] *= np.float32(10.0)
+    u = w.view(np.uint32)
+    u16 = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    hole = np.empty((n + 1) // 2, np.uint8)
+    plug = np.empty_like(hole)
+    am = np.empty((n + 63) // 64, np.float32)
+    out32 = np.empty(n, np.float32)
+    out16 = np.empty(n, np.uint16)
+    P = lambda a: ctypes.c_void_p(a.ctypes.data)
+
+    def per_call(fn):
+        assert fn() == 0
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            assert fn() == 0
+        return (time.perf_counter() - t0) / reps
+
+    enc = per_call(lambda: lib.glint_encode_bf16_host(P(u16), n, 64, P(hole), P(plug), P(am)))
+    e32 = per_call(lambda: lib.glint_expand_packed_to_f32_host(P(hole), P(plug), P(am), n, 64, P(out32)))
+    e16 = per_call(lambda: lib.glint_expand_packed_to_bf16_host(P(hole), P(plug), P(am), n, 64, P(out16)))
+    return {
+        "config": "4096x4096 BF16, seed 1001, 0.1% outliers, bs 64; pageable host buffers",
+        "encode_ms": enc * 1e3, "encode_bf16_in_gbs": 2 * n / enc / 1e9,
+        "expand_f32_ms": e32 * 1e3, "expand_f32_out_gbs": 4 * n / e32 / 1e9,
+        "expand_bf16_ms": e16 * 1e3, "expand_bf16_out_gbs": 2 * n / e16 / 1e9,
     }
 
 
@@ -169,42 +243,124 @@ def bench_int8(torch, H, steps: int):
     return {"ms": ms, "tops": ops / ms / 1e9, "mfma_frac": ops / ms / 1e9 / I8_PEAK_TOPS, "shape": [M, N, K]}
 
 
-def cpu_baseline(seconds_target: float = 10.0):
-    """The repo's numpy restatement of the reference host path (glint_np: encode_f32,
-    expand, x @ W^T) on a bounded sample of the same workload, single process."""
+def cpu_baseline(seconds_target: float = 20.0):
+    """The CPU path beside the GPU, on this host: the repo's C restatement of the reference
+    host path (oracle/glint_oracle.c, OpenMP over the threads it reports) running the
+    headline GEMV (expand-on-the-fly H-TILE, f32 accumulate) at full size, and encoding the
+    CPU-reference configuration (4096x4096, seed 1001, 0.1% outliers x10). Also the numpy
+    restatement (one core) on a 256-row sample. Each leg is repeated for a bounded time."""
     import numpy as np
     from oracle import glint_oracle as G
-    rng = np.random.default_rng(2002)
-    K = GEMV_K
-    rows = 256
-    w = rng.normal(0, 0.02, rows * K).astype(np.float32)
+    orc = G.Oracle()
+    N, K = GEMV_N, GEMV_K
+    w = np.random.default_rng(2002).normal(0.0, 0.02, N * K).astype(np.float32)
     u16 = G.f32_to_bf16_bits(w)
-    hole, plug, am = G.encode_bf16(u16, 64)
-    x = G.bf16_bits_to_f32(G.f32_to_bf16_bits(rng.normal(0, 1, K).astype(np.float32)))
-    t0 = time.perf_counter()
-    reps = 0
-    while time.perf_counter() - t0 < seconds_target / 2:
-        W = G.expand(hole, plug, am, rows * K, 64).reshape(rows, K)
-        _ = W @ x
-        reps += 1
-    gemv_s = (time.perf_counter() - t0) / reps
-    gemv_gbs = gemv_bytes(rows, K) / gemv_s / 1e9
-    t0 = time.perf_counter()
-    reps = 0
-    while time.perf_counter() - t0 < seconds_target / 2:
-        G.encode_bf16(u16, 64)
-        reps += 1
-    enc_s = (time.perf_counter() - t0) / reps
+    del w
+    hole, plug, am = orc.encode_bf16(u16, 64)
+    x = G.f32_to_bf16_bits(np.random.default_rng(2001).normal(0.0, 1.0, K).astype(np.float32))
+
+    def rate(fn, budget):
+        fn()
+        t0, reps = time.perf_counter(), 0
+        while time.perf_counter() - t0 < budget:
+            fn()
+            reps += 1
+        return (time.perf_counter() - t0) / reps, reps
+
+    gemv_s, gemv_reps = rate(lambda: orc.htile_f32(hole, plug, am, x, 1, N, K, 64), seconds_target * 0.4)
+    rng = np.random.default_rng(1001)
+    n0 = 4096 * 4096
+    w0 = rng.normal(0.0, 0.02, n0).astype(np.float32)
+    w0[rng.choice(n0, n0 // 1000, replace=False)] *= np.float32(10.0)
+    u0 = G.f32_to_bf16_bits(w0)
+    enc_s, enc_reps = rate(lambda: orc.encode_bf16(u0, 64), seconds_target * 0.3)
+    rows = 256
+    hs, ps, ams = hole[:rows * K // 2], plug[:rows * K // 2], am[:rows * K // 64]
+    xf = G.bf16_bits_to_f32(x)
+    np_s, np_reps = rate(lambda: G.expand(hs, ps, ams, rows * K, 64).reshape(rows, K) @ xf, seconds_target * 0.2)
+    threads = orc.threads()
     return {
-        "value": gemv_gbs, "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": f"numpy glint_np restatement: expand + x@W^T of {rows}x{K} rows of the GEMV weight, repeated ~{seconds_target / 2:.0f} s",
-        "encode_bf16_in_gbs": 2 * rows * K / enc_s / 1e9,
-        "encode_sample": f"numpy encode_f32 of {rows}x{K} BF16 weights, repeated ~{seconds_target / 2:.0f} s",
+        "value": gemv_bytes(N, K) / gemv_s / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"C oracle H-TILE GEMV 14336x4096 (bs 64, bf16 x, f32 accumulate), full size, "
+                  f"{gemv_reps} runs in ~{seconds_target * 0.4:.0f} s, OpenMP {threads} threads",
+        "gemv_us": gemv_s * 1e6,
+        "encode_bf16_in_gbs": 2 * n0 / enc_s / 1e9, "encode_threads": threads,
+        "encode_sample": f"C oracle encode of the 4096x4096 CPU-reference config (seed 1001, 0.1% outliers), "
+                         f"{enc_reps} runs",
+        "numpy_gemv_gbs": gemv_bytes(rows, K) / np_s / 1e9, "numpy_cores": 1,
+        "numpy_sample": f"numpy glint_np restatement: expand + x @ W^T of {rows}x{K} rows, {np_reps} runs",
     }
 
 
+# ---------------------------------------------------------------- profile summaries
+GEMV_KERNEL = "k_htile_gemv_xreg<true>"
+TRAFFIC_JSON = ROOT / "profiles" / "htile_gemv_m1_14336x4096.traffic.json"
+PMC_CMD = ("rocprofv3 --pmc {ctr} -d <dir> -o run -- python3 bench.py --quick --no-cpu --headline-only "
+           "--calibrate-copy --steps 20 --warmup 5")
+
+
+def _pmc_avg(db_path, counter):
+    """Per-dispatch average of `counter` by kernel name from a rocprofv3 (rocpd) database."""
+    import sqlite3
+    import statistics
+    cur = sqlite3.connect(db_path).cursor()
+    by = {}
+    for name, ctr, val in cur.execute("select kernel_name, counter_name, value from counters_collection"):
+        if ctr == counter:
+            by.setdefault(name, []).append(val)
+    return {k: (statistics.mean(v), len(v)) for k, v in by.items()}
+
+
+def summarize_traffic(fetch_db, write_db) -> dict:
+    """HBM bytes per headline GEMV launch from two --pmc runs (FETCH_SIZE, WRITE_SIZE, KiB
+    per dispatch). Each counter is scaled by what it reads for the 256 MiB device copy
+    (`__amd_rocclr_copyBuffer`, 10 calls made by --calibrate-copy): true bytes / counted."""
+    copy_bytes = 256 << 20
+    out = {"algorithmic_bytes": gemv_bytes(GEMV_N, GEMV_K)}
+    for tag, db, ctr in (("fetch", fetch_db, "FETCH_SIZE"), ("write", write_db, "WRITE_SIZE")):
+        avg = _pmc_avg(db, ctr)
+        copy = [v for k, v in avg.items() if "copyBuffer" in k]
+        gemv = [v for k, v in avg.items() if GEMV_KERNEL in k.replace(" ", "")]
+        if not copy or not gemv:
+            raise SystemExit(f"{db}: need copyBuffer and {GEMV_KERNEL} dispatches with {ctr}")
+        scale = copy_bytes / (copy[0][0] * 1024.0)
+        out[f"{tag}_counter_kib"] = gemv[0][0]
+        out[f"{tag}_dispatches"] = gemv[0][1]
+        out[f"{tag}_copy_counter_kib"] = copy[0][0]
+        out[f"{tag}_scale"] = scale
+        out[f"{tag}_bytes"] = gemv[0][0] * 1024.0 * scale
+    out["traffic_bytes"] = out["fetch_bytes"] + out["write_bytes"]
+    out["traffic_over_algorithmic"] = out["traffic_bytes"] / out["algorithmic_bytes"]
+    out["commands"] = [PMC_CMD.format(ctr="FETCH_SIZE"), PMC_CMD.format(ctr="WRITE_SIZE"),
+                       "python3 bench.py --summarize-traffic <fetch dir>/run_results.db <write dir>/run_results.db"]
+    TRAFFIC_JSON.write_text(json.dumps(out, indent=1) + "\n")
+    return out
+
+
+def summarize_trace(kt_db, bench_json=None) -> str:
+    """Per-kernel dispatch count and average / min / max duration from a --kernel-trace run,
+    written as a text table next to the traffic figures."""
+    import sqlite3
+    import statistics
+    cur = sqlite3.connect(kt_db).cursor()
+    by = {}
+    for name, start, end, gx, wx in cur.execute("select name, start, end, grid_x, workgroup_x from kernels"):
+        by.setdefault((name, gx, wx), []).append((end - start) / 1e3)
+    lines = [f"{'kernel':90s} {'grid_x':>9s} {'wg':>5s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} "
+             f"{'total_ms':>9s}"]
+    for (name, gx, wx), ds in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{name[:90]:90s} {gx:9d} {wx:5d} {len(ds):6d} {statistics.mean(ds):9.2f} {min(ds):9.2f} "
+                     f"{max(ds):9.2f} {sum(ds) / 1e3:9.3f}")
+    text = "\n".join(lines)
+    if bench_json:
+        j = json.loads(Path(bench_json).read_text().strip().splitlines()[-1])
+        text += (f"\n\nbench.py (same run) ms_per_step {j['ms_per_step'] * 1e3:.2f} us -> {j['value']:.0f} GB/s, "
+                 f"roofline frac {j['roofline']['frac']}")
+    return text
+
+
 def load_traffic():
-    p = ROOT / "profiles" / "htile_gemv_m1_14336x4096.traffic.json"
+    p = TRAFFIC_JSON
     if p.is_file():
         try:
             return json.loads(p.read_text()).get("traffic_bytes")
@@ -222,7 +378,18 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 10 plain 256 MiB device copies (the reference kernel for scaling PMC byte counters)")
+    ap.add_argument("--headline-only", action="store_true", help="only the bf16-out 14336x4096 GEMV loop")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
+                    help="write the traffic figures from two rocprofv3 --pmc databases (no GPU needed)")
+    ap.add_argument("--summarize-trace", nargs="+", metavar="DB",
+                    help="print the per-kernel table of a rocprofv3 --kernel-trace database [and bench JSON]")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        print(json.dumps(summarize_traffic(*args.summarize_traffic), indent=1))
+        return 0
+    if args.summarize_trace:
+        print(summarize_trace(*args.summarize_trace[:2]))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the GLINT hot path has no multi-GPU mode in this build "
               "(see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
@@ -242,7 +409,7 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    gemv, pins, x = bench_gemv(torch, H, args.steps, args.warmup)
+    gemv, pins, x = bench_gemv(torch, H, args.steps, args.warmup, args.headline_only)
     log(f"gemv {gemv['ms'] * 1e3:.2f} us {gemv['gbs']:.0f} GB/s")
     del pins
     torch.cuda.empty_cache()
@@ -254,6 +421,8 @@ def main() -> int:
         log("prefill done")
         extra["int8_gemm"] = bench_int8(torch, H, steps=10)
         log(f"int8 {extra['int8_gemm']['tops']:.0f} TOPS")
+        extra["host_abi_pcie"] = bench_host_abi(H)
+        log(f"host ABI encode {extra['host_abi_pcie']['encode_bf16_in_gbs']:.1f} GB/s bf16-in (PCIe inclusive)")
     cpu = None if args.no_cpu else cpu_baseline()
     achieved = gemv["gbs"]
     line = {

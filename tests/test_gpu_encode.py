@@ -67,16 +67,31 @@ def test_every_bf16_pattern(oracle, order):
 
 
 def test_baseline_config_full_size(oracle):
-    """W[4096x4096] ~ N(0, 0.02^2), seed 1001, 0.1% outliers x10, bs=64."""
-    rng = np.random.default_rng(1001)
-    n = 4096 * 4096
-    w = rng.normal(0.0, 0.02, n).astype(np.float32)
-    idx = rng.choice(n, n // 1000, replace=False)
-    w[idx] *= 10
-    u16 = bf16_bits(w)
+    """W[4096x4096] ~ N(0, 0.02^2), seed 1001, 0.1% outliers x10,
+    bs=64; against the oracle and the committed fixture digests (tests/golden/)."""
+    import hashlib
+    import json
+    import sys
+    from pathlib import Path
+    gdir = Path(__file__).resolve().parent / "golden"
+    sys.path.insert(0, str(gdir))
+    import make_golden
+    fixture = json.loads((gdir / "encode_4096x4096_outliers.json").read_text())
+    u16 = make_golden.config0_input()
+    n = u16.size
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    assert sha(u16) == fixture["input_bf16_sha256"]
     got = gpu_encode(u16, 64)
     want = oracle.encode_bf16(u16, 64)
     assert_same(got, want, "4096x4096")
+    for name, a in zip(("hole", "plug", "absmax"), got):
+        assert sha(a) == fixture[f"{name}_sha256"], name
+    rec16 = host(H.expand_bf16(*(dev(a) for a in got), n, 64), np.uint16)
+    assert sha(rec16) == fixture["expand_bf16_sha256"]
+    rec = host(H.expand_f32(*(dev(a) for a in got), n, 64))
+    assert rec.tobytes() == oracle.expand_f32(*want, n, 64).tobytes()
+    rmse = float(np.sqrt(np.mean((G.bf16_bits_to_f32(rec16).astype(np.float64) - G.bf16_bits_to_f32(u16)) ** 2)))
+    assert abs(rmse - fixture["expand_rmse"]) <= 1e-12
     # round trip through the GPU expand reproduces the oracle's reconstruction exactly
     torch = torch_cuda()
     hole, plug, am = (dev(a) for a in got)

@@ -293,6 +293,29 @@ def test_int8_integer_parts_are_exact(oracle):
     assert np.array_equal(out, ref)
 
 
+def test_int8_scale_bf16_special_cases(oracle):
+    """The bf16 epilogue RNE(f32(acc) * sa * sb) on inputs whose answer is fixed without
+    the formula: unit scales on |acc| <= 256 give the integer itself (exact in bf16);
+    power-of-two scales shift the exponent only; 257 rounds to even (256), 259 to 260;
+    a row scale of 0 gives +0 / -0 by the sign of acc."""
+    M, N = 4, 6
+    C = np.array([[0, 1, -1, 255, -256, 256], [257, 259, -257, 3, 100, -7],
+                  [1, 2, 3, 4, 5, 6], [-1, -2, 9, 0, 11, 13]], np.int32)
+    ones_m, ones_n = np.ones(M, np.float32), np.ones(N, np.float32)
+    got = G.bf16_bits_to_f32(oracle.int8_scale_bf16(C, ones_m, ones_n, M, N))
+    want = C.astype(np.float64)
+    want[1, 0], want[1, 1], want[1, 2] = 256.0, 260.0, -256.0
+    assert np.array_equal(got.astype(np.float64), want)
+    sa = np.array([0.5, 0.25, 2.0 ** -10, 4.0], np.float32)
+    sb = np.array([1.0, 2.0, 0.125, 1.0, 2.0 ** -7, 8.0], np.float32)
+    got = G.bf16_bits_to_f32(oracle.int8_scale_bf16(C, sa, sb, M, N)).astype(np.float64)
+    scaled = np.where(np.abs(want) <= 256, C.astype(np.float64), want) * sa[:, None].astype(np.float64) * sb[None, :]
+    small = np.abs(C) <= 256
+    assert np.array_equal(got[small], scaled[small])
+    zero = oracle.int8_scale_bf16(C, np.zeros(M, np.float32), ones_n, M, N)
+    assert np.array_equal(zero, np.where(C < 0, 0x8000, 0).astype(np.uint16))
+
+
 # ------------------------------------------------------- the pins catch planted mistakes
 def test_planted_mistakes_are_caught():
     """Mutations of the numpy oracle that a plausible bug would introduce must fail
