@@ -132,10 +132,39 @@ def llama3_8b_shapes():
     return shapes
 
 
+MODEL_STREAMS = 4
+
+
+def spread_over_streams(torch, make_call, count: int, nstreams: int):
+    """One pass over `count` independent calls, call i on stream i % nstreams (HIP streams
+    at the default priority), fenced by events so the pass starts and ends on the current
+    stream and times like one call. make_call(i, stream_handle) -> zero-argument call."""
+    import ctypes
+    main = torch.cuda.current_stream()
+    streams = [torch.cuda.Stream() for _ in range(nstreams)]
+    calls = [make_call(i, ctypes.c_void_p(streams[i % nstreams].cuda_stream)) for i in range(count)]
+
+    def run():
+        start = torch.cuda.Event()
+        start.record(main)
+        for st in streams:
+            st.wait_event(start)
+        for c in calls:
+            c()
+        for st in streams:
+            done = torch.cuda.Event()
+            done.record(st)
+            main.wait_event(done)
+    return run
+
+
 def bench_model_encode(torch, H, passes: int):
+    """Encode then expand (to BF16) the Llama-3-8B-shaped tensor set. The tensors are
+    independent, so a pass spreads them over MODEL_STREAMS streams as a pin writer would;
+    the one-stream pass is reported beside it."""
     shapes = llama3_8b_shapes()
     total = sum(a * b for a, b in shapes)
-    ws, pins, outs = [], [], []
+    ws, pins = [], []
     for t, (a, b) in enumerate(shapes):
         g = torch.Generator(device="cuda").manual_seed(4000 + t)
         w = (torch.randn(a * b, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
@@ -146,29 +175,58 @@ def bench_model_encode(torch, H, passes: int):
         pins.append((torch.empty((n + 1) // 2, dtype=torch.uint8, device="cuda"),
                      torch.empty((n + 1) // 2, dtype=torch.uint8, device="cuda"),
                      torch.empty((n + 63) // 64, dtype=torch.float32, device="cuda")))
-    lib, st = H.encode_lib(), stream_handle(torch)
-    enc_calls = [bound(lib.glint_encode_bf16_device, w, w.numel(), 64, p[0], p[1], p[2], st) for w, p in zip(ws, pins)]
-    enc = lambda: [c() for c in enc_calls]
-    ms_enc = timed(torch, [enc], passes, 1)
-    del enc_calls, enc
+    lib = H.encode_lib()
+    enc = lambda i, st: bound(lib.glint_encode_bf16_device, ws[i], ws[i].numel(), 64, pins[i][0], pins[i][1],
+                              pins[i][2], st)
+    ms_enc = timed(torch, [spread_over_streams(torch, enc, len(shapes), MODEL_STREAMS)], passes, 1)
+    ms_enc1 = timed(torch, [spread_over_streams(torch, enc, len(shapes), 1)], passes, 1)
     del ws
     torch.cuda.empty_cache()
     outs = [torch.empty(p[0].numel() * 2, dtype=torch.bfloat16, device="cuda") for p in pins]
     ns = [a * b for a, b in shapes]
-    exp_calls = [bound(lib.glint_expand_packed_to_bf16_device, p[0], p[1], p[2], n, 64, o, st)
-                 for p, n, o in zip(pins, ns, outs)]
-    exp = lambda: [c() for c in exp_calls]
-    ms_exp = timed(torch, [exp], passes, 1)
-    del exp_calls, exp
+    exp = lambda i, st: bound(lib.glint_expand_packed_to_bf16_device, pins[i][0], pins[i][1], pins[i][2], ns[i], 64,
+                              outs[i], st)
+    ms_exp = timed(torch, [spread_over_streams(torch, exp, len(shapes), MODEL_STREAMS)], passes, 1)
+    ms_exp1 = timed(torch, [spread_over_streams(torch, exp, len(shapes), 1)], passes, 1)
     del outs, pins
     torch.cuda.empty_cache()
     b = 3.0625 * total
     return {
-        "params": total, "tensors": len(shapes), "passes": passes,
+        "params": total, "tensors": len(shapes), "passes": passes, "streams": MODEL_STREAMS,
         "encode_ms": ms_enc, "encode_bf16_in_gbs": 2 * total / ms_enc / 1e6,
         "encode_hbm_gbs": b / ms_enc / 1e6, "encode_frac": b / ms_enc / 1e6 / HBM_PEAK_GBS,
         "expand_bf16_ms": ms_exp, "expand_hbm_gbs": b / ms_exp / 1e6, "expand_frac": b / ms_exp / 1e6 / HBM_PEAK_GBS,
+        "one_stream": {"encode_ms": ms_enc1, "encode_frac": b / ms_enc1 / 1e6 / HBM_PEAK_GBS,
+                       "expand_bf16_ms": ms_exp1, "expand_frac": b / ms_exp1 / 1e6 / HBM_PEAK_GBS},
     }
+
+
+def bench_encode_4096(torch, H, passes: int = 5):
+    """The CPU-reference configuration on the GPU: 4096x4096 BF16 (seed 1001, 0.1% outliers
+    x10), bs 64, 20 distinct copies (> 256 MB Infinity Cache) encoded per pass, spread over
+    MODEL_STREAMS streams; also on one stream."""
+    import numpy as np
+    rng = np.random.default_rng(1001)
+    n = 4096 * 4096
+    w = rng.normal(0.0, 0.02, n).astype(np.float32)
+    w[rng.choice(n, n // 1000, replace=False)] *= np.float32(10.0)
+    u = w.view(np.uint32)
+    u16 = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    src = torch.from_numpy(u16.view(np.int16)).cuda()
+    copies = 20
+    ws = [src.clone() for _ in range(copies)]
+    pins = [(torch.empty(n // 2, dtype=torch.uint8, device="cuda"), torch.empty(n // 2, dtype=torch.uint8, device="cuda"),
+             torch.empty(n // 64, dtype=torch.float32, device="cuda")) for _ in range(copies)]
+    lib = H.encode_lib()
+    enc = lambda i, st: bound(lib.glint_encode_bf16_device, ws[i], n, 64, pins[i][0], pins[i][1], pins[i][2], st)
+    ms = timed(torch, [spread_over_streams(torch, enc, copies, MODEL_STREAMS)], passes, 1) / copies
+    ms1 = timed(torch, [spread_over_streams(torch, enc, copies, 1)], passes, 1) / copies
+    del ws, pins, src
+    torch.cuda.empty_cache()
+    return {"config": "4096x4096 BF16, seed 1001, 0.1% outliers x10, bs 64; 20 copies per pass",
+            "streams": MODEL_STREAMS, "ms_per_matrix": ms, "encode_bf16_in_gbs": 2 * n / ms / 1e6,
+            "encode_frac": 3.0625 * n / ms / 1e6 / HBM_PEAK_GBS,
+            "one_stream_ms_per_matrix": ms1, "one_stream_frac": 3.0625 * n / ms1 / 1e6 / HBM_PEAK_GBS}
 
 
 def bench_host_abi(H, reps: int = 5):
@@ -415,6 +473,8 @@ def main() -> int:
     torch.cuda.empty_cache()
     extra = {}
     if not args.quick:
+        extra["encode_4096x4096"] = bench_encode_4096(torch, H)
+        log(f"encode 4096^2 {extra['encode_4096x4096']['encode_bf16_in_gbs']:.0f} GB/s bf16-in")
         extra["model_encode"] = bench_model_encode(torch, H, passes=3)
         log(f"model encode {extra['model_encode']['encode_bf16_in_gbs']:.0f} GB/s bf16-in")
         extra["prefill"] = bench_prefill(torch, H, steps=5)

@@ -66,6 +66,32 @@ __device__ __forceinline__ void glint_fill_cells_lds64_direct(float *ltab) {
     __syncthreads();
 }
 
+/* The same fill split in two so it can be overlapped with a kernel's first loads: the
+ * cell values go out first (issue order is wait order for vector loads), the LDS writes
+ * come after the kernel has issued its own loads. 8 runs per thread cover the table for
+ * blockDim >= 512; a loop covers smaller blocks. The caller issues the barrier. */
+struct GlintCellFill {
+    float v[8];
+    int run[8];
+};
+__device__ __forceinline__ void glint_cells_fill_load(GlintCellFill &f) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        f.run[k] = min((int)threadIdx.x + k * (int)blockDim.x, GLINT_LDS_CELLS64_WORDS / 4 - 1);
+        f.v[k] = (&kCells[0][0])[f.run[k] >> 4];
+    }
+}
+__device__ __forceinline__ void glint_cells_fill_store(float *ltab, const GlintCellFill &f) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) /* clamped runs rewrite the last run with its own value */
+        ((f32x4 *)ltab)[f.run[k]] = f32x4{f.v[k], f.v[k], f.v[k], f.v[k]};
+    for (int r = threadIdx.x + 8 * blockDim.x; r < GLINT_LDS_CELLS64_WORDS / 4; r += blockDim.x) {
+        const float v = (&kCells[0][0])[r >> 4];
+        ((f32x4 *)ltab)[r] = f32x4{v, v, v, v};
+    }
+}
+
 /* Byte address of code byte K of E for the lane whose lane*4 is `lane4` (in byte 0). */
 template <int K>
 __device__ __forceinline__ uint32_t glint_cell_addr(uint32_t E, uint32_t lane4) {

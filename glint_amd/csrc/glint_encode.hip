@@ -62,7 +62,7 @@ __device__ __forceinline__ glint_i16x2 glint_mag_key(uint32_t d) {
 #define ENC_THREADS 1024
 #endif
 #ifndef ENC_UNROLL
-#define ENC_UNROLL 4
+#define ENC_UNROLL 2
 #endif
 #ifndef ENC_WPE /* minimum waves per SIMD the register allocation must allow */
 #define ENC_WPE 4
@@ -144,6 +144,11 @@ __device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const gl
         absmax[chunk * 8 + (lane >> 3)] = s;
 }
 
+/* One wave handles groups of ENC_UNROLL consecutive chunks: groups wave, wave + nwaves, ...
+ * two groups in flight (register double buffer, unconditional clamped loads, full rounds
+ * so the wait counter can count them); the table fill's loads go out first and its LDS
+ * writes after the first two groups' loads. Chunks past the last full group are spread
+ * one per wave at the end. */
 __global__ __launch_bounds__(ENC_THREADS, ENC_WPE) void k_encode_bf16_b64(const glint_u32x4 *__restrict__ w,
                                                                  uint32_t *__restrict__ hole,
                                                                  uint32_t *__restrict__ plug,
@@ -155,33 +160,71 @@ __global__ __launch_bounds__(ENC_THREADS, ENC_WPE) void k_encode_bf16_b64(const 
      * entry stride (mod 2^32) */
     const uint32_t lane_k =
         (uint32_t)(lane % ENC_COPIES) * 16u - GLINT_CODE_MAGIC_BITS * (uint32_t)(ENC_COPIES * 16);
-    const int64_t wave = (int64_t)blockIdx.x * (ENC_THREADS / 64) + (threadIdx.x >> 6);
-    const int64_t nwaves = (int64_t)gridDim.x * (ENC_THREADS / 64);
-    int64_t c0 = wave * ENC_UNROLL;
-    glint_u32x4 d[ENC_UNROLL];
-    /* first loads go out before the table fill */
-    if (c0 + ENC_UNROLL <= nchunks) {
+    /* wave-uniform, so group arithmetic stays in scalar registers */
+    const int wave = (int)blockIdx.x * (ENC_THREADS / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = (int)gridDim.x * (ENC_THREADS / 64);
+    const int ngroups = (int)(nchunks / ENC_UNROLL);
+    const int my = wave < ngroups ? (ngroups - wave + nwaves - 1) / nwaves : 0; /* groups wave + i nwaves */
+    const int last = max(ngroups - 1, 0);
+
+    constexpr int kEntries = GLINT_CODE_BUCKETS * ENC_COPIES;
+    constexpr int kFill = (kEntries + 1023) / 1024; /* entries per thread at 1024 threads */
+    GlintCodeEntry fe[kFill];
+    int fi[kFill];
 #pragma unroll
-        for (int u = 0; u < ENC_UNROLL; ++u)
-            d[u] = __builtin_nontemporal_load(&w[(c0 + u) * 64 + lane]);
+    for (int k = 0; k < kFill; ++k) {
+        fi[k] = min((int)threadIdx.x + k * (int)blockDim.x, kEntries - 1);
+        fe[k] = kCodeTable[fi[k] / ENC_COPIES];
     }
-    glint_fill_code_lds(tab);
-    for (; c0 + ENC_UNROLL <= nchunks; c0 += nwaves * ENC_UNROLL) {
-        glint_u32x4 cur[ENC_UNROLL];
+    /* unconditional loads (a branch here would make every later wait count the worst
+     * path); chunk indices are clamped to the last chunk for the case of no full group */
+    const int64_t lastc = nchunks - 1;
+    glint_u32x4 da[ENC_UNROLL], db[ENC_UNROLL];
+    {
+        const int64_t ga = (int64_t)min(wave, last) * ENC_UNROLL, gb = (int64_t)min(wave + nwaves, last) * ENC_UNROLL;
 #pragma unroll
         for (int u = 0; u < ENC_UNROLL; ++u)
-            cur[u] = d[u];
-        const int64_t cn = c0 + nwaves * ENC_UNROLL;
-        if (cn + ENC_UNROLL <= nchunks) {
-#pragma unroll
-            for (int u = 0; u < ENC_UNROLL; ++u)
-                d[u] = __builtin_nontemporal_load(&w[(cn + u) * 64 + lane]);
-        }
+            da[u] = __builtin_nontemporal_load(&w[min(ga + u, lastc) * 64 + lane]);
 #pragma unroll
         for (int u = 0; u < ENC_UNROLL; ++u)
-            glint_encode_chunk(cur[u], tab, lane_k, c0 + u, lane, hole, plug, absmax);
+            db[u] = __builtin_nontemporal_load(&w[min(gb + u, lastc) * 64 + lane]);
     }
-    for (int64_t c = c0; c < nchunks && c < c0 + ENC_UNROLL; ++c)
+#pragma unroll
+    for (int k = 0; k < kFill; ++k) /* clamped indices rewrite the last entry with its own value */
+        tab[fi[k]] = glint_u32x4{fe[k].thr, glint_spread_code(fe[k].base), glint_spread_code(fe[k].base + 1), 0u};
+    for (int e = threadIdx.x + kFill * blockDim.x; e < kEntries; e += blockDim.x) { /* blockDim < 1024 only */
+        const GlintCodeEntry ce = kCodeTable[e / ENC_COPIES];
+        tab[e] = glint_u32x4{ce.thr, glint_spread_code(ce.base), glint_spread_code(ce.base + 1), 0u};
+    }
+    __syncthreads();
+
+    int i = 0;
+    for (; i + 2 <= my; i += 2) {
+        const int64_t c0 = (int64_t)(wave + i * nwaves) * ENC_UNROLL;
+#pragma unroll
+        for (int u = 0; u < ENC_UNROLL; ++u)
+            glint_encode_chunk(da[u], tab, lane_k, c0 + u, lane, hole, plug, absmax);
+        const int64_t ga = (int64_t)min(wave + (i + 2) * nwaves, last) * ENC_UNROLL;
+#pragma unroll
+        for (int u = 0; u < ENC_UNROLL; ++u)
+            da[u] = __builtin_nontemporal_load(&w[(ga + u) * 64 + lane]);
+        const int64_t c1 = (int64_t)(wave + (i + 1) * nwaves) * ENC_UNROLL;
+#pragma unroll
+        for (int u = 0; u < ENC_UNROLL; ++u)
+            glint_encode_chunk(db[u], tab, lane_k, c1 + u, lane, hole, plug, absmax);
+        const int64_t gb = (int64_t)min(wave + (i + 3) * nwaves, last) * ENC_UNROLL;
+#pragma unroll
+        for (int u = 0; u < ENC_UNROLL; ++u)
+            db[u] = __builtin_nontemporal_load(&w[(gb + u) * 64 + lane]);
+    }
+    if (i < my) {
+        const int64_t c0 = (int64_t)(wave + i * nwaves) * ENC_UNROLL;
+#pragma unroll
+        for (int u = 0; u < ENC_UNROLL; ++u)
+            glint_encode_chunk(da[u], tab, lane_k, c0 + u, lane, hole, plug, absmax);
+    }
+    const int64_t c = (int64_t)ngroups * ENC_UNROLL + wave; /* at most ENC_UNROLL - 1 leftover chunks */
+    if (c < nchunks)
         glint_encode_chunk(w[c * 64 + lane], tab, lane_k, c, lane, hole, plug, absmax);
 }
 
@@ -269,8 +312,11 @@ static int encode_device(const T *d_w, int64_t n, int bs, uint8_t *d_hole, uint8
         n_fast = (n / 512) * 512;
     if (n_fast) {
         const int64_t nchunks = n_fast / 512;
+        /* a group per wave while there are enough groups, at most the resident blocks; the
+         * leftover chunks (< ENC_UNROLL) need fewer waves than one block has */
         const unsigned grid =
             glint_grid(nchunks, (ENC_THREADS / 64) * ENC_UNROLL, (int)glint_resident_grid((const void *)k_encode_bf16_b64, ENC_THREADS, 0));
+
         k_encode_bf16_b64<<<grid, ENC_THREADS, 0, st>>>((const glint_u32x4 *)d_w, (uint32_t *)d_hole,
                                                         (uint32_t *)d_plug, d_am, nchunks);
     }
@@ -396,6 +442,118 @@ __global__ __launch_bounds__(256) void k_expand_generic(const uint8_t *__restric
     }
 }
 
+/* Run-mapped expand (power-of-two bs >= 8, n % 2048 == 0 part): a wave chunk is 256 runs of
+ * 8 elements; lane l owns runs 64 s + l (s < 4), i.e. one dword of each plane per run, so
+ * every plane load of a wave reads 256 B contiguous and every BF16 store writes 1 KiB
+ * contiguous (f32: two 16-B stores, 2 KiB). Chunks are double-buffered in registers with
+ * unconditional (clamped) loads in full rounds. */
+#ifndef EXPANDR_THREADS
+#define EXPANDR_THREADS 1024
+#endif
+#ifndef EXPANDR_HWCVT
+#define EXPANDR_HWCVT 1 /* BF16 by v_cvt_pk_bf16_f32 (RNE); NaN absmax takes the scalar rule */
+#endif
+
+struct ExpandChunk {
+    uint32_t h[4], p[4];
+    float a[4];
+};
+
+/* Loads of wave chunk c: runs c*256 + 64 s + lane. `abase` = c * (2048 >> shift) is the
+ * chunk's first absmax index (bs <= 2048, so a chunk starts on a block boundary). */
+__device__ __forceinline__ void expand_load_chunk(const uint32_t *__restrict__ hole, const uint32_t *__restrict__ plug,
+                                                  const float *__restrict__ absmax, int64_t c, int lane, int shift,
+                                                  ExpandChunk &ck) {
+    const uint32_t *h = hole + c * 256, *p = plug + c * 256;
+    const float *a = absmax + (c << (11 - shift));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        ck.h[s] = __builtin_nontemporal_load(h + s * 64 + lane);
+        ck.p[s] = __builtin_nontemporal_load(p + s * 64 + lane);
+        ck.a[s] = a[(uint32_t)(s * 512 + lane * 8) >> shift];
+    }
+}
+
+__device__ __forceinline__ uint32_t expand_pack2(float lo, float hi) {
+#if EXPANDR_HWCVT
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+#else
+    return glint_pack_bf16x2(lo, hi);
+#endif
+}
+
+template <bool BF16>
+__device__ __forceinline__ void expand_chunk(const float *ltab, uint32_t lane4, const ExpandChunk &ck, void *__restrict__ out,
+                                             int64_t c, int lane) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const uint32_t E = glint_codes_even(ck.h[s], ck.p[s]);
+        const uint32_t O = glint_codes_odd(ck.h[s], ck.p[s]);
+        const float a = ck.a[s];
+        float r[8];
+        r[0] = glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)) * a;
+        r[1] = glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)) * a;
+        r[2] = glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)) * a;
+        r[3] = glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)) * a;
+        r[4] = glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)) * a;
+        r[5] = glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)) * a;
+        r[6] = glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)) * a;
+        r[7] = glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)) * a;
+        const int64_t run = c * 256 + s * 64 + lane;
+        if (BF16) {
+            glint_u32x4 v;
+            if (a == a) {
+                v = glint_u32x4{expand_pack2(r[0], r[1]), expand_pack2(r[2], r[3]), expand_pack2(r[4], r[5]),
+                                expand_pack2(r[6], r[7])};
+            } else { /* NaN absmax: the reference NaN rule for every element */
+                v = glint_u32x4{(uint32_t)glint_f32_to_bf16(r[0]) | (uint32_t)glint_f32_to_bf16(r[1]) << 16,
+                                (uint32_t)glint_f32_to_bf16(r[2]) | (uint32_t)glint_f32_to_bf16(r[3]) << 16,
+                                (uint32_t)glint_f32_to_bf16(r[4]) | (uint32_t)glint_f32_to_bf16(r[5]) << 16,
+                                (uint32_t)glint_f32_to_bf16(r[6]) | (uint32_t)glint_f32_to_bf16(r[7]) << 16};
+            }
+            ((glint_u32x4 *)out)[run] = v;
+        } else {
+            ((glint_f32x4 *)out)[2 * run] = glint_f32x4{r[0], r[1], r[2], r[3]};
+            ((glint_f32x4 *)out)[2 * run + 1] = glint_f32x4{r[4], r[5], r[6], r[7]};
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(EXPANDR_THREADS) void k_expand_runs(const uint32_t *__restrict__ hole,
+                                                                 const uint32_t *__restrict__ plug,
+                                                                 const float *__restrict__ absmax,
+                                                                 void *__restrict__ out, int64_t nchunks, int shift) {
+    __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS];
+    const int lane = threadIdx.x & 63;
+    const uint32_t lane4 = (uint32_t)lane * 4u;
+    /* wave-uniform, so chunk arithmetic stays in scalar registers */
+    const int wave = (int)blockIdx.x * (EXPANDR_THREADS / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = (int)gridDim.x * (EXPANDR_THREADS / 64);
+    const int nch = (int)nchunks;
+    const int my = wave < nch ? (nch - wave + nwaves - 1) / nwaves : 0; /* chunks wave + i nwaves */
+    const int last = nch - 1;
+    GlintCellFill fill;
+    glint_cells_fill_load(fill);
+    ExpandChunk ca, cb;
+    expand_load_chunk(hole, plug, absmax, min(wave, last), lane, shift, ca);
+    expand_load_chunk(hole, plug, absmax, min(wave + nwaves, last), lane, shift, cb);
+    glint_cells_fill_store(ltab, fill);
+    __syncthreads();
+    int i = 0;
+    for (; i + 2 <= my; i += 2) {
+        expand_chunk<BF16>(ltab, lane4, ca, out, wave + i * nwaves, lane);
+        expand_load_chunk(hole, plug, absmax, min(wave + (i + 2) * nwaves, last), lane, shift, ca);
+        expand_chunk<BF16>(ltab, lane4, cb, out, wave + (i + 1) * nwaves, lane);
+        expand_load_chunk(hole, plug, absmax, min(wave + (i + 3) * nwaves, last), lane, shift, cb);
+    }
+    if (i < my)
+        expand_chunk<BF16>(ltab, lane4, ca, out, (int64_t)wave + (int64_t)i * nwaves, lane);
+}
+
 template <bool BF16>
 static int expand_device(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_am, int64_t n, int bs, void *d_out,
                          hipStream_t st) {
@@ -405,10 +563,18 @@ static int expand_device(const uint8_t *d_hole, const uint8_t *d_plug, const flo
         return 0;
     const int cus = glint_num_cus();
     int64_t n_fast = 0;
-    if (bs % 32 == 0 && glint_aligned(d_hole, 16) && glint_aligned(d_plug, 16) && glint_aligned(d_am, 4) &&
-        glint_aligned(d_out, 16))
+    const bool aligned = glint_aligned(d_hole, 16) && glint_aligned(d_plug, 16) && glint_aligned(d_am, 4) &&
+                         glint_aligned(d_out, 16);
+    if (aligned && bs >= 8 && bs <= 2048 && (bs & (bs - 1)) == 0 && n >= 2048 && n / 2048 < (1LL << 30)) {
+        n_fast = (n / 2048) * 2048;
+        const int64_t nchunks = n_fast / 2048;
+        const int64_t resident = glint_resident_grid((const void *)k_expand_runs<BF16>, EXPANDR_THREADS, 0);
+        const int64_t wanted = (nchunks + EXPANDR_THREADS / 64 - 1) / (EXPANDR_THREADS / 64);
+        const unsigned grid = (unsigned)(wanted < resident ? wanted : resident);
+        k_expand_runs<BF16><<<grid, EXPANDR_THREADS, 0, st>>>((const uint32_t *)d_hole, (const uint32_t *)d_plug, d_am,
+                                                               d_out, nchunks, __builtin_ctz((unsigned)bs));
+    } else if (aligned && bs % 32 == 0 && n >= 32) { /* ngroups >= 1: the kernel clamps to ngroups - 1 */
         n_fast = (n / 32) * 32;
-    if (n_fast) {
         const int64_t ngroups = n_fast / 32;
         const int resident = (int)glint_resident_grid((const void *)k_expand_fast<BF16>, EXPAND_THREADS, 0);
         k_expand_fast<BF16><<<glint_grid(ngroups, EXPAND_THREADS * EXPAND_U, resident), EXPAND_THREADS, 0, st>>>(
