@@ -191,47 +191,70 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 }
 
 /* ------------------------------------------------ GEMV with x in registers */
-/* For K a multiple of 2048 (every K of the decode shapes): the row is cut into S = K/2048
- * slices of 64 chunks of 32 elements. Wave (s, g) of a workgroup holds slice s of x in
- * registers (lane l: the 32 f32 of chunk 64 s + l) and runs rows r0 + g, r0 + g + G, ...
- * of the workgroup's row range; LDS then serves only the cell lookups. Per row a wave
- * loads 1 KiB of each plane (16 B per lane) plus the 32 block scales, rows double-buffered
- * in registers; its partial sum is folded to 4 row-of-16 sums by DPP and parked in LDS,
- * and after one barrier the workgroup adds the 4 S partials of each row in a fixed order. */
+/* For K a multiple of 64 EL (EL = 32 or 16 elements per lane; every K of the decode shapes):
+ * a row is cut into chunks of EL elements (EL/2 bytes of each plane, inside one absmax
+ * block) and S = K / (64 EL) slices of 64 chunks. Wave (s, g) of a workgroup holds slice s
+ * of x in registers (lane l: the EL f32 of chunk 64 s + l) and runs rows r0 + g,
+ * r0 + g + G, ... of the workgroup's row range; LDS then serves only the cell lookups. Per
+ * row a wave loads 32 EL bytes of each plane plus its block scales, rows multi-buffered in
+ * registers; its partial sum is folded to 4 row-of-16 sums by DPP and parked in LDS, and
+ * after one barrier the workgroup adds the 4 S partials of each row in a fixed order. */
 #ifndef GEMV_X_THREADS
 #define GEMV_X_THREADS 512 /* most threads per workgroup (whole waves of S slices are used) */
+#endif
+#ifndef GEMV_X_EL
+#define GEMV_X_EL 32 /* elements per lane per row: 32 (16-B plane loads) or 16 (8-B) */
 #endif
 #ifndef GEMV_X_DEPTH
 #define GEMV_X_DEPTH 3 /* rows of loads in flight per wave */
 #endif
+#ifndef GEMV_X_PRE
+#define GEMV_X_PRE GEMV_X_DEPTH /* of those, rows issued before the table fill's barrier */
+#endif
 #ifndef GEMV_X_BATCH
-#define GEMV_X_BATCH 2 /* groups of 8 cell lookups a wave may have in flight (1, 2 or 4) */
+#define GEMV_X_BATCH 2 /* groups of 8 cell lookups a wave may have in flight */
+#endif
+#ifndef GEMV_X_WPE
+#define GEMV_X_WPE 1 /* minimum waves per SIMD the register allocation must allow */
 #endif
 #define GEMV_X_RED_MAX 4096 /* floats of per-row partials a workgroup may park in LDS */
 
+template <int EL> struct GemvVec;
+template <> struct GemvVec<32> { typedef glint_u32x4 T; };
+template <> struct GemvVec<16> { typedef glint_u32x2 T; };
+
+template <int EL>
 struct GemvRow {
-    glint_u32x4 h, p;
+    typename GemvVec<EL>::T h, p; /* EL packed elements of each plane */
     float a;
 };
 
-__device__ __forceinline__ void gemv_x_load(const glint_u32x4 *__restrict__ hole, const glint_u32x4 *__restrict__ plug,
+template <int EL>
+__device__ __forceinline__ void gemv_x_load(const void *__restrict__ hole, const void *__restrict__ plug,
                                             const float *__restrict__ absmax, int64_t n, int nch, uint32_t j,
-                                            GemvRow &row) {
-    row.h = __builtin_nontemporal_load(hole + n * nch + j);
-    row.p = __builtin_nontemporal_load(plug + n * nch + j);
-    row.a = absmax[n * (nch >> 1) + (j >> 1)];
+                                            GemvRow<EL> &row) {
+    typedef typename GemvVec<EL>::T V;
+    row.h = __builtin_nontemporal_load((const V *)hole + n * nch + j);
+    row.p = __builtin_nontemporal_load((const V *)plug + n * nch + j);
+    row.a = absmax[n * (nch / (64 / EL)) + (j / (64 / EL))];
 }
 
-template <bool OUT_BF16>
-__global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_xreg(
-    const glint_u32x4 *__restrict__ hole, const glint_u32x4 *__restrict__ plug, const float *__restrict__ absmax,
+template <int EL>
+__device__ __forceinline__ uint32_t gemv_word(const typename GemvVec<EL>::T &v, int q) {
+    return v[q];
+}
+
+template <int EL, bool OUT_BF16>
+__global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE))) void k_htile_gemv_xreg(
+    const void *__restrict__ hole, const void *__restrict__ plug, const float *__restrict__ absmax,
     const glint_u32x4 *__restrict__ x, void *__restrict__ y, int N, int K, int G, int rows_per_wg) {
     __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS]; /* 64 KiB at LDS offset 0 */
     extern __shared__ float red[];                                              /* [rows_per_wg][S][4] */
+    constexpr int Q = EL / 8; /* 8-element groups per chunk = packed words per plane */
 
     const int lane = threadIdx.x & 63;
     const uint32_t lane4 = (uint32_t)lane * 4u;
-    const int nch = K >> 5, S = nch >> 6;
+    const int nch = K / EL, S = nch >> 6;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = w % S, g = w / S;
     const int r0 = blockIdx.x * rows_per_wg;
@@ -242,36 +265,23 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_xreg(
     auto row_of = [&](int i) -> int64_t { return (int64_t)min(r0 + g + min(i, max(my - 1, 0)) * G, N - 1); };
 
     /* Loads go out in the order they are consumed (the wait counter is in order): the
-     * cell table, x, then the first two rows. 8 runs per thread cover the 4096 16-B runs
-     * of the table when blockDim >= 512; a loop after them covers smaller blocks. */
-    /* run indices past 4095 are clamped: those threads rewrite run 4095 with its own value */
-    float cv[8];
-    int w4[8];
+     * cell table, x, then the first rows; the table's LDS writes follow. */
+    GlintCellFill fill;
+    glint_cells_fill_load(fill);
+    glint_u32x4 xv[Q];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        w4[k] = min((int)threadIdx.x + k * (int)blockDim.x, 4095);
-        cv[k] = (&kCells[0][0])[w4[k] >> 4];
-    }
-    glint_u32x4 xv[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        xv[q] = x[j * 4 + q];
+    for (int q = 0; q < Q; ++q)
+        xv[q] = x[j * Q + q];
     __builtin_amdgcn_sched_barrier(0);
-    GemvRow buf[GEMV_X_DEPTH];
+    GemvRow<EL> buf[GEMV_X_DEPTH];
 #pragma unroll
-    for (int d = 0; d < GEMV_X_DEPTH; ++d)
-        gemv_x_load(hole, plug, absmax, row_of(d), nch, j, buf[d]);
+    for (int d = 0; d < GEMV_X_PRE; ++d)
+        gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, j, buf[d]);
     __builtin_amdgcn_sched_barrier(0);
+    glint_cells_fill_store(ltab, fill);
+    float xr[EL];
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-        ((glint_f32x4 *)ltab)[w4[k]] = glint_f32x4{cv[k], cv[k], cv[k], cv[k]};
-    for (int r = threadIdx.x + 8 * blockDim.x; r < 4096; r += blockDim.x) { /* blockDim < 512 only */
-        const float v = (&kCells[0][0])[r >> 4];
-        ((glint_f32x4 *)ltab)[r] = glint_f32x4{v, v, v, v};
-    }
-    float xr[32];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < Q; ++q) {
         const glint_u32x4 v = xv[q];
         xr[8 * q + 0] = glint_bf16lo(v.x); xr[8 * q + 1] = glint_bf16hi(v.x);
         xr[8 * q + 2] = glint_bf16lo(v.y); xr[8 * q + 3] = glint_bf16hi(v.y);
@@ -279,15 +289,17 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_xreg(
         xr[8 * q + 6] = glint_bf16lo(v.w); xr[8 * q + 7] = glint_bf16hi(v.w);
     }
     __syncthreads();
-
-    auto compute_row = [&](int i, const GemvRow &row) {
-        float part = 0.0f;
-        const uint32_t H[4] = {row.h.x, row.h.y, row.h.z, row.h.w};
-        const uint32_t P[4] = {row.p.x, row.p.y, row.p.z, row.p.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t E = glint_codes_even(H[q], P[q]);
-            const uint32_t O = glint_codes_odd(H[q], P[q]);
+    for (int d = GEMV_X_PRE; d < GEMV_X_DEPTH; ++d)
+        gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, j, buf[d]);
+
+    auto compute_row = [&](int i, const GemvRow<EL> &row) {
+        float part = 0.0f;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const uint32_t H = gemv_word<EL>(row.h, q), P = gemv_word<EL>(row.p, q);
+            const uint32_t E = glint_codes_even(H, P);
+            const uint32_t O = glint_codes_odd(H, P);
             part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)), xr[8 * q + 0], part);
             part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)), xr[8 * q + 1], part);
             part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)), xr[8 * q + 2], part);
@@ -312,7 +324,7 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_xreg(
 #pragma unroll
         for (int d = 0; d < GEMV_X_DEPTH; ++d) {
             compute_row(i + d, buf[d]);
-            gemv_x_load(hole, plug, absmax, row_of(i + d + GEMV_X_DEPTH), nch, j, buf[d]);
+            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + GEMV_X_DEPTH), nch, j, buf[d]);
         }
     }
 #pragma unroll
@@ -559,9 +571,9 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             k_htile_mfma_b64<128><<<dim3(gx, (M + 127) / 128), 256, 0, st>>>(
                 (const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
         }
-    } else if (gemv_ok && (K % 2048) == 0 && K / 2048 <= GEMV_X_THREADS / 64) {
-        const int S = K / 2048, G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
-        auto kern = k_htile_gemv_xreg<OUT_BF16>;
+    } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS / 64) {
+        const int S = K / (64 * GEMV_X_EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
+        auto kern = k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16>;
         const int64_t resident = glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4);
         const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
         int64_t rows_per_wg = G * per_wave;
@@ -572,8 +584,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         const size_t lds = (size_t)rows_per_wg * S * 4 * sizeof(float);
         if (glint_set_lds_limit((const void *)kern, GEMV_X_RED_MAX * 4) != 0)
             return -3;
-        kern<<<grid, threads, lds, st>>>((const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax,
-                                         (const glint_u32x4 *)x, y, N, K, G, (int)rows_per_wg);
+        kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const glint_u32x4 *)x, y, N, K, G, (int)rows_per_wg);
     } else if (gemv_ok) {
         constexpr int R = GEMV_R, D = GEMV_D;
         const size_t lds = GEMV_LDS_BYTES(K);
