@@ -69,13 +69,20 @@ __global__ __launch_bounds__(256) void k_quant_act(const glint_u32x4 *__restrict
 #define Q_LDS_ROW 80 /* 64 bytes + 16 of padding: 8 consecutive rows hit 8 disjoint bank quads */
 
 /* 256 threads = 4 waves in 2x2; wave (wm, wn) owns rows [32 wm, +32) x cols [32 wn, +32) of
- * the 64x64 tile = 2x2 MFMA tiles. */
+ * the 64x64 tile = 2x2 MFMA tiles. Per 64-slice kb: ic = exact int32 dot product (one MFMA
+ * with zero C), acc = acc + ((float)ic * sx) * sw. PLUG adds, per kb and right after the
+ * base term, a p7_plug_res4_v1 slice read from its nibbles (element 2i in the low nibble,
+ * value nibble - 8) with its own block scales: acc = acc + ((float)ip * sx) * sp. ACCUM
+ * stores y + acc instead of acc (the second pass of the two-pass forms). */
+template <bool PLUG, bool ACCUM>
 __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict__ xq, const float *__restrict__ sx,
                                                        const int8_t *__restrict__ wq, const float *__restrict__ sw,
-                                                       float *__restrict__ y, int m, int n, int k_in) {
+                                                       float *__restrict__ y, int m, int n, int k_in,
+                                                       const uint8_t *__restrict__ pq4, const float *__restrict__ psc) {
     __shared__ __attribute__((aligned(16))) int8_t sA[Q_BM * Q_LDS_ROW];
     __shared__ __attribute__((aligned(16))) int8_t sB[Q_BN * Q_LDS_ROW];
-    __shared__ float sSx[Q_BM], sSw[Q_BN];
+    __shared__ __attribute__((aligned(16))) int8_t sP[PLUG ? Q_BN * Q_LDS_ROW : 16];
+    __shared__ float sSx[Q_BM], sSw[Q_BN], sSp[PLUG ? Q_BN : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * Q_BM, n0 = blockIdx.x * Q_BN;
@@ -88,7 +95,8 @@ __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict_
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 acc[a][b][i] = 0.0f;
-    /* staging: thread t copies 16 B of A row (t >> 2) and of B row (t >> 2), K bytes (t & 3) * 16 */
+    /* staging: thread t copies 16 B of A row (t >> 2) and of B row (t >> 2), K bytes (t & 3) * 16;
+     * the plug slice is 8 B of nibbles per thread, widened to the same 16 B */
     const int sr = tid >> 2, sc = (tid & 3) * 16;
     for (int kb = 0; kb < nkb; ++kb) {
         glint_u32x4 va = glint_u32x4{0u, 0u, 0u, 0u}, vb = va;
@@ -98,29 +106,64 @@ __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict_
             vb = *(const glint_u32x4 *)(wq + (int64_t)(n0 + sr) * k_in + (int64_t)kb * 64 + sc);
         *(glint_u32x4 *)(sA + sr * Q_LDS_ROW + sc) = va;
         *(glint_u32x4 *)(sB + sr * Q_LDS_ROW + sc) = vb;
+        if (PLUG) {
+            /* rows past n read as nibble 8 (value 0); k_in is even, so a row's nibbles start on a byte */
+            uint32_t nib[2] = {0x88888888u, 0x88888888u};
+            if (n0 + sr < n) {
+                const uint8_t *src = pq4 + (((int64_t)(n0 + sr) * k_in + (int64_t)kb * 64 + sc) >> 1);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    nib[h] = (uint32_t)src[4 * h] | (uint32_t)src[4 * h + 1] << 8 | (uint32_t)src[4 * h + 2] << 16 |
+                             (uint32_t)src[4 * h + 3] << 24;
+            }
+            uint32_t out[4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                /* bytes 4h..4h+3 hold elements 8h..8h+7: low nibble first; value = nibble - 8 */
+                const uint32_t lo = nib[h] & 0x0F0F0F0Fu, hi = (nib[h] >> 4) & 0x0F0F0F0Fu;
+                const uint32_t e0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u); /* elements 0..3 */
+                const uint32_t e1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u); /* elements 4..7 */
+                /* per byte: nibble - 8 mod 256; setting bit 7 of every byte first keeps the
+                 * subtraction's borrow inside the byte, the xor clears it again */
+                out[2 * h] = ((e0 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                out[2 * h + 1] = ((e1 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+            }
+            *(glint_u32x4 *)(sP + sr * Q_LDS_ROW + sc) = glint_u32x4{out[0], out[1], out[2], out[3]};
+        }
         if (tid < Q_BM)
             sSx[tid] = (m0 + tid < m) ? sx[(int64_t)(m0 + tid) * nkb + kb] : 0.0f;
         else if (tid < Q_BM + Q_BN)
             sSw[tid - Q_BM] = (n0 + tid - Q_BM < n) ? sw[(int64_t)(n0 + tid - Q_BM) * nkb + kb] : 0.0f;
+        else if (PLUG && tid < Q_BM + 2 * Q_BN)
+            sSp[tid - Q_BM - Q_BN] = (n0 + tid - Q_BM - Q_BN < n) ? psc[(int64_t)(n0 + tid - Q_BM - Q_BN) * nkb + kb] : 0.0f;
         __syncthreads();
-        glint_i32x4 af[2], bf[2];
+        glint_i32x4 af[2], bf[2], pf[2];
 #pragma unroll
         for (int a = 0; a < 2; ++a)
             af[a] = *(const glint_i32x4 *)(sA + (wm * 32 + a * 16 + (lane & 15)) * Q_LDS_ROW + (lane >> 4) * 16);
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < 2; ++b) {
             bf[b] = *(const glint_i32x4 *)(sB + (wn * 32 + b * 16 + (lane & 15)) * Q_LDS_ROW + (lane >> 4) * 16);
+            if (PLUG)
+                pf[b] = *(const glint_i32x4 *)(sP + (wn * 32 + b * 16 + (lane & 15)) * Q_LDS_ROW + (lane >> 4) * 16);
+        }
 #pragma unroll
         for (int a = 0; a < 2; ++a)
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 const glint_i32x4 ic = glint_mfma_i8(af[a], bf[b], glint_i32x4{0, 0, 0, 0});
-                const float swv = sSw[wn * 32 + b * 16 + (lane & 15)];
+                glint_i32x4 ip = glint_i32x4{0, 0, 0, 0};
+                if (PLUG)
+                    ip = glint_mfma_i8(af[a], pf[b], glint_i32x4{0, 0, 0, 0});
+                const int col = wn * 32 + b * 16 + (lane & 15);
+                const float swv = sSw[col];
+                const float spv = PLUG ? sSp[col] : 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float sxv = sSx[wm * 32 + a * 16 + (lane >> 4) * 4 + i];
-                    const float t = (float)ic[i] * sxv;
-                    acc[a][b][i] = acc[a][b][i] + t * swv;
+                    acc[a][b][i] = acc[a][b][i] + ((float)ic[i] * sxv) * swv;
+                    if (PLUG)
+                        acc[a][b][i] = acc[a][b][i] + ((float)ip[i] * sxv) * spv;
                 }
             }
         __syncthreads();
@@ -133,9 +176,40 @@ __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict_
             for (int i = 0; i < 4; ++i) {
                 const int r = m0 + wm * 32 + a * 16 + (lane >> 4) * 4 + i;
                 const int c = n0 + wn * 32 + b * 16 + (lane & 15);
-                if (r < m && c < n)
-                    y[(int64_t)r * n + c] = acc[a][b][i];
+                if (r < m && c < n) {
+                    float *dst = y + (int64_t)r * n + c;
+                    *dst = ACCUM ? *dst + acc[a][b][i] : acc[a][b][i];
+                }
             }
+}
+
+/* p7_plug_res4_v1 slice to int8: element i = nibble i (low nibble first) - 8. */
+__global__ __launch_bounds__(256) void k_unpack_res4(const uint8_t *__restrict__ q4, int8_t *__restrict__ out, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = (int8_t)((int)((q4[i >> 1] >> ((i & 1) * 4)) & 15u) - 8);
+}
+
+/* Quantization residual of the activation, quantized again by the same rule: per (row,
+ * 64-block), r = x - (float)xq * sx (a product, then a difference), s = amax|r| > 0 ?
+ * amax / 127 : 1, rq = clamp(rint(r / s), -127, 127). One wave per block, one element per
+ * lane. Reference cuda/int8_mma_gemm.cu:172-190. */
+__global__ __launch_bounds__(256) void k_quant_act_resid(const uint16_t *__restrict__ x, const int8_t *__restrict__ xq,
+                                                         const float *__restrict__ sx, int64_t nblocks,
+                                                         int8_t *__restrict__ rq, float *__restrict__ sr) {
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = (int64_t)gridDim.x * (blockDim.x / 64);
+    for (int64_t b = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); b < nblocks; b += waves) {
+        const int64_t i = b * 64 + lane;
+        const float r = __uint_as_float((uint32_t)x[i] << 16) - (float)xq[i] * sx[b];
+        const float am = glint_wave_max(fabsf(r));
+        const float s = (am > 0.0f) ? (am / 127.0f) : 1.0f;
+        int v = (int)rintf(r / s);
+        v = v > 127 ? 127 : (v < -127 ? -127 : v);
+        rq[i] = (int8_t)v;
+        if (lane == 0)
+            sr[b] = s;
+    }
 }
 
 /* ------------------------------------------------------------ plain INT8 GEMM */
@@ -223,20 +297,88 @@ __global__ __launch_bounds__(256) void k_int8_gemm(const int8_t *__restrict__ A,
 }
 
 /* ------------------------------------------------------------------ C ABI */
-GLINT_API int int8_mma_gemm(const void *x, Int8MmaLinear w, float *y, int m, int8_t *xq, float *sx,
-                            struct ihipStream_t *stream) {
-    if (!x || !y || !xq || !sx || !w.q || !w.scale || m < 1 || w.n_out < 1 || w.k_in < 64 || (w.k_in % 64) != 0)
-        return (int)hipErrorInvalidValue;
-    hipStream_t st = (hipStream_t)stream;
-    if (!glint_aligned(x, 16) || !glint_aligned(xq, 16) || !glint_aligned(w.q, 16))
-        return (int)hipErrorInvalidValue;
-    const int64_t nchunk8 = (int64_t)m * w.k_in / 8;
+static bool q_args_ok(const void *x, const void *y, const void *xq, const void *sx, const Int8MmaLinear &w, int m) {
+    return x && y && xq && sx && w.q && w.scale && m >= 1 && w.n_out >= 1 && w.k_in >= 64 && (w.k_in % 64) == 0 &&
+           glint_aligned(x, 16) && glint_aligned(xq, 16) && glint_aligned(w.q, 16);
+}
+
+static void q_launch_quant(const void *x, int m, int k_in, int8_t *xq, float *sx, hipStream_t st) {
+    const int64_t nchunk8 = (int64_t)m * k_in / 8;
     int64_t grid = (nchunk8 + 255) / 256;
     if (grid > 4096)
         grid = 4096;
     k_quant_act<<<(unsigned)grid, 256, 0, st>>>((const glint_u32x4 *)x, nchunk8, (glint_u32x2 *)xq, sx);
-    dim3 g2((w.n_out + Q_BN - 1) / Q_BN, (m + Q_BM - 1) / Q_BM);
-    k_int8_mma_gemm<<<g2, 256, 0, st>>>(xq, sx, w.q, w.scale, y, m, w.n_out, w.k_in);
+}
+
+template <bool PLUG, bool ACCUM>
+static void q_launch_gemm(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw, float *y, int m,
+                          int n, int k_in, const uint8_t *pq4, const float *psc, hipStream_t st) {
+    dim3 g((n + Q_BN - 1) / Q_BN, (m + Q_BM - 1) / Q_BM);
+    k_int8_mma_gemm<PLUG, ACCUM><<<g, 256, 0, st>>>(xq, sx, wq, sw, y, m, n, k_in, pq4, psc);
+}
+
+static void q_launch_unpack(const uint8_t *q4, int8_t *out, int64_t n, hipStream_t st) {
+    int64_t grid = (n + 255) / 256;
+    if (grid > 8192)
+        grid = 8192;
+    k_unpack_res4<<<(unsigned)grid, 256, 0, st>>>(q4, out, n);
+}
+
+GLINT_API int int8_mma_gemm(const void *x, Int8MmaLinear w, float *y, int m, int8_t *xq, float *sx,
+                            struct ihipStream_t *stream) {
+    if (!q_args_ok(x, y, xq, sx, w, m))
+        return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    q_launch_quant(x, m, w.k_in, xq, sx, st);
+    q_launch_gemm<false, false>(xq, sx, w.q, w.scale, y, m, w.n_out, w.k_in, nullptr, nullptr, st);
+    return (int)hipGetLastError();
+}
+
+GLINT_API int int8_mma_gemm_plug(const void *x, Int8MmaLinear w, const uint8_t *plug_q4, const float *plug_scale,
+                                 float *y, int m, int8_t *xq, float *sx, int8_t *plug_i8,
+                                 struct ihipStream_t *stream) {
+    if (!q_args_ok(x, y, xq, sx, w, m) || !plug_q4 || !plug_scale || !plug_i8 || !glint_aligned(plug_i8, 16))
+        return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    q_launch_quant(x, m, w.k_in, xq, sx, st);
+    q_launch_gemm<false, false>(xq, sx, w.q, w.scale, y, m, w.n_out, w.k_in, nullptr, nullptr, st);
+    q_launch_unpack(plug_q4, plug_i8, (int64_t)w.n_out * w.k_in, st);
+    q_launch_gemm<false, true>(xq, sx, plug_i8, plug_scale, y, m, w.n_out, w.k_in, nullptr, nullptr, st);
+    return (int)hipGetLastError();
+}
+
+GLINT_API int int8_mma_gemm_plug_fused(const void *x, Int8MmaLinear w, const uint8_t *plug_q4,
+                                       const float *plug_scale, float *y, int m, int8_t *xq, float *sx,
+                                       struct ihipStream_t *stream) {
+    if (!q_args_ok(x, y, xq, sx, w, m) || !plug_q4 || !plug_scale)
+        return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    q_launch_quant(x, m, w.k_in, xq, sx, st);
+    q_launch_gemm<true, false>(xq, sx, w.q, w.scale, y, m, w.n_out, w.k_in, plug_q4, plug_scale, st);
+    return (int)hipGetLastError();
+}
+
+GLINT_API int int8_mma_gemm_resolve(const void *x, Int8MmaLinear w, const uint8_t *plug_q4, const float *plug_scale,
+                                    float *y, int m, int8_t *xq, float *sx, int8_t *rq, float *sr, int8_t *plug_i8,
+                                    struct ihipStream_t *stream) {
+    const bool plug = plug_q4 != nullptr;
+    if (!q_args_ok(x, y, xq, sx, w, m) || !rq || !sr || !glint_aligned(rq, 16) || plug != (plug_i8 != nullptr) ||
+        plug != (plug_scale != nullptr) || (plug && !glint_aligned(plug_i8, 16)))
+        return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t nblocks = (int64_t)m * (w.k_in / 64);
+    q_launch_quant(x, m, w.k_in, xq, sx, st);
+    int64_t grid = (nblocks + 3) / 4;
+    if (grid > 8192)
+        grid = 8192;
+    k_quant_act_resid<<<(unsigned)grid, 256, 0, st>>>((const uint16_t *)x, xq, sx, nblocks, rq, sr);
+    q_launch_gemm<false, false>(xq, sx, w.q, w.scale, y, m, w.n_out, w.k_in, nullptr, nullptr, st);
+    q_launch_gemm<false, true>(rq, sr, w.q, w.scale, y, m, w.n_out, w.k_in, nullptr, nullptr, st);
+    if (plug) {
+        q_launch_unpack(plug_q4, plug_i8, (int64_t)w.n_out * w.k_in, st);
+        q_launch_gemm<false, true>(xq, sx, plug_i8, plug_scale, y, m, w.n_out, w.k_in, nullptr, nullptr, st);
+        q_launch_gemm<false, true>(rq, sr, plug_i8, plug_scale, y, m, w.n_out, w.k_in, nullptr, nullptr, st);
+    }
     return (int)hipGetLastError();
 }
 

@@ -65,12 +65,31 @@ class Int8MmaLinear(_c.Structure):
     _fields_ = [("q", VP), ("scale", VP), ("n_out", I32), ("k_in", I32)]
 
 
+class GlintStreamerStats(ctypes.Structure):
+    """include/glint_plug_streamer.h GlintStreamerStats."""
+    _fields_ = [("total_h2d_bytes", ctypes.c_uint64), ("total_stall_ms", ctypes.c_double),
+                ("per_layer_stall_ms", ctypes.c_double * 64), ("n_layers", ctypes.c_int)]
+
+
 _P7_SIGS = {
     "p7_abi_version": ([], _c.c_char_p),
+    "p7_abi_selftest": ([_c.c_char_p, _c.c_size_t], I32),
     "int8_mma_gemm": ([VP, Int8MmaLinear, VP, I32, VP, VP, VP], I32),
+    "int8_mma_gemm_plug": ([VP, Int8MmaLinear, VP, VP, VP, I32, VP, VP, VP, VP], I32),
+    "int8_mma_gemm_plug_fused": ([VP, Int8MmaLinear, VP, VP, VP, I32, VP, VP, VP], I32),
+    "int8_mma_gemm_resolve": ([VP, Int8MmaLinear, VP, VP, VP, I32, VP, VP, VP, VP, VP, VP], I32),
     "p7_int8_gemm_flat": ([VP, VP, VP, I32, I32, VP, I32, VP, VP, VP], I32),
+    "p7_int8_gemm_plug_flat": ([VP, VP, VP, VP, VP, I32, I32, VP, I32, VP, VP, VP], I32),
     "glint_int8_gemm_i32": ([VP, VP, VP, I32, I32, I32, VP], I32),
     "glint_int8_gemm_scaled_bf16": ([VP, VP, VP, VP, VP, I32, I32, I32, VP], I32),
+    "glint_plug_streamer_create": ([_c.POINTER(VP), I32, _c.POINTER(_c.c_uint64), VP, VP], I32),
+    "glint_plug_streamer_destroy": ([VP], None),
+    "glint_plug_streamer_set_host_data": ([VP, I32, VP, _c.c_uint64], I32),
+    "glint_plug_streamer_start": ([VP], I32),
+    "glint_plug_streamer_acquire": ([VP, I32, _c.POINTER(VP)], I32),
+    "glint_plug_streamer_release": ([VP, I32], I32),
+    "glint_plug_streamer_get_stats": ([VP, _c.POINTER(GlintStreamerStats)], I32),
+    "glint_plug_streamer_reset_stats": ([VP], None),
 }
 
 ENCODE_SYMBOLS = tuple(_ENCODE_SIGS)
@@ -225,6 +244,94 @@ def int8_mma_gemm(x, q, scale, n_out: int, k_in: int, xq=None, sx=None, stream=N
     lin = Int8MmaLinear(q.data_ptr(), scale.data_ptr(), n_out, k_in)
     _check(p7_lib().int8_mma_gemm(_p(x), lin, _p(y), m, _p(xq), _p(sx), _stream(stream)), "int8_mma_gemm")
     return y, xq, sx
+
+
+def int8_mma_gemm_plug(x, q, scale, plug_q4, plug_scale, n_out: int, k_in: int, fused: bool = False, stream=None):
+    """The late-plug forms: two passes through int8 scratch (int8_mma_gemm_plug) or one fused
+    kernel (int8_mma_gemm_plug_fused). Returns y f32 [m, n_out]."""
+    torch = _torch()
+    x = _as_u16(x)
+    m = x.numel() // k_in
+    y = torch.empty((m, n_out), dtype=torch.float32, device=x.device)
+    xq = torch.empty(m * k_in, dtype=torch.int8, device=x.device)
+    sx = torch.empty(m * (k_in // 64), dtype=torch.float32, device=x.device)
+    lin = Int8MmaLinear(q.data_ptr(), scale.data_ptr(), n_out, k_in)
+    lib = p7_lib()
+    if fused:
+        _check(lib.int8_mma_gemm_plug_fused(_p(x), lin, _p(plug_q4), _p(plug_scale), _p(y), m, _p(xq), _p(sx),
+                                            _stream(stream)), "int8_mma_gemm_plug_fused")
+    else:
+        pi8 = torch.empty(n_out * k_in, dtype=torch.int8, device=x.device)
+        _check(lib.int8_mma_gemm_plug(_p(x), lin, _p(plug_q4), _p(plug_scale), _p(y), m, _p(xq), _p(sx), _p(pi8),
+                                      _stream(stream)), "int8_mma_gemm_plug")
+    return y
+
+
+def int8_mma_gemm_resolve(x, q, scale, n_out: int, k_in: int, plug_q4=None, plug_scale=None, stream=None):
+    """int8_mma_gemm_resolve: base (+ plug) plus the re-quantized activation residual.
+    Returns (y, xq, sx, rq, sr)."""
+    torch = _torch()
+    x = _as_u16(x)
+    m = x.numel() // k_in
+    dev = x.device
+    y = torch.empty((m, n_out), dtype=torch.float32, device=dev)
+    xq = torch.empty(m * k_in, dtype=torch.int8, device=dev)
+    sx = torch.empty(m * (k_in // 64), dtype=torch.float32, device=dev)
+    rq = torch.empty_like(xq)
+    sr = torch.empty_like(sx)
+    pi8 = torch.empty(n_out * k_in, dtype=torch.int8, device=dev) if plug_q4 is not None else None
+    lin = Int8MmaLinear(q.data_ptr(), scale.data_ptr(), n_out, k_in)
+    opt = lambda t: VP(t.data_ptr()) if t is not None else VP(None)
+    _check(p7_lib().int8_mma_gemm_resolve(_p(x), lin, opt(plug_q4), opt(plug_scale), _p(y), m, _p(xq), _p(sx),
+                                          _p(rq), _p(sr), opt(pi8), _stream(stream)), "int8_mma_gemm_resolve")
+    return y, xq, sx, rq, sr
+
+
+class PlugStreamer:
+    """The 2-slot plug ring (include/glint_plug_streamer.h) over raw device pointers.
+    Methods return the C return codes unchanged."""
+
+    def __init__(self, layer_bytes, copy_stream, compute_stream):
+        self.lib = p7_lib()
+        self.h = VP()
+        n = len(layer_bytes)
+        arr = (ctypes.c_uint64 * n)(*layer_bytes)
+        rc = self.lib.glint_plug_streamer_create(ctypes.byref(self.h), n, arr, VP(copy_stream.cuda_stream),
+                                                 VP(compute_stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"glint_plug_streamer_create rc={rc}")
+
+    def set_host_data(self, layer: int, data: bytes) -> int:
+        buf = ctypes.create_string_buffer(bytes(data), len(data))
+        return self.lib.glint_plug_streamer_set_host_data(self.h, layer, buf, len(data))
+
+    def start(self) -> int:
+        return self.lib.glint_plug_streamer_start(self.h)
+
+    def acquire(self, layer: int):
+        p = VP()
+        rc = self.lib.glint_plug_streamer_acquire(self.h, layer, ctypes.byref(p))
+        return rc, p.value
+
+    def release(self, layer: int) -> int:
+        return self.lib.glint_plug_streamer_release(self.h, layer)
+
+    def stats(self) -> GlintStreamerStats:
+        st = GlintStreamerStats()
+        _check(self.lib.glint_plug_streamer_get_stats(self.h, ctypes.byref(st)), "glint_plug_streamer_get_stats")
+        return st
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.glint_plug_streamer_destroy(self.h)
+            self.h = VP()
+
+
+def p7_selftest():
+    """p7_abi_selftest: (rc, message)."""
+    msg = ctypes.create_string_buffer(512)
+    rc = p7_lib().p7_abi_selftest(msg, 512)
+    return rc, msg.value.decode()
 
 
 def int8_gemm_i32(A, B, stream=None):

@@ -35,6 +35,31 @@ static inline size_t int8_mma_sx_bytes(int m, int k_in) { return (size_t)m * (si
 int int8_mma_gemm(const void *x_bf16, Int8MmaLinear w, float *y, int m, int8_t *xq, float *sx,
                   struct ihipStream_t *stream);
 
+/* Late plug, two passes: y = X (base)^T, then y += X (plug)^T with the same activation
+ * quantization; the plug is a p7_plug_res4_v1 slice (plug_q4: ceil(n_out * k_in / 2) bytes,
+ * element 2i in the low nibble, value nibble - 8; plug_scale: one f32 per 64 weights in the
+ * base's block order) unpacked into plug_i8 (n_out * k_in bytes of caller scratch, 16-B
+ * aligned). Each pass sums its kb terms as int8_mma_gemm does; the second adds into y.
+ * Reference: include/int8_mma_gemm.h:41-47 (cuda/int8_mma_gemm.cu:157-181). */
+int int8_mma_gemm_plug(const void *x_bf16, Int8MmaLinear w, const uint8_t *plug_q4, const float *plug_scale,
+                       float *y, int m, int8_t *xq, float *sx, int8_t *plug_i8, struct ihipStream_t *stream);
+
+/* Late plug in one kernel: per kb, acc = acc + ((float)ic * sx) * sw, then
+ * acc = acc + ((float)ip * sx) * sp, ip the plug slice's dot product (nibbles unpacked in
+ * LDS); no scratch. Reference: include/int8_mma_gemm.h:49-54 (cuda/int8_mma_gemm.cu:224-240). */
+int int8_mma_gemm_plug_fused(const void *x_bf16, Int8MmaLinear w, const uint8_t *plug_q4,
+                             const float *plug_scale, float *y, int m, int8_t *xq, float *sx,
+                             struct ihipStream_t *stream);
+
+/* Resolution: int8_mma_gemm (optionally plus a plug), plus the activation's quantization
+ * residual r = x - (float)xq * sx re-quantized by the same rule into rq/sr (scratch the size
+ * of xq/sx) and multiplied as further accumulating passes: y = xq W, += rq W, and with a plug
+ * += xq P, += rq P. The three plug pointers are all NULL or all set.
+ * Reference: include/int8_mma_gemm.h:56-61 (cuda/int8_mma_gemm.cu:183-222). */
+int int8_mma_gemm_resolve(const void *x_bf16, Int8MmaLinear w, const uint8_t *plug_q4, const float *plug_scale,
+                          float *y, int m, int8_t *xq, float *sx, int8_t *rq, float *sr, int8_t *plug_i8,
+                          struct ihipStream_t *stream);
+
 /* ---- Additive (no reference counterpart): the plain INT8 GEMM of the benchmark config. ----
  * C[m, n] = sum_k A[m, k] * B[n, k] in int32 (exact), A [M, K], B [N, K] row-major int8.
  * Requires K % 64 == 0. */

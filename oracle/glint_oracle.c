@@ -14,7 +14,11 @@
  *                      test_glint_tools.py:31-37; the -0.0 zero-block answer;
  *   oracle_htile_*     float64 brute force and the Python tile simulator order;
  *   oracle_quant_act / oracle_int8_*   exact integer brute force (numpy int64 matmul)
- *                      and rint ties-to-even known answers.
+ *                      and rint ties-to-even known answers; the plug forms by nibble known
+ *                      answers, a zero plug (equal to the base) and power-of-two scales on
+ *                      small integers (every f32 step exact, so fused, two-pass and the
+ *                      integer formula agree bit for bit); the residual by the rounding
+ *                      bound |r - rq sr| <= sr / 2 and the sign of the reconstruction.
  */
 #include <math.h>
 #include <stdint.h>
@@ -221,6 +225,65 @@ EXPORT void oracle_int8_mma_emu(const int8_t *xq, const float *sx, const int8_t 
                 acc += a * sw[(int64_t)j * nkb + kb];
             }
             y[(int64_t)i * n + j] = acc;
+        }
+}
+
+/* p7_plug_res4_v1 slice to int8 (cuda/int8_mma_gemm.cu:157-163): element i is nibble i of
+ * the packed bytes, low nibble first, minus 8. */
+EXPORT void oracle_unpack_res4(const uint8_t *q4, int64_t n, int8_t *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = (int8_t)((int)((q4[i >> 1] >> ((i & 1) * 4)) & 15u) - 8);
+}
+
+/* Fused late plug (cuda/int8_mma_gemm.cu:105-124,224-240): per kb, the base term then the
+ * plug term are added to one accumulator: acc += (ic*sx)*sw; acc += (ip*sx)*sp. */
+EXPORT void oracle_int8_mma_plug_fused(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw,
+                                       const int8_t *pq, const float *sp, int m, int n, int k, float *y) {
+    const int nkb = k / 64;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j) {
+            float acc = 0.f;
+            for (int kb = 0; kb < nkb; ++kb) {
+                int ic = 0, ip = 0;
+                for (int t = 0; t < 64; ++t) {
+                    const int a = xq[(int64_t)i * k + kb * 64 + t];
+                    ic += a * (int)wq[(int64_t)j * k + kb * 64 + t];
+                    ip += a * (int)pq[(int64_t)j * k + kb * 64 + t];
+                }
+                const float xs = sx[(int64_t)i * nkb + kb];
+                acc += ((float)ic * xs) * sw[(int64_t)j * nkb + kb];
+                acc += ((float)ip * xs) * sp[(int64_t)j * nkb + kb];
+            }
+            y[(int64_t)i * n + j] = acc;
+        }
+}
+
+/* Activation quantization residual re-quantized (cuda/int8_mma_gemm.cu:172-190): per (row,
+ * 64-block) r = x - (float)xq * sx as a product then a difference (no fused multiply-add),
+ * s = amax|r| > 0 ? amax / 127 : 1 (NaN skipped), rq = clamp(cvt(rint(r / s)), -127, 127). */
+EXPORT void oracle_quant_act_resid(const uint16_t *x, const int8_t *xq, const float *sx, int m, int k, int8_t *rq,
+                                   float *sr) {
+    const int nkb = k / 64;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int r = 0; r < m; ++r)
+        for (int kb = 0; kb < nkb; ++kb) {
+            const int64_t base = (int64_t)r * k + (int64_t)kb * 64;
+            const float s0 = sx[(int64_t)r * nkb + kb];
+            float res[64], am = 0.f;
+            for (int t = 0; t < 64; ++t) {
+                const float prod = (float)xq[base + t] * s0;
+                res[t] = bf16_to_f32(x[base + t]) - prod;
+                am = fmaxf(am, fabsf(res[t]));
+            }
+            const float s = (am > 0.f) ? (am / 127.f) : 1.f;
+            sr[(int64_t)r * nkb + kb] = s;
+            for (int t = 0; t < 64; ++t) {
+                int v = cvt_s32(rintf(res[t] / s));
+                v = v > 127 ? 127 : (v < -127 ? -127 : v);
+                rq[base + t] = (int8_t)v;
+            }
         }
 }
 

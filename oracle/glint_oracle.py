@@ -215,6 +215,9 @@ class Oracle:
             "oracle_int8_mma_emu": ([vp, vp, vp, vp, i32, i32, i32, vp], None),
             "oracle_int8_gemm_i32": ([vp, vp, i32, i32, i32, i32, i32, vp], None),
             "oracle_int8_scale_bf16": ([vp, vp, vp, i32, i32, vp], None),
+            "oracle_unpack_res4": ([vp, i64, vp], None),
+            "oracle_int8_mma_plug_fused": ([vp, vp, vp, vp, vp, vp, i32, i32, i32, vp], None),
+            "oracle_quant_act_resid": ([vp, vp, vp, i32, i32, vp, vp], None),
             "oracle_threads": ([], i32),
         }
         for name, (args, res) in sig.items():
@@ -285,6 +288,28 @@ class Oracle:
         xq, sx, wq, sw = (np.ascontiguousarray(t) for t in (xq, sx, wq, sw))
         self.lib.oracle_int8_mma_emu(_ptr(xq), _ptr(sx), _ptr(wq), _ptr(sw), m, n, k, _ptr(y))
         return y.reshape(m, n)
+
+    def unpack_res4(self, q4, n: int) -> np.ndarray:
+        q4 = np.ascontiguousarray(q4, np.uint8)
+        out = np.empty(n, np.int8)
+        self.lib.oracle_unpack_res4(_ptr(q4), n, _ptr(out))
+        return out
+
+    def int8_mma_plug_fused(self, xq, sx, wq, sw, pq, sp, m, n, k) -> np.ndarray:
+        arrs = [np.ascontiguousarray(a, t) for a, t in ((xq, np.int8), (sx, np.float32), (wq, np.int8),
+                                                          (sw, np.float32), (pq, np.int8), (sp, np.float32))]
+        y = np.empty(m * n, np.float32)
+        self.lib.oracle_int8_mma_plug_fused(*[_ptr(a) for a in arrs], m, n, k, _ptr(y))
+        return y.reshape(m, n)
+
+    def quant_act_resid(self, x_u16, xq, sx, m: int, k: int):
+        x_u16 = np.ascontiguousarray(x_u16, np.uint16)
+        xq = np.ascontiguousarray(xq, np.int8)
+        sx = np.ascontiguousarray(sx, np.float32)
+        rq = np.empty(m * k, np.int8)
+        sr = np.empty(m * (k // 64), np.float32)
+        self.lib.oracle_quant_act_resid(_ptr(x_u16), _ptr(xq), _ptr(sx), m, k, _ptr(rq), _ptr(sr))
+        return rq, sr
 
     def int8_gemm_i32(self, A, B, M, N, K, row0=0, row1=None) -> np.ndarray:
         row1 = M if row1 is None else row1

@@ -12,7 +12,7 @@ from glint_amd import glint_hip
 ROOT = Path(__file__).resolve().parent.parent
 HEADERS = {
     "libglint_encode.so": ["glint_encode.h", "glint_htile.h"],
-    "libp7_kernels.so": ["int8_mma_gemm.h", "p7_attach.h"],
+    "libp7_kernels.so": ["int8_mma_gemm.h", "p7_attach.h", "glint_plug_streamer.h"],
 }
 
 
@@ -53,7 +53,13 @@ def test_reference_symbol_set_present():
               "launch_glint_htile_s3_f32_stream", "launch_glint_htile_s3_f32"):
         assert s in enc, s
     p7 = exported(glint_hip.LIB_DIR / "libp7_kernels.so")
-    for s in ("p7_abi_version", "int8_mma_gemm", "p7_int8_gemm_flat"):
+    # the twelve symbols cuda/p7_attach_check.c:11-14 requires, plus the rest of the attach contract
+    for s in ("p7_abi_version", "p7_abi_selftest", "int8_mma_gemm", "glint_plug_streamer_create",
+              "glint_plug_streamer_set_host_data", "glint_plug_streamer_start", "glint_plug_streamer_acquire",
+              "glint_plug_streamer_release", "glint_plug_streamer_get_stats", "glint_plug_streamer_destroy",
+              "p7_int8_gemm_flat", "p7_int8_gemm_plug_flat",
+              "int8_mma_gemm_plug", "int8_mma_gemm_plug_fused", "int8_mma_gemm_resolve",
+              "glint_plug_streamer_reset_stats"):
         assert s in p7, s
 
 
@@ -83,6 +89,23 @@ def test_bad_arguments_rejected_without_a_device():
     assert p7.int8_mma_gemm(one, bad, one, 1, one, one, null) == 1
     assert p7.p7_int8_gemm_flat(one, one, one, 64, 96, one, 1, one, one, null) == 1
     assert p7.glint_int8_gemm_i32(one, one, one, 4, 4, 100, null) == 1
+    ok = glint_hip.Int8MmaLinear(16, 16, 64, 128)
+    x16 = ctypes.c_void_p(16)
+    assert p7.int8_mma_gemm_plug(x16, ok, null, one, one, 1, x16, one, x16, null) == 1  # plug missing
+    assert p7.int8_mma_gemm_plug_fused(one, bad, one, one, one, 1, one, one, null) == 1
+    assert p7.p7_int8_gemm_plug_flat(one, one, one, one, one, 64, 96, one, 1, one, one, null) == 1
+    # resolve: the three plug pointers must be all set or all NULL (int8_mma_gemm.h:56-61)
+    assert p7.int8_mma_gemm_resolve(x16, ok, one, null, one, 1, x16, one, x16, one, x16, null) == 1
+    # streamer argument checks come before any device call (glint_plug_streamer.h codes)
+    h = ctypes.c_void_p()
+    sizes = (ctypes.c_uint64 * 1)(16)
+    assert p7.glint_plug_streamer_create(ctypes.byref(h), 0, sizes, null, null) == -1
+    assert p7.glint_plug_streamer_create(ctypes.byref(h), 65, sizes, null, null) == -1
+    assert p7.glint_plug_streamer_start(null) == -1
+    assert p7.glint_plug_streamer_release(null, 0) == -1
+    p = ctypes.c_void_p()
+    assert p7.glint_plug_streamer_acquire(null, 0, ctypes.byref(p)) == -1
+    assert p7.glint_plug_streamer_set_host_data(null, 0, one, 16) == -1
 
 
 def test_drop_in_module_surface():

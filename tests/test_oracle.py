@@ -316,6 +316,88 @@ def test_int8_scale_bf16_special_cases(oracle):
     assert np.array_equal(zero, np.where(C < 0, 0x8000, 0).astype(np.uint16))
 
 
+def test_unpack_res4_known_answers(oracle):
+    """p7_plug_res4_v1 (tools/plug_encode.c:3-6): element 2i in the low nibble, biased +8."""
+    got = oracle.unpack_res4(np.array([0x80, 0x0F, 0x88, 0x79, 0xF1], np.uint8), 10)
+    assert got.tolist() == [-8, 0, 7, -8, 0, 0, 1, -1, -7, 7]
+    assert oracle.unpack_res4(np.array([0x3C], np.uint8), 1).tolist() == [4]  # odd n: high nibble unused
+
+
+def _small_int8_case(rng, m, n, k, lo=-3, hi=4):
+    nkb = k // 64
+    xq = rng.integers(lo, hi, m * k).astype(np.int8)
+    wq = rng.integers(lo, hi, n * k).astype(np.int8)
+    pq = rng.integers(-7, 8, n * k).astype(np.int8)
+    sx = (2.0 ** rng.integers(-2, 3, m * nkb)).astype(np.float32)
+    sw = (2.0 ** rng.integers(-2, 3, n * nkb)).astype(np.float32)
+    sp = (2.0 ** rng.integers(-2, 3, n * nkb)).astype(np.float32)
+    return xq, sx, wq, sw, pq, sp
+
+
+def _exact_formula(xq, sx, wq, sw, m, n, k):
+    """sum_kb ic_kb * sx * sw in float64 (exact for the small-integer, power-of-two cases)."""
+    nkb = k // 64
+    X = xq.astype(np.int64).reshape(m, nkb, 64)
+    W = wq.astype(np.int64).reshape(n, nkb, 64)
+    ic = np.einsum("mbt,nbt->mnb", X, W).astype(np.float64)
+    return (ic * sx.reshape(m, 1, nkb) * sw.reshape(1, n, nkb)).sum(axis=2)
+
+
+def test_plug_forms_exact_on_power_of_two_scales(oracle):
+    """With small integers and power-of-two scales every f32 step is exact, so the fused
+    late plug, the two-pass plug (base pass + plug pass added) and the integer formula
+    agree bit for bit; a transposed scale or a plug on the wrong operand would not."""
+    rng = np.random.default_rng(11)
+    m, n, k = 5, 7, 256
+    xq, sx, wq, sw, pq, sp = _small_int8_case(rng, m, n, k)
+    want = _exact_formula(xq, sx, wq, sw, m, n, k) + _exact_formula(xq, sx, pq, sp, m, n, k)
+    fused = oracle.int8_mma_plug_fused(xq, sx, wq, sw, pq, sp, m, n, k)
+    two = oracle.int8_mma_emu(xq, sx, wq, sw, m, n, k) + oracle.int8_mma_emu(xq, sx, pq, sp, m, n, k)
+    assert np.array_equal(fused.astype(np.float64), want)
+    assert np.array_equal(two.astype(np.float64), want)
+
+
+def test_zero_plug_equals_base(oracle):
+    """Nibbles 0x88 decode to 0: both plug forms reproduce the base bit for bit."""
+    rng = np.random.default_rng(12)
+    m, n, k = 6, 9, 192
+    xq = rng.integers(-127, 128, m * k).astype(np.int8)
+    wq = rng.integers(-127, 128, n * k).astype(np.int8)
+    sx = rng.uniform(1e-3, 2e-2, m * k // 64).astype(np.float32)
+    sw = rng.uniform(1e-3, 2e-2, n * k // 64).astype(np.float32)
+    sp = rng.uniform(1e-3, 2e-2, n * k // 64).astype(np.float32)
+    pq = oracle.unpack_res4(np.full(n * k // 2, 0x88, np.uint8), n * k)
+    base = oracle.int8_mma_emu(xq, sx, wq, sw, m, n, k)
+    assert np.array_equal(oracle.int8_mma_plug_fused(xq, sx, wq, sw, pq, sp, m, n, k), base)
+    assert np.array_equal(base + oracle.int8_mma_emu(xq, sx, pq, sp, m, n, k), base)
+
+
+def test_quant_act_resid_pins(oracle):
+    """The residual r = x - xq sx re-quantized: (1) a block on the quantization grid has
+    r = 0 exactly (rq = 0, sr = 1); (2) elsewhere |r - rq sr| <= sr / 2 (rounding), so the
+    two-level reconstruction xq sx + rq sr is ~127x closer to x than xq sx alone; a sign
+    flip of r or a scale from the wrong block breaks both."""
+    grid = (np.arange(-127, 128, 4)[:64] * 2.0 ** -7).astype(np.float32)  # 64 values, amax 125 * 2^-7
+    grid[0] = 127 * 2.0 ** -7
+    rng = np.random.default_rng(13)
+    m, k = 9, 320
+    x = rng.normal(0, 1, m * k).astype(np.float32)
+    x[:64] = grid
+    u16 = G.f32_to_bf16_bits(x)
+    xq, sx = oracle.quant_act(u16, m, k)
+    rq, sr = oracle.quant_act_resid(u16, xq, sx, m, k)
+    assert np.all(rq[:64] == 0) and sr[0] == 1.0
+    xf = G.bf16_bits_to_f32(u16).astype(np.float64)
+    blk = np.repeat(np.arange(m * k // 64), 64)
+    r = xf - xq.astype(np.float64) * sx[blk]
+    err2 = np.abs(r - rq.astype(np.float64) * sr[blk])
+    # rounding of rint, plus the f32 evaluation of r (a rounded product, a rounded difference)
+    f32_r = 2.0 ** -23 * np.maximum(np.abs(xf), np.abs(xq.astype(np.float64) * sx[blk]))
+    assert np.all(err2 <= sr[blk] * (0.5 + 1e-6) + f32_r)
+    e1, e2 = np.abs(r).max(), err2.max()
+    assert e2 * 60 < e1, (e1, e2)
+
+
 # ------------------------------------------------------- the pins catch planted mistakes
 def test_planted_mistakes_are_caught():
     """Mutations of the numpy oracle that a plausible bug would introduce must fail
