@@ -539,6 +539,134 @@ __global__ __launch_bounds__(256) void k_htile_mfma_b64(const glint_u32x4 *__res
             }
 }
 
+/* Prefill GEMM, large M: block tile 256 (M) x 128 (N) x 64 (K), 512 threads = 8 waves in
+ * 4 (M) x 2 (N), wave tile 64 x 64 = 4 x 4 MFMA tiles (v_mfma_f32_16x16x32_bf16, two K halves
+ * per step). LDS holds the 32-copy cell table and two buffers of the x and W tiles, so each
+ * K step needs one barrier: the waves run the MFMAs of buffer kb & 1 while they dequantize
+ * the next W tile (loaded from HBM one step ahead) into the other buffer. Per step a thread
+ * dequantizes 16 weights of one row (8 B of each plane) and stages 64 B of x. */
+#define MF2_BM 256
+#define MF2_BN 128
+#define MF2_THREADS 512
+#define MF2_LDW 80 /* 64 + 16 bf16 per LDS row: measured 4x fewer bank-conflict cycles than 72 */
+#ifndef MF2_MIN_M
+#define MF2_MIN_M 256 /* smallest M that takes the 256 x 128 tiles */
+#endif
+
+
+__global__ __launch_bounds__(MF2_THREADS) void k_htile_mfma2(const glint_u32x2 *__restrict__ hole,
+                                                             const glint_u32x2 *__restrict__ plug,
+                                                             const float *__restrict__ absmax,
+                                                             const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
+                                                             int M, int N, int K) {
+    __shared__ float ltab[GLINT_LDS_CELLS_WORDS];
+    __shared__ float stage[256];
+    __shared__ __attribute__((aligned(16))) uint16_t sX[2][MF2_BM * MF2_LDW];
+    __shared__ __attribute__((aligned(16))) uint16_t sW[2][MF2_BN * MF2_LDW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * MF2_BM, n0 = blockIdx.x * MF2_BN;
+    const uint32_t lb = lane & 31;
+    const int nK = K >> 6;
+    /* producer roles: W row wr (0..127), 16-element quarter wq; x rows xr + 64 i, 8-col chunk xc */
+    const int wr = tid >> 2, wq = tid & 3;
+    const int xr = tid >> 3, xc = tid & 7;
+    const int wrow = n0 + wr;
+    glint_f32x4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
+
+    glint_u32x2 hv, pv;
+    float av;
+    glint_u32x4 xv[4];
+    auto gload = [&](int kb) {
+        if (wrow < N) {
+            const int64_t q = (int64_t)wrow * (K >> 4) + kb * 4 + wq; /* 16-element groups */
+            hv = __builtin_nontemporal_load(&hole[q]);
+            pv = __builtin_nontemporal_load(&plug[q]);
+            av = absmax[(int64_t)wrow * (K >> 6) + kb];
+        } else {
+            hv = pv = glint_u32x2{0u, 0u};
+            av = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = m0 + xr + 64 * i;
+            xv[i] = (m < M) ? *(const glint_u32x4 *)(x + (int64_t)m * K + (int64_t)kb * 64 + xc * 8)
+                            : glint_u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto produce = [&](int buf) {
+        const uint32_t H[2] = {hv.x, hv.y}, P[2] = {pv.x, pv.y};
+        uint32_t packed[8];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t E = glint_codes_even(H[q], P[q]);
+            const uint32_t O = glint_codes_odd(H[q], P[q]);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const float ve = ltab[(((E >> (8 * b)) & 0xFFu) << 5) | lb] * av;
+                const float vo = ltab[(((O >> (8 * b)) & 0xFFu) << 5) | lb] * av;
+                packed[4 * q + b] = glint_cvt_bf16x2(ve, vo);
+            }
+        }
+        glint_u32x4 *dst = (glint_u32x4 *)(sW[buf] + wr * MF2_LDW + wq * 16);
+        dst[0] = glint_u32x4{packed[0], packed[1], packed[2], packed[3]};
+        dst[1] = glint_u32x4{packed[4], packed[5], packed[6], packed[7]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *(glint_u32x4 *)(sX[buf] + (xr + 64 * i) * MF2_LDW + xc * 8) = xv[i];
+    };
+
+    glint_fill_cells_lds(ltab, stage);
+    gload(0);
+    produce(0);
+    if (nK > 1)
+        gload(1);
+    __syncthreads();
+    for (int kb = 0; kb < nK; ++kb) {
+        const int cur = kb & 1;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int kofs = ks * 32 + (lane >> 4) * 8;
+            glint_bf16x8 af[4], bfr[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+                af[a] = __builtin_bit_cast(
+                    glint_bf16x8, *(const glint_u32x4 *)(sX[cur] + (wm * 64 + a * 16 + (lane & 15)) * MF2_LDW + kofs));
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                bfr[b] = __builtin_bit_cast(
+                    glint_bf16x8, *(const glint_u32x4 *)(sW[cur] + (wn * 64 + b * 16 + (lane & 15)) * MF2_LDW + kofs));
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
+        }
+        if (kb + 1 < nK) {
+            produce(cur ^ 1);
+            if (kb + 2 < nK)
+                gload(kb + 2);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm * 64 + a * 16 + (lane >> 4) * 4 + i;
+                const int n = n0 + wn * 64 + b * 16 + (lane & 15);
+                if (m < M && n < N)
+                    y[(int64_t)m * N + n] = glint_f32_to_bf16(acc[a][b][i]);
+            }
+}
+
 /* ------------------------------------------------------------------ dispatch */
 /* One resident wave of workgroups (every CU filled to its occupancy limit), or fewer if
  * there are fewer wave tasks; the waves then loop over their tasks. */
@@ -567,6 +695,9 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         if (M <= 64) {
             k_htile_mfma_b64<64><<<dim3(gx, (M + 63) / 64), 256, 0, st>>>(
                 (const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
+        } else if (M >= MF2_MIN_M) {
+            k_htile_mfma2<<<dim3((N + MF2_BN - 1) / MF2_BN, (M + MF2_BM - 1) / MF2_BM), MF2_THREADS, 0, st>>>(
+                (const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
         } else {
             k_htile_mfma_b64<128><<<dim3(gx, (M + 127) / 128), 256, 0, st>>>(
                 (const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
