@@ -301,6 +301,25 @@ def bench_int8(torch, H, steps: int):
     return {"ms": ms, "tops": ops / ms / 1e9, "mfma_frac": ops / ms / 1e9 / I8_PEAK_TOPS, "shape": [M, N, K]}
 
 
+def bench_w8a16(torch, H, steps: int):
+    """int8_tile_gemm_bf16 (W8A16 over an INT8 pin linear): HBM-bound decode shapes and the
+    MFMA-bound 2048 x 8192 x 8192 shape of the INT8 config."""
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(6001)
+    for M, N, K in ((1, 14336, 4096), (64, 14336, 4096), (2048, 8192, 8192)):
+        q = torch.randint(-127, 128, (N * K,), device="cuda", generator=g, dtype=torch.int8)
+        sc = torch.rand(N * K // 64, device="cuda", generator=g) * 0.02 + 1e-3
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        y = torch.empty(M, N, dtype=torch.float32, device="cuda")
+        ms = timed(torch, [lambda: H.int8_tile_gemm(x, q, sc, N, K, y=y)], steps, 2)
+        fl = 2.0 * M * N * K
+        byt = N * K * (1 + 4 / 64) + 2 * M * K + 4 * M * N
+        out[f"M{M}_{N}x{K}"] = {"ms": ms, "tflops": fl / ms / 1e9, "mfma_frac": fl / ms / 1e9 / BF16_PEAK_TFLOPS,
+                                "eff_gbs": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS}
+        del q, sc, x, y
+    return out
+
+
 def cpu_baseline(seconds_target: float = 20.0):
     """The CPU path beside the GPU, on this host: the repo's C restatement of the reference
     host path (oracle/glint_oracle.c, OpenMP over the threads it reports) running the
@@ -351,7 +370,7 @@ def cpu_baseline(seconds_target: float = 20.0):
 
 
 # ---------------------------------------------------------------- profile summaries
-GEMV_KERNEL = "k_htile_gemv_xreg<true>"
+GEMV_KERNEL = "k_htile_gemv_xreg<32,true,"  # headline dispatch (bf16 out), spaces removed
 TRAFFIC_JSON = ROOT / "profiles" / "htile_gemv_m1_14336x4096.traffic.json"
 PMC_CMD = ("rocprofv3 --pmc {ctr} -d <dir> -o run -- python3 bench.py --quick --no-cpu --headline-only "
            "--calibrate-copy --steps 20 --warmup 5")
@@ -481,6 +500,8 @@ def main() -> int:
         log("prefill done")
         extra["int8_gemm"] = bench_int8(torch, H, steps=10)
         log(f"int8 {extra['int8_gemm']['tops']:.0f} TOPS")
+        extra["w8a16"] = bench_w8a16(torch, H, steps=10)
+        log("w8a16 done")
         extra["host_abi_pcie"] = bench_host_abi(H)
         log(f"host ABI encode {extra['host_abi_pcie']['encode_bf16_in_gbs']:.1f} GB/s bf16-in (PCIe inclusive)")
     cpu = None if args.no_cpu else cpu_baseline()

@@ -12,13 +12,18 @@
  *   read, 1 f32 FMA; per row one FMA by the block absmax and 4 DPP adds.
  * k_htile_gemv_b64 — decode for the other K % 64 == 0: x staged in LDS as f32 planes,
  *   (task, step) items double-buffered in registers.
- * k_htile_mfma_b64 — prefill (M > 1, bf16 out, bs = 64): BF16 MFMA on LDS-dequantized
- *   weight tiles, f32 accumulation.
+ * k_tile_mfma<..., GlintTileProducer> (tile_mfma.h) — prefill (M > 1, bf16 out, bs = 64): BF16
+ *   MFMA on double-buffered LDS-dequantized weight tiles, f32 accumulation; 256 x 128 tiles
+ *   over 8 waves for M >= 256, 128 x 64 / 64 x 64 over 4 waves below. The tile kernel is
+ *   shared with the INT8-pin W8A16 GEMM.
  * k_htile_generic — every other shape (any M, K, bs, alignment): 64x32 output tiles,
  *   weights decoded to f32 in LDS per 32-wide K step, f32 FMAs in k order.
  */
+#include <algorithm>
+
 #include "glint_common.h"
 #include "glint_htile.h"
+#include "tile_mfma.h"
 
 /* ---------------------------------------------------------------- GEMV (M = 1) */
 #ifndef GEMV_R
@@ -244,12 +249,49 @@ __device__ __forceinline__ uint32_t gemv_word(const typename GemvVec<EL>::T &v, 
     return v[q];
 }
 
-template <int EL, bool OUT_BF16>
+/* The 64-copy cell table through the scalar path: run r (16 B, 4 copies of cell r >> 4) of
+ * thread t is t + k blockDim.x, so a wave's 64 runs of step k hold the 4 cells starting at
+ * (wave base + k blockDim.x) / 16, one s_load_dwordx4 per step (blockDim.x % 16 == 0).
+ * Scalar loads do not queue behind the wave's vector loads of weight rows. 13 steps cover
+ * the 4096 runs for blockDim.x >= 316; a loop covers smaller blocks. */
+#define GLINT_FILL_STEPS 13
+struct GlintCellFillS {
+    glint_f32x4 c[GLINT_FILL_STEPS]; /* wave-uniform: lands in scalar registers */
+};
+__device__ __forceinline__ void glint_cells_fill_sload(GlintCellFillS &f) {
+    const int wbase = __builtin_amdgcn_readfirstlane((int)threadIdx.x & ~63);
+#pragma unroll
+    for (int k = 0; k < GLINT_FILL_STEPS; ++k) {
+        const int c0 = min((wbase + k * (int)blockDim.x) >> 4, 252);
+        f.c[k] = *(const glint_f32x4 *)(&kCells[0][0] + c0);
+    }
+}
+__device__ __forceinline__ void glint_cells_fill_sstore(float *ltab, const GlintCellFillS &f) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const bool odd = (threadIdx.x >> 4) & 1, high = (threadIdx.x >> 5) & 1; /* cell c0 + (lane >> 4) */
+#pragma unroll
+    for (int k = 0; k < GLINT_FILL_STEPS; ++k) {
+        const int r = (int)threadIdx.x + k * (int)blockDim.x;
+        const float lo = odd ? f.c[k].y : f.c[k].x, hi = odd ? f.c[k].w : f.c[k].z;
+        const float v = high ? hi : lo;
+        if (r < GLINT_LDS_CELLS64_WORDS / 4)
+            ((f32x4 *)ltab)[r] = f32x4{v, v, v, v};
+    }
+    for (int r = threadIdx.x + GLINT_FILL_STEPS * blockDim.x; r < GLINT_LDS_CELLS64_WORDS / 4; r += blockDim.x) {
+        const float v = (&kCells[0][0])[r >> 4];
+        ((f32x4 *)ltab)[r] = f32x4{v, v, v, v};
+    }
+}
+
+/* XC > 0: x goes through LDS. Thread t loads 16-B chunks t + c blockDim.x (c < XC, which is
+ * K / 8 / blockDim.x exactly), the G waves of a slice then read it from LDS instead of each
+ * loading it from L2. XC == 0: each wave loads its slice itself (G == 1, no repeats). */
+template <int EL, bool OUT_BF16, int XC>
 __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE))) void k_htile_gemv_xreg(
     const void *__restrict__ hole, const void *__restrict__ plug, const float *__restrict__ absmax,
     const glint_u32x4 *__restrict__ x, void *__restrict__ y, int N, int K, int G, int rows_per_wg) {
     __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS]; /* 64 KiB at LDS offset 0 */
-    extern __shared__ float red[];                                              /* [rows_per_wg][S][4] */
+    extern __shared__ __attribute__((aligned(16))) float red[]; /* [rows_per_wg][S][4]; first x when XC > 0 */
     constexpr int Q = EL / 8; /* 8-element groups per chunk = packed words per plane */
 
     const int lane = threadIdx.x & 63;
@@ -260,25 +302,42 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
     const int r0 = blockIdx.x * rows_per_wg;
     const int nrows = max(min(rows_per_wg, N - r0), 0);
     const int my = g < nrows ? (nrows - g + G - 1) / G : 0; /* rows r0 + g + i G, i < my */
-    const uint32_t j = (uint32_t)(s * 64 + lane);
     /* row of item i, clamped into the matrix (a clamped reload is never used) */
     auto row_of = [&](int i) -> int64_t { return (int64_t)min(r0 + g + min(i, max(my - 1, 0)) * G, N - 1); };
+    const uint32_t j = (uint32_t)(s * 64 + lane);
 
     /* Loads go out in the order they are consumed (the wait counter is in order): the
      * cell table, x, then the first rows; the table's LDS writes follow. */
-    GlintCellFill fill;
-    glint_cells_fill_load(fill);
-    glint_u32x4 xv[Q];
+    GlintCellFillS fill;
+    glint_cells_fill_sload(fill);
+    glint_u32x4 xv[XC > Q ? XC : Q];
+    if (XC > 0) {
 #pragma unroll
-    for (int q = 0; q < Q; ++q)
-        xv[q] = x[j * Q + q];
+        for (int c = 0; c < XC; ++c)
+            xv[c] = x[threadIdx.x + c * blockDim.x];
+    } else {
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+            xv[q] = x[j * Q + q];
+    }
     __builtin_amdgcn_sched_barrier(0);
     GemvRow<EL> buf[GEMV_X_DEPTH];
 #pragma unroll
     for (int d = 0; d < GEMV_X_PRE; ++d)
         gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, j, buf[d]);
     __builtin_amdgcn_sched_barrier(0);
-    glint_cells_fill_store(ltab, fill);
+    glint_cells_fill_sstore(ltab, fill);
+    if (XC > 0) {
+#pragma unroll
+        for (int c = 0; c < XC; ++c)
+            ((glint_u32x4 *)red)[threadIdx.x + c * blockDim.x] = xv[c];
+    }
+    __syncthreads();
+    if (XC > 0) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+            xv[q] = ((const glint_u32x4 *)red)[j * Q + q];
+    }
     float xr[EL];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
@@ -288,7 +347,8 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
         xr[8 * q + 4] = glint_bf16lo(v.z); xr[8 * q + 5] = glint_bf16hi(v.z);
         xr[8 * q + 6] = glint_bf16lo(v.w); xr[8 * q + 7] = glint_bf16hi(v.w);
     }
-    __syncthreads();
+    if (XC > 0)
+        __syncthreads(); /* x is read out before the row partials reuse its LDS */
 #pragma unroll
     for (int d = GEMV_X_PRE; d < GEMV_X_DEPTH; ++d)
         gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, j, buf[d]);
@@ -334,13 +394,14 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
     __syncthreads();
 
     for (int t = threadIdx.x; t < nrows; t += blockDim.x) {
+        const int row = r0 + t;
         float sum = 0.0f;
         for (int k = 0; k < S * 4; ++k)
             sum += red[t * S * 4 + k];
         if (OUT_BF16)
-            ((uint16_t *)y)[r0 + t] = glint_f32_to_bf16(sum);
+            ((uint16_t *)y)[row] = glint_f32_to_bf16(sum);
         else
-            ((float *)y)[r0 + t] = sum;
+            ((float *)y)[row] = sum;
     }
 }
 
@@ -412,260 +473,14 @@ __global__ __launch_bounds__(256) void k_htile_generic(const uint8_t *__restrict
 }
 
 /* ---------------------------------------------------- prefill GEMM on BF16 MFMA */
-/* y[M, N] (bf16) = x[M, K] W^T for bs = 64, K % 64 == 0. Block tile BM x 128 x 64 (K);
- * 4 waves in 2 x 2, wave tile (BM/2) x 64 = (BM/32) x 4 MFMA tiles of 16x16
- * (v_mfma_f32_16x16x32_bf16, two K halves per step). Per K step each thread turns 32
- * packed weights of one row (16 B of each plane) into BF16 RNE(cell * absmax) through
- * the bank-private LDS table and writes them to the W tile; the next step's planes and
- * x tile are loaded from HBM while the MFMAs run. LDS rows are padded by 8 BF16 so the
- * 16 rows read by one MFMA operand load fall in distinct bank groups. */
-typedef __bf16 glint_bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 glint_bf16x2 __attribute__((ext_vector_type(2)));
-typedef float glint_f32x2 __attribute__((ext_vector_type(2)));
-
-#define MF_BN 128
-#define MF_LDW 72 /* 64 + 8 bf16 per LDS row */
-
-__device__ __forceinline__ uint32_t glint_cvt_bf16x2(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(glint_f32x2{lo, hi}, glint_bf16x2));
-}
-
-template <int BM>
-__global__ __launch_bounds__(256) void k_htile_mfma_b64(const glint_u32x4 *__restrict__ hole,
-                                                        const glint_u32x4 *__restrict__ plug,
-                                                        const float *__restrict__ absmax, const uint16_t *__restrict__ x,
-                                                        uint16_t *__restrict__ y, int M, int N, int K) {
-    constexpr int WM = BM / 2, TM = WM / 16, XV = BM / 32; /* x u32x4 loads per thread */
-    __shared__ float ltab[GLINT_LDS_CELLS_WORDS];
-    __shared__ float stage[256];
-    __shared__ __attribute__((aligned(16))) uint16_t sX[BM * MF_LDW];
-    __shared__ __attribute__((aligned(16))) uint16_t sW[MF_BN * MF_LDW];
-    glint_fill_cells_lds(ltab, stage);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * MF_BN;
-    const uint32_t lb = lane & 31;
-    const int nK = K >> 6;
-    /* staging roles: weights row wr = tid >> 1, K half wh = tid & 1 (32 elements) */
-    const int wr = tid >> 1, wh = tid & 1;
-    const int wn_row = n0 + wr;
-    glint_f32x4 acc[TM][4];
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-            acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
-
-    glint_u32x4 hv, pv, xv[XV];
-    float av;
-    auto gload = [&](int kb) {
-        if (wn_row < N) {
-            const int64_t q = (int64_t)wn_row * (K >> 5) + kb * 2 + wh; /* 32-element groups */
-            hv = __builtin_nontemporal_load(&hole[q]);
-            pv = __builtin_nontemporal_load(&plug[q]);
-            av = absmax[(int64_t)wn_row * (K >> 6) + kb];
-        } else {
-            hv = pv = glint_u32x4{0u, 0u, 0u, 0u};
-            av = 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < XV; ++i) {
-            const int idx = tid + 256 * i, xr = idx >> 3, xc = idx & 7;
-            const int m = m0 + xr;
-            xv[i] = (m < M) ? *(const glint_u32x4 *)(x + (int64_t)m * K + (int64_t)kb * 64 + xc * 8)
-                            : glint_u32x4{0u, 0u, 0u, 0u};
-        }
-    };
-    gload(0);
-    for (int kb = 0; kb < nK; ++kb) {
-        /* dequantize this thread's 32 weights and stage x */
-        {
-            const uint32_t H[4] = {hv.x, hv.y, hv.z, hv.w}, P[4] = {pv.x, pv.y, pv.z, pv.w};
-            uint32_t packed[16];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t E = ((H[q] << 4) & 0xF0F0F0F0u) | (P[q] & 0x0F0F0F0Fu);
-                const uint32_t O = (H[q] & 0xF0F0F0F0u) | ((P[q] >> 4) & 0x0F0F0F0Fu);
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const float ve = ltab[(((E >> (8 * b)) & 0xFFu) << 5) | lb] * av;
-                    const float vo = ltab[(((O >> (8 * b)) & 0xFFu) << 5) | lb] * av;
-                    packed[4 * q + b] = glint_cvt_bf16x2(ve, vo);
-                }
-            }
-            glint_u32x4 *dst = (glint_u32x4 *)(sW + wr * MF_LDW + wh * 32);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                dst[i] = glint_u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
-#pragma unroll
-            for (int i = 0; i < XV; ++i) {
-                const int idx = tid + 256 * i, xr = idx >> 3, xc = idx & 7;
-                *(glint_u32x4 *)(sX + xr * MF_LDW + xc * 8) = xv[i];
-            }
-        }
-        __syncthreads();
-        if (kb + 1 < nK)
-            gload(kb + 1);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int kofs = ks * 32 + (lane >> 4) * 8;
-            glint_bf16x8 af[TM], bfr[4];
-#pragma unroll
-            for (int a = 0; a < TM; ++a)
-                af[a] = __builtin_bit_cast(glint_bf16x8,
-                                           *(const glint_u32x4 *)(sX + (wm * WM + a * 16 + (lane & 15)) * MF_LDW + kofs));
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                bfr[b] = __builtin_bit_cast(glint_bf16x8,
-                                            *(const glint_u32x4 *)(sW + (wn * 64 + b * 16 + (lane & 15)) * MF_LDW + kofs));
-#pragma unroll
-            for (int a = 0; a < TM; ++a)
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = m0 + wm * WM + a * 16 + (lane >> 4) * 4 + i;
-                const int n = n0 + wn * 64 + b * 16 + (lane & 15);
-                if (m < M && n < N)
-                    y[(int64_t)m * N + n] = glint_f32_to_bf16(acc[a][b][i]);
-            }
-}
-
-/* Prefill GEMM, large M: block tile 256 (M) x 128 (N) x 64 (K), 512 threads = 8 waves in
- * 4 (M) x 2 (N), wave tile 64 x 64 = 4 x 4 MFMA tiles (v_mfma_f32_16x16x32_bf16, two K halves
- * per step). LDS holds the 32-copy cell table and two buffers of the x and W tiles, so each
- * K step needs one barrier: the waves run the MFMAs of buffer kb & 1 while they dequantize
- * the next W tile (loaded from HBM one step ahead) into the other buffer. Per step a thread
- * dequantizes 16 weights of one row (8 B of each plane) and stages 64 B of x. */
+/* Prefill GEMM, large M: the shared double-buffered tile kernel with 256 (M) x 128 (N)
+ * blocks over 8 waves in 4 x 2 (wave tile 64 x 64); each thread dequantizes 16 weights
+ * (8 B of each plane) per K step through the 32-copy cell table. */
 #define MF2_BM 256
 #define MF2_BN 128
-#define MF2_THREADS 512
-#define MF2_LDW 80 /* 64 + 16 bf16 per LDS row: measured 4x fewer bank-conflict cycles than 72 */
 #ifndef MF2_MIN_M
 #define MF2_MIN_M 256 /* smallest M that takes the 256 x 128 tiles */
 #endif
-
-
-__global__ __launch_bounds__(MF2_THREADS) void k_htile_mfma2(const glint_u32x2 *__restrict__ hole,
-                                                             const glint_u32x2 *__restrict__ plug,
-                                                             const float *__restrict__ absmax,
-                                                             const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
-                                                             int M, int N, int K) {
-    __shared__ float ltab[GLINT_LDS_CELLS_WORDS];
-    __shared__ float stage[256];
-    __shared__ __attribute__((aligned(16))) uint16_t sX[2][MF2_BM * MF2_LDW];
-    __shared__ __attribute__((aligned(16))) uint16_t sW[2][MF2_BN * MF2_LDW];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * MF2_BM, n0 = blockIdx.x * MF2_BN;
-    const uint32_t lb = lane & 31;
-    const int nK = K >> 6;
-    /* producer roles: W row wr (0..127), 16-element quarter wq; x rows xr + 64 i, 8-col chunk xc */
-    const int wr = tid >> 2, wq = tid & 3;
-    const int xr = tid >> 3, xc = tid & 7;
-    const int wrow = n0 + wr;
-    glint_f32x4 acc[4][4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-            acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
-
-    glint_u32x2 hv, pv;
-    float av;
-    glint_u32x4 xv[4];
-    auto gload = [&](int kb) {
-        if (wrow < N) {
-            const int64_t q = (int64_t)wrow * (K >> 4) + kb * 4 + wq; /* 16-element groups */
-            hv = __builtin_nontemporal_load(&hole[q]);
-            pv = __builtin_nontemporal_load(&plug[q]);
-            av = absmax[(int64_t)wrow * (K >> 6) + kb];
-        } else {
-            hv = pv = glint_u32x2{0u, 0u};
-            av = 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m0 + xr + 64 * i;
-            xv[i] = (m < M) ? *(const glint_u32x4 *)(x + (int64_t)m * K + (int64_t)kb * 64 + xc * 8)
-                            : glint_u32x4{0u, 0u, 0u, 0u};
-        }
-    };
-    auto produce = [&](int buf) {
-        const uint32_t H[2] = {hv.x, hv.y}, P[2] = {pv.x, pv.y};
-        uint32_t packed[8];
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const uint32_t E = glint_codes_even(H[q], P[q]);
-            const uint32_t O = glint_codes_odd(H[q], P[q]);
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const float ve = ltab[(((E >> (8 * b)) & 0xFFu) << 5) | lb] * av;
-                const float vo = ltab[(((O >> (8 * b)) & 0xFFu) << 5) | lb] * av;
-                packed[4 * q + b] = glint_cvt_bf16x2(ve, vo);
-            }
-        }
-        glint_u32x4 *dst = (glint_u32x4 *)(sW[buf] + wr * MF2_LDW + wq * 16);
-        dst[0] = glint_u32x4{packed[0], packed[1], packed[2], packed[3]};
-        dst[1] = glint_u32x4{packed[4], packed[5], packed[6], packed[7]};
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *(glint_u32x4 *)(sX[buf] + (xr + 64 * i) * MF2_LDW + xc * 8) = xv[i];
-    };
-
-    glint_fill_cells_lds(ltab, stage);
-    gload(0);
-    produce(0);
-    if (nK > 1)
-        gload(1);
-    __syncthreads();
-    for (int kb = 0; kb < nK; ++kb) {
-        const int cur = kb & 1;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int kofs = ks * 32 + (lane >> 4) * 8;
-            glint_bf16x8 af[4], bfr[4];
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-                af[a] = __builtin_bit_cast(
-                    glint_bf16x8, *(const glint_u32x4 *)(sX[cur] + (wm * 64 + a * 16 + (lane & 15)) * MF2_LDW + kofs));
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                bfr[b] = __builtin_bit_cast(
-                    glint_bf16x8, *(const glint_u32x4 *)(sW[cur] + (wn * 64 + b * 16 + (lane & 15)) * MF2_LDW + kofs));
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
-        }
-        if (kb + 1 < nK) {
-            produce(cur ^ 1);
-            if (kb + 2 < nK)
-                gload(kb + 2);
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = m0 + wm * 64 + a * 16 + (lane >> 4) * 4 + i;
-                const int n = n0 + wn * 64 + b * 16 + (lane & 15);
-                if (m < M && n < N)
-                    y[(int64_t)m * N + n] = glint_f32_to_bf16(acc[a][b][i]);
-            }
-}
 
 /* ------------------------------------------------------------------ dispatch */
 /* One resident wave of workgroups (every CU filled to its occupancy limit), or fewer if
@@ -691,20 +506,23 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
     const bool mfma_ok = OUT_BF16 && M > 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) &&
                          glint_aligned(plug, 16) && glint_aligned(absmax, 4) && glint_aligned(x, 16);
     if (mfma_ok) {
-        const unsigned gx = (unsigned)((N + MF_BN - 1) / MF_BN);
-        if (M <= 64) {
-            k_htile_mfma_b64<64><<<dim3(gx, (M + 63) / 64), 256, 0, st>>>(
-                (const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
-        } else if (M >= MF2_MIN_M) {
-            k_htile_mfma2<<<dim3((N + MF2_BN - 1) / MF2_BN, (M + MF2_BM - 1) / MF2_BM), MF2_THREADS, 0, st>>>(
-                (const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
-        } else {
-            k_htile_mfma_b64<128><<<dim3(gx, (M + 127) / 128), 256, 0, st>>>(
-                (const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K);
-        }
+        const GlintTileProducer p{(const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, N, K, nullptr};
+        const uint16_t *xb = (const uint16_t *)x;
+        uint16_t *yb = (uint16_t *)y;
+        if (M <= 64)
+            k_tile_mfma<64, 64, 2, 2, GlintTileProducer, TileOutBF16>
+                <<<dim3((N + 63) / 64, (M + 63) / 64), 256, 0, st>>>(p, xb, yb, M, N, K);
+        else if (M < MF2_MIN_M)
+            k_tile_mfma<128, 64, 2, 2, GlintTileProducer, TileOutBF16>
+                <<<dim3((N + 63) / 64, (M + 127) / 128), 256, 0, st>>>(p, xb, yb, M, N, K);
+        else
+            k_tile_mfma<MF2_BM, MF2_BN, 4, 2, GlintTileProducer, TileOutBF16>
+                <<<dim3((N + MF2_BN - 1) / MF2_BN, (M + MF2_BM - 1) / MF2_BM), 512, 0, st>>>(p, xb, yb, M, N, K);
     } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS / 64) {
         const int S = K / (64 * GEMV_X_EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
-        auto kern = k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16>;
+        /* K / 8 chunks of x over 64 S G threads: 4 / G per thread */
+        auto kern = G >= 4 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 1>
+                           : (G >= 2 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 2> : k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 0>);
         const int64_t resident = glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4);
         const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
         int64_t rows_per_wg = G * per_wave;
@@ -712,7 +530,9 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         if (rows_per_wg > cap)
             rows_per_wg = cap;
         const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
-        const size_t lds = (size_t)rows_per_wg * S * 4 * sizeof(float);
+        size_t lds = (size_t)rows_per_wg * S * 4 * sizeof(float);
+        if (G >= 2 && lds < (size_t)K * 2)
+            lds = (size_t)K * 2; /* x staging; K <= 8192 here, within GEMV_X_RED_MAX floats */
         if (glint_set_lds_limit((const void *)kern, GEMV_X_RED_MAX * 4) != 0)
             return -3;
         kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const glint_u32x4 *)x, y, N, K, G, (int)rows_per_wg);

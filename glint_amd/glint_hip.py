@@ -65,6 +65,11 @@ class Int8MmaLinear(_c.Structure):
     _fields_ = [("q", VP), ("scale", VP), ("n_out", I32), ("k_in", I32)]
 
 
+class Int8PinLinear(_c.Structure):
+    """include/int8_tile_gemm.h Int8PinLinear, passed by value (same layout as Int8MmaLinear)."""
+    _fields_ = [("q", VP), ("scale", VP), ("n_out", I32), ("k_in", I32)]
+
+
 class GlintStreamerStats(ctypes.Structure):
     """include/glint_plug_streamer.h GlintStreamerStats."""
     _fields_ = [("total_h2d_bytes", ctypes.c_uint64), ("total_stall_ms", ctypes.c_double),
@@ -80,6 +85,7 @@ _P7_SIGS = {
     "int8_mma_gemm_resolve": ([VP, Int8MmaLinear, VP, VP, VP, I32, VP, VP, VP, VP, VP, VP], I32),
     "p7_int8_gemm_flat": ([VP, VP, VP, I32, I32, VP, I32, VP, VP, VP], I32),
     "p7_int8_gemm_plug_flat": ([VP, VP, VP, VP, VP, I32, I32, VP, I32, VP, VP, VP], I32),
+    "int8_tile_gemm_bf16": ([VP, Int8PinLinear, VP, I32, VP], I32),
     "glint_int8_gemm_i32": ([VP, VP, VP, I32, I32, I32, VP], I32),
     "glint_int8_gemm_scaled_bf16": ([VP, VP, VP, VP, VP, I32, I32, I32, VP], I32),
     "glint_plug_streamer_create": ([_c.POINTER(VP), I32, _c.POINTER(_c.c_uint64), VP, VP], I32),
@@ -244,6 +250,19 @@ def int8_mma_gemm(x, q, scale, n_out: int, k_in: int, xq=None, sx=None, stream=N
     lin = Int8MmaLinear(q.data_ptr(), scale.data_ptr(), n_out, k_in)
     _check(p7_lib().int8_mma_gemm(_p(x), lin, _p(y), m, _p(xq), _p(sx), _stream(stream)), "int8_mma_gemm")
     return y, xq, sx
+
+
+def int8_tile_gemm(x, q, scale, n_out: int, k_in: int, m: Optional[int] = None, y=None, stream=None):
+    """W8A16 over an INT8 pin linear: x bf16 [m, k_in] -> y f32 [m, n_out] (int8_tile_gemm_bf16).
+    x, q and scale may be views at any offset; the call takes their data pointers as they are."""
+    torch = _torch()
+    x = _as_u16(x)
+    m = x.numel() // k_in if m is None else m
+    if y is None:
+        y = torch.empty((m, n_out), dtype=torch.float32, device=x.device)
+    lin = Int8PinLinear(q.data_ptr(), scale.data_ptr(), n_out, k_in)
+    _check(p7_lib().int8_tile_gemm_bf16(_p(x), lin, _p(y), m, _stream(stream)), "int8_tile_gemm_bf16")
+    return y
 
 
 def int8_mma_gemm_plug(x, q, scale, plug_q4, plug_scale, n_out: int, k_in: int, fused: bool = False, stream=None):

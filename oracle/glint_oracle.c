@@ -18,7 +18,11 @@
  *                      answers, a zero plug (equal to the base) and power-of-two scales on
  *                      small integers (every f32 step exact, so fused, two-pass and the
  *                      integer formula agree bit for bit); the residual by the rounding
- *                      bound |r - rq sr| <= sr / 2 and the sign of the reconstruction.
+ *                      bound |r - rq sr| <= sr / 2 and the sign of the reconstruction;
+ *   oracle_int8_pin_* / oracle_int8_tile_f64   BF16 rounding known answers (ties to even on
+ *                      exact halfway products), the flat scale index on k_in % 64 != 0
+ *                      against a numpy restatement, and exact integer results for
+ *                      power-of-two scales (numpy int64 matmul).
  */
 #include <math.h>
 #include <stdint.h>
@@ -309,6 +313,35 @@ EXPORT void oracle_int8_scale_bf16(const int32_t *C, const float *sa, const floa
     for (int i = 0; i < M; ++i)
         for (int j = 0; j < N; ++j)
             out[(int64_t)i * N + j] = oracle_f32_to_bf16_one(((float)C[(int64_t)i * N + j] * sa[i]) * sb[j]);
+}
+
+/* W8A16 over an INT8 pin linear (int8_tile_gemm.h:10-27, test_int8_tile_gemm.cu:53-55,
+ * 89-113): weight i = bf16 RNE((float)q[i] * scale[i / 64]) over the flat index
+ * i = n * K + k; bits of every weight of W [N, K]. */
+EXPORT void oracle_int8_pin_dequant_bf16(const int8_t *q, const float *scale, int64_t n, uint16_t *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = oracle_f32_to_bf16_one((float)q[i] * scale[i / 64]);
+}
+
+/* y[m, n] = sum_k x[m, k] * w[n, k] in double with w the BF16 dequant above, and the sum
+ * of |terms| per output (the reference's check: |got - dot| <= 1e-4 * absdot). */
+EXPORT void oracle_int8_tile_f64(const uint16_t *x, const int8_t *q, const float *scale, int M, int N, int K,
+                                 double *y, double *abs_sum) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            double acc = 0, aacc = 0;
+            for (int k = 0; k < K; ++k) {
+                const int64_t i = (int64_t)n * K + k;
+                const float w = bf16_to_f32(oracle_f32_to_bf16_one((float)q[i] * scale[i / 64]));
+                const double t = (double)bf16_to_f32(x[(int64_t)m * K + k]) * (double)w;
+                acc += t;
+                aacc += fabs(t);
+            }
+            y[(int64_t)m * N + n] = acc;
+            abs_sum[(int64_t)m * N + n] = aacc;
+        }
 }
 
 EXPORT int oracle_threads(void) {

@@ -218,6 +218,8 @@ class Oracle:
             "oracle_unpack_res4": ([vp, i64, vp], None),
             "oracle_int8_mma_plug_fused": ([vp, vp, vp, vp, vp, vp, i32, i32, i32, vp], None),
             "oracle_quant_act_resid": ([vp, vp, vp, i32, i32, vp, vp], None),
+            "oracle_int8_pin_dequant_bf16": ([vp, vp, i64, vp], None),
+            "oracle_int8_tile_f64": ([vp, vp, vp, i32, i32, i32, vp, vp], None),
             "oracle_threads": ([], i32),
         }
         for name, (args, res) in sig.items():
@@ -323,3 +325,21 @@ class Oracle:
         C, sa, sb = (np.ascontiguousarray(t) for t in (C, sa, sb))
         self.lib.oracle_int8_scale_bf16(_ptr(C), _ptr(sa), _ptr(sb), M, N, _ptr(out))
         return out.reshape(M, N)
+
+    def int8_pin_dequant_bf16(self, q, scale) -> np.ndarray:
+        q = np.ascontiguousarray(q, np.int8).reshape(-1)
+        scale = np.ascontiguousarray(scale, np.float32)
+        assert scale.size >= (q.size + 63) // 64
+        out = np.empty(q.size, np.uint16)
+        self.lib.oracle_int8_pin_dequant_bf16(_ptr(q), _ptr(scale), q.size, _ptr(out))
+        return out
+
+    def int8_tile_f64(self, x_u16, q, scale, M, N, K):
+        x_u16 = np.ascontiguousarray(x_u16, np.uint16)
+        q = np.ascontiguousarray(q, np.int8)
+        scale = np.ascontiguousarray(scale, np.float32)
+        assert x_u16.size >= M * K and q.size >= N * K and scale.size >= (N * K + 63) // 64
+        y = np.empty(M * N, np.float64)
+        a = np.empty(M * N, np.float64)
+        self.lib.oracle_int8_tile_f64(_ptr(x_u16), _ptr(q), _ptr(scale), M, N, K, _ptr(y), _ptr(a))
+        return y.reshape(M, N), a.reshape(M, N)

@@ -12,7 +12,7 @@ from glint_amd import glint_hip
 ROOT = Path(__file__).resolve().parent.parent
 HEADERS = {
     "libglint_encode.so": ["glint_encode.h", "glint_htile.h"],
-    "libp7_kernels.so": ["int8_mma_gemm.h", "p7_attach.h", "glint_plug_streamer.h"],
+    "libp7_kernels.so": ["int8_mma_gemm.h", "int8_tile_gemm.h", "p7_attach.h", "glint_plug_streamer.h"],
 }
 
 
@@ -96,6 +96,8 @@ def test_bad_arguments_rejected_without_a_device():
     assert p7.p7_int8_gemm_plug_flat(one, one, one, one, one, 64, 96, one, 1, one, one, null) == 1
     # resolve: the three plug pointers must be all set or all NULL (int8_mma_gemm.h:56-61)
     assert p7.int8_mma_gemm_resolve(x16, ok, one, null, one, 1, x16, one, x16, one, x16, null) == 1
+    # W8A16: a pending error (here: no device) or a bad argument returns nonzero, launching nothing
+    assert p7.int8_tile_gemm_bf16(null, glint_hip.Int8PinLinear(16, 16, 64, 128), one, 1, null) != 0
     # streamer argument checks come before any device call (glint_plug_streamer.h codes)
     h = ctypes.c_void_p()
     sizes = (ctypes.c_uint64 * 1)(16)

@@ -398,6 +398,55 @@ def test_quant_act_resid_pins(oracle):
     assert e2 * 60 < e1, (e1, e2)
 
 
+# ------------------------------------------------------------ W8A16 over an INT8 pin
+def test_int8_pin_dequant_known_answers(oracle):
+    """BF16 RNE of (float)q * s (test_int8_tile_gemm.cu:53-55), worked by hand:
+    1 * (1 + 2^-8) is halfway between 1.0 and 1 + 2^-7 and ties to even (0x3F80);
+    1 * (1 + 3 * 2^-8) is halfway between 0x3F81 and 0x3F82 and ties to even (0x3F82);
+    3 * (1 + 2^-8) = 3.01171875 is 0.75 of a 2^-6 step above 3 (0x4041);
+    127 * (1 + 2^-8) = 127.49609375 rounds to 127.5 (0x42FF); q = 0 gives +0."""
+    s = np.array([1 + 2.0 ** -8] * 1, np.float32)
+    q = np.array([1, 3, -1, 0, 127, -127], np.int8)
+    got = oracle.int8_pin_dequant_bf16(q, s)
+    assert got.tolist() == [0x3F80, 0x4041, 0xBF80, 0x0000, 0x42FF, 0xC2FF]
+    got = oracle.int8_pin_dequant_bf16(np.array([1], np.int8), np.array([1 + 3 * 2.0 ** -8], np.float32))
+    assert got.tolist() == [0x3F82]
+
+
+def test_int8_pin_scale_index_is_flat(oracle):
+    """k_in = 37: a row's 64-blocks start mid-row, w[i] uses scale[i // 64] over the flat
+    index (int8_tile_gemm.h:10-12). A numpy restatement agrees; a row-local index does not."""
+    n, k = 7, 37
+    rng = np.random.default_rng(3)
+    q = rng.integers(-127, 128, n * k, dtype=np.int8)
+    s = (1e-3 + 2e-2 * rng.random((n * k + 63) // 64)).astype(np.float32)
+    got = oracle.int8_pin_dequant_bf16(q, s)
+    flat = G.f32_to_bf16_bits(q.astype(np.float32) * s[np.arange(n * k) // 64])
+    assert np.array_equal(got, flat)
+    rowlocal = G.f32_to_bf16_bits(q.astype(np.float32) * s[(np.arange(n * k) % k) // 64])
+    assert not np.array_equal(got, rowlocal)
+
+
+def test_int8_tile_f64_is_exact_on_dyadic_data(oracle):
+    """Small integer x, q and power-of-two scales: every BF16 rounding is exact and the
+    double sums are exact, so y must equal the integer GEMM scaled by the flat blocks'
+    2^-e (numpy int64), and the |term| sums likewise. k_in = 100 crosses blocks mid-row;
+    m != n catches a transposed operand."""
+    m, n, k = 5, 9, 100
+    rng = np.random.default_rng(11)
+    xi = rng.integers(-4, 5, (m, k))
+    q = rng.integers(-127, 128, n * k, dtype=np.int8)
+    e = rng.integers(3, 12, (n * k + 63) // 64)
+    s = np.ldexp(np.ones(e.size), -e).astype(np.float32)
+    emax = int(e.max())
+    wi = q.astype(np.int64) * (np.int64(1) << (emax - e[np.arange(n * k) // 64]))  # w * 2^emax, exact
+    wi = wi.reshape(n, k)
+    want = (xi @ wi.T).astype(np.float64) / 2.0 ** emax
+    want_abs = (np.abs(xi) @ np.abs(wi).T).astype(np.float64) / 2.0 ** emax
+    y, a = oracle.int8_tile_f64(G.f32_to_bf16_bits(xi.astype(np.float32)), q, s, m, n, k)
+    assert np.array_equal(y, want) and np.array_equal(a, want_abs)
+
+
 # ------------------------------------------------------- the pins catch planted mistakes
 def test_planted_mistakes_are_caught():
     """Mutations of the numpy oracle that a plausible bug would introduce must fail
