@@ -4,15 +4,16 @@
  * y[M, N] = x[M, K] W^T, x BF16 [M, K] row-major with 16-B aligned rows and K % 64 == 0.
  * W is made 16 weights at a time by a Producer, which owns the weight format:
  *   struct Regs;                                  registers of one thread's step
- *   load(Regs &, int row, int quarter, int kb)    global loads of W[row, 64 kb + 16 quarter, +16)
+ *   load(Regs &, int row, int quarter, int kb)    global loads of W[row, 64 kb + 16 quarter, +16),
+ *                                                 row < N and kb < K / 64 (the kernel clamps)
  *   produce(const Regs &, uint32_t (&)[8], lane)  the 16 weights as BF16 pairs (lo = even k)
  *   LDS_WORDS, setup(float *lds)                  LDS the producer needs (filled before step 0)
  *
  * Block tile BM x BN x 64 (K) over WM x WN waves; each wave owns a (BM / WM) x (BN / WN)
  * tile of v_mfma_f32_16x16x32_bf16 accumulators (f32). Thread t produces W row t / 4,
  * K quarter t % 4 (so BN * 4 == threads), and stages BM * 8 / threads 16-B chunks of x.
- * Each operand has two LDS buffers: step kb runs its MFMAs from buffer kb & 1 while the
- * threads write step kb + 1 into the other (its global loads went out one step earlier),
+ * Each operand has two LDS buffers: step kb runs its MFMAs from buffer kb & 1, then the
+ * threads write step kb + 1 into the other (its global loads went out two steps earlier),
  * so a K step needs one barrier. LDS rows are 80 BF16 (160 B): with 72-element rows the
  * bank-conflict counter read 4x higher for the same work.
  *
@@ -60,15 +61,10 @@ struct GlintTileProducer {
         glint_fill_cells_lds(lds, lds + GLINT_LDS_CELLS_WORDS);
     }
     __device__ __forceinline__ void load(Regs &r, int row, int quarter, int kb) const {
-        if (row < N) {
-            const int64_t q = (int64_t)row * (K >> 4) + kb * 4 + quarter;
-            r.h = __builtin_nontemporal_load(&hole[q]);
-            r.p = __builtin_nontemporal_load(&plug[q]);
-            r.a = absmax[(int64_t)row * (K >> 6) + kb];
-        } else {
-            r.h = r.p = glint_u32x2{0u, 0u};
-            r.a = 0.0f;
-        }
+        const int64_t q = (int64_t)row * (K >> 4) + kb * 4 + quarter;
+        r.h = __builtin_nontemporal_load(&hole[q]);
+        r.p = __builtin_nontemporal_load(&plug[q]);
+        r.a = absmax[(int64_t)row * (K >> 6) + kb];
     }
     __device__ __forceinline__ void produce(const Regs &r, uint32_t (&packed)[8], int lane) const {
         const uint32_t lb = lane & 31;
@@ -100,13 +96,8 @@ struct Int8PinTileProducer {
     };
     __device__ __forceinline__ void setup(float *) {}
     __device__ __forceinline__ void load(Regs &r, int row, int quarter, int kb) const {
-        if (row < N) {
-            r.w = __builtin_nontemporal_load(&q[(int64_t)row * (K >> 4) + kb * 4 + quarter]);
-            r.s = scale[(int64_t)row * (K >> 6) + kb];
-        } else {
-            r.w = glint_u32x4{0u, 0u, 0u, 0u};
-            r.s = 0.0f;
-        }
+        r.w = __builtin_nontemporal_load(&q[(int64_t)row * (K >> 4) + kb * 4 + quarter]);
+        r.s = scale[(int64_t)row * (K >> 6) + kb];
     }
     __device__ __forceinline__ void produce(const Regs &r, uint32_t (&packed)[8], int) const {
         const uint32_t W[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
@@ -145,35 +136,38 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
         for (int b = 0; b < TN; ++b)
             acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
 
-    typename P::Regs wv;
-    glint_u32x4 xv[XV];
-    auto gload = [&](int kb) {
-        p.load(wv, n0 + wr, wq, kb);
+    /* Two register stages alternate over even and odd steps: the loads of step kb + 3 are
+     * issued at the end of step kb and written to LDS at the end of step kb + 2. Rows past M
+     * or N are clamped into the matrix (their outputs are not stored) and steps past the end
+     * reload the last one, so every load is unconditional. */
+    struct Stage {
+        typename P::Regs w;
+        glint_u32x4 x[XV];
+    };
+    Stage s0, s1;
+    const int wrow = min(n0 + wr, N - 1);
+    auto gload = [&](int kb, Stage &st) {
+        kb = min(kb, nK - 1);
+        p.load(st.w, wrow, wq, kb);
 #pragma unroll
         for (int i = 0; i < XV; ++i) {
-            const int m = m0 + xr + (T / 8) * i;
-            xv[i] = (m < M) ? *(const glint_u32x4 *)(x + (int64_t)m * K + (int64_t)kb * 64 + xc * 8)
-                            : glint_u32x4{0u, 0u, 0u, 0u};
+            const int m = min(m0 + xr + (T / 8) * i, M - 1);
+            st.x[i] = *(const glint_u32x4 *)(x + (int64_t)m * K + (int64_t)kb * 64 + xc * 8);
         }
     };
-    auto produce = [&](int buf) {
+    auto produce = [&](int buf, const Stage &st) {
         uint32_t packed[8];
-        p.produce(wv, packed, lane);
+        p.produce(st.w, packed, lane);
         glint_u32x4 *dst = (glint_u32x4 *)(sW[buf] + wr * TILE_LDW + wq * 16);
         dst[0] = glint_u32x4{packed[0], packed[1], packed[2], packed[3]};
         dst[1] = glint_u32x4{packed[4], packed[5], packed[6], packed[7]};
 #pragma unroll
         for (int i = 0; i < XV; ++i)
-            *(glint_u32x4 *)(sX[buf] + (xr + (T / 8) * i) * TILE_LDW + xc * 8) = xv[i];
+            *(glint_u32x4 *)(sX[buf] + (xr + (T / 8) * i) * TILE_LDW + xc * 8) = st.x[i];
     };
-
-    p.setup(ptab);
-    gload(0);
-    produce(0);
-    if (nK > 1)
-        gload(1);
-    __syncthreads();
-    for (int kb = 0; kb < nK; ++kb) {
+    /* step kb: MFMAs from buffer kb & 1, step kb + 1 (in `next`) into the other buffer, then
+     * `next` is refilled with step kb + 3 */
+    auto step = [&](int kb, Stage &next) {
         const int cur = kb & 1;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -197,13 +191,24 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
                 for (int b = 0; b < TN; ++b)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
         }
-        if (kb + 1 < nK) {
-            produce(cur ^ 1);
-            if (kb + 2 < nK)
-                gload(kb + 2);
-        }
+        produce(cur ^ 1, next); /* past the end: a clamped copy nobody reads */
+        gload(kb + 3, next);
         __syncthreads();
+    };
+
+    p.setup(ptab);
+    gload(0, s0);
+    produce(0, s0);
+    gload(1, s1);
+    gload(2, s0);
+    __syncthreads();
+    int kb = 0;
+    for (; kb + 2 <= nK; kb += 2) {
+        step(kb, s1);
+        step(kb + 1, s0);
     }
+    if (kb < nK)
+        step(kb, s1);
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll

@@ -66,8 +66,12 @@ def test_flat_entry_and_refusal():
     assert rc == 1
 
 
-@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 130, 192), (256, 512, 1024), (2048, 256, 8192)])
+@pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 130, 192), (256, 512, 1024), (2048, 256, 8192),
+                                   (257, 300, 640), (512, 1024, 2048), (300, 257, 64), (1000, 520, 128)])
 def test_int8_gemm_exact(oracle, M, N, K):
+    """Below 256 rows or columns the 128 x 128 tile kernel runs, above the 256 x 256 one
+    (ragged edges, one and odd numbers of K steps)."""
+    print(f"int8_gemm M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M + N + K)
     A = rng.integers(-127, 128, (M, K), dtype=np.int8)
     B = rng.integers(-127, 128, (N, K), dtype=np.int8)
@@ -83,7 +87,7 @@ def test_int8_gemm_exact(oracle, M, N, K):
 
 def test_int8_gemm_extremes(oracle):
     """All -127 / all 127 at the largest K of the benchmark: |C| = K * 127^2 = 132 million."""
-    M, N, K = 128, 128, 8192
+    M, N, K = 256, 256, 8192
     A = np.full((M, K), -127, np.int8)
     B = np.full((N, K), 127, np.int8)
     B[1::2] = -127
