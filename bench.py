@@ -320,6 +320,43 @@ def bench_w8a16(torch, H, steps: int):
     return out
 
 
+def bench_pin_tools(tensors: int = 16):
+    """The pin tools' device path end to end: convert a synthetic two-shard BF16 model
+    (tensors x 4096 x 4096) from safetensors files to a pin and unpin it back to BF16.
+    Includes file reads and writes (page cache), host staging and PCIe both ways."""
+    import tempfile
+    import time
+    import numpy as np
+    from glint_amd import pin_tools as P
+    from glint_amd.safetensors_io import write_safetensors
+    rng = np.random.default_rng(4000)
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as td:
+        src = Path(td) / "src"
+        src.mkdir()
+        wmap = {}
+        for s in range(2):
+            shard = f"model-0000{s + 1}-of-00002.safetensors"
+            ts = []
+            for l in range(tensors // 2):
+                w = (rng.standard_normal((4096, 4096), dtype=np.float32) * 0.02).view(np.uint32)
+                raw = ((w + (0x7FFF + ((w >> 16) & 1))) >> 16).astype("<u2").tobytes()
+                ts.append((f"layers.{s * tensors // 2 + l}.mlp.weight", "BF16", (4096, 4096), raw))
+            write_safetensors(src / shard, ts)
+            wmap.update({t[0]: shard for t in ts})
+        (src / P.INDEX_NAME).write_text(json.dumps({"metadata": {}, "weight_map": wmap}))
+        P.convert(src, Path(td) / "warm", dry_run=True)
+        t0 = time.perf_counter()
+        P.convert(src, Path(td) / "pin")
+        t_conv = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        P.unpin(Path(td) / "pin", Path(td) / "back")
+        t_unpin = time.perf_counter() - t0
+    gb = tensors * 4096 * 4096 * 2 / 1e9
+    return {"config": f"{tensors} x 4096x4096 BF16 in two shards ({gb:.2f} GB), files in the page cache",
+            "convert_s": t_conv, "convert_bf16_in_gbs": gb / t_conv, "unpin_s": t_unpin,
+            "unpin_bf16_out_gbs": gb / t_unpin}
+
+
 def cpu_baseline(seconds_target: float = 20.0):
     """The CPU path beside the GPU, on this host: the repo's C restatement of the reference
     host path (oracle/glint_oracle.c, OpenMP over the threads it reports) running the
@@ -503,6 +540,8 @@ def main() -> int:
         extra["w8a16"] = bench_w8a16(torch, H, steps=10)
         log("w8a16 done")
         extra["host_abi_pcie"] = bench_host_abi(H)
+        extra["pin_tools"] = bench_pin_tools()
+        log(f"pin tools convert {extra['pin_tools']['convert_bf16_in_gbs']:.2f} GB/s bf16-in (files and PCIe inclusive)")
         log(f"host ABI encode {extra['host_abi_pcie']['encode_bf16_in_gbs']:.1f} GB/s bf16-in (PCIe inclusive)")
     cpu = None if args.no_cpu else cpu_baseline()
     achieved = gemv["gbs"]
