@@ -320,6 +320,35 @@ def bench_w8a16(torch, H, steps: int):
     return out
 
 
+def bench_kmajor(torch, H, steps: int = 100, copies: int = 20):
+    """The K-major decode step at the decode shape (N 14336, K 4096): fold GEMV (HBM bytes:
+    hole_k N K / 2 + scales_k N K / 16 + x + y), device selection of 10% of the channels,
+    and the plug correction over them. Pins rotate over `copies` (about 1.3 GB)."""
+    N, K = GEMV_N, GEMV_K
+    g = torch.Generator(device="cuda").manual_seed(4242)
+    pins = []
+    for _ in range(copies):
+        w = (torch.randn(N * K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        h, p, a = H.encode_bf16(w, 64)
+        pins.append(H.kmajor_pack(h, p, a, N, K))
+        del w, h, p, a
+    x = torch.randn(K, device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.empty(N, dtype=torch.float32, device="cuda")
+    part = torch.empty(32 * N, dtype=torch.float32, device="cuda")
+    ksg, ks = 32, 16
+    fold_bytes = N * K / 2 + N * K / 16 + 2 * K + 4 * N
+    ms_fold = timed(torch, [lambda pk=pk: H.gemv_km_fold(pk[0], pk[2], x, N, K, ksg, y=y, part=part) for pk in pins],
+                    steps, 10)
+    idx, cnt = H.select_topk(x, K // 10)
+    ms_sel = timed(torch, [lambda: H.select_topk(x, K // 10, idx=idx, cnt=cnt)], steps, 10)
+    ms_corr = timed(torch, [lambda pk=pk: H.apply_corr_km(pk[0], pk[1], pk[2], x, idx, cnt, y, N, K, ks, part=part)
+                            for pk in pins], steps, 10)
+    del pins
+    return {"config": f"N {N} K {K}, fold ksg {ksg}, 10% of channels selected, correction ks {ks}",
+            "fold_ms": ms_fold, "fold_gbs": fold_bytes / ms_fold / 1e6, "fold_frac": fold_bytes / ms_fold / 1e6 / HBM_PEAK_GBS,
+            "select_ms": ms_sel, "corr_ms": ms_corr, "selected": int(cnt.item())}
+
+
 def bench_pin_tools(tensors: int = 16):
     """The pin tools' device path end to end: convert a synthetic two-shard BF16 model
     (tensors x 4096 x 4096) from safetensors files to a pin and unpin it back to BF16.
@@ -539,6 +568,8 @@ def main() -> int:
         log(f"int8 {extra['int8_gemm']['tops']:.0f} TOPS")
         extra["w8a16"] = bench_w8a16(torch, H, steps=10)
         log("w8a16 done")
+        extra["kmajor_decode"] = bench_kmajor(torch, H)
+        log(f"k-major fold {extra['kmajor_decode']['fold_ms'] * 1e3:.1f} us")
         extra["host_abi_pcie"] = bench_host_abi(H)
         extra["pin_tools"] = bench_pin_tools()
         log(f"pin tools convert {extra['pin_tools']['convert_bf16_in_gbs']:.2f} GB/s bf16-in (files and PCIe inclusive)")

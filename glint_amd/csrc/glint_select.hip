@@ -1,0 +1,411 @@
+/* K-major decode path for gfx950: layout conversion, parent-only (fold) GEMV, channel
+ * selection and the selected-plug correction (reference mojo/p7_glint_gemv_km.mojo,
+ * mojo/p7_select_device.mojo, mojo/p7_glint_select_decode.mojo; semantics in
+ * include/glint_select.h).
+ *
+ * k_kmajor_pack_planes — 64 rows x 64 channels per workgroup through LDS: 8-byte loads of
+ *   the row-major planes, 4-byte stores of the K-major rows.
+ * k_gemv_km_fold — a lane owns 32 output rows (16 B of a K-major hole row), so a wave
+ *   reads 1 KiB contiguous per channel; the 8 waves of a workgroup take 8 parts of the
+ *   workgroup's channel slice (grid.y) and meet in LDS. Per element: one v_perm for the
+ *   address, one lookup in the 64-copy PARENT table, one FMA by the wave-uniform x[c];
+ *   the block scale is applied once per run of channels inside a 64-block.
+ * k_select_topk — one workgroup: keys in LDS, 15 bisection steps of a block count, then
+ *   a block scan that writes the kept channels in ascending order.
+ * k_apply_corr_km — the fold kernel's mapping over the selected list (count read on the
+ *   device), with the 256-entry delta table (CELLS - PARENT) in 64 lane copies.
+ */
+#include <algorithm>
+
+#include "glint_common.h"
+#include "glint_select.h"
+
+static __constant__ float kParent[16] = GLINT_PARENT_INIT;
+
+#define KM_T 256
+
+/* ------------------------------------------------------------------- layout */
+#define KP_ROWS 64
+#define KP_LDS_ROW 36 /* 32 bytes of a row's 64 channels + 4 bytes of padding */
+
+/* Workgroup (channel tile c0 = 64 bx, row tile r0 = 64 by). Load: thread t reads bytes
+ * [c0/2 + 8 (t % 4), +8) of row r0 + t / 4 of both planes. Store: thread t writes the
+ * K-major bytes [(r0 + 16 (t % 4)) / 2, +8) of channel c0 + t / 4. */
+__global__ __launch_bounds__(KM_T) void k_kmajor_pack_planes(const uint8_t *__restrict__ hole,
+                                                             const uint8_t *__restrict__ plug,
+                                                             uint8_t *__restrict__ hole_k, uint8_t *__restrict__ plug_k,
+                                                             int N, int K) {
+    __shared__ uint8_t th[KP_ROWS * KP_LDS_ROW], tp[KP_ROWS * KP_LDS_ROW];
+    const int t = threadIdx.x;
+    const int c0 = blockIdx.x * 64, r0 = blockIdx.y * KP_ROWS;
+    {
+        const int row = t >> 2, q = t & 3;
+        uint2 vh = make_uint2(0u, 0u), vp = vh;
+        if (r0 + row < N) {
+            const int64_t off = ((int64_t)(r0 + row) * K + c0) / 2 + 8 * q;
+            vh = *(const uint2 *)(hole + off);
+            vp = *(const uint2 *)(plug + off);
+        }
+        *(uint32_t *)(th + row * KP_LDS_ROW + 8 * q) = vh.x;
+        *(uint32_t *)(th + row * KP_LDS_ROW + 8 * q + 4) = vh.y;
+        *(uint32_t *)(tp + row * KP_LDS_ROW + 8 * q) = vp.x;
+        *(uint32_t *)(tp + row * KP_LDS_ROW + 8 * q + 4) = vp.y;
+    }
+    __syncthreads();
+    const int cc = t >> 2, q = t & 3;
+    const int rb = 16 * q; /* first of this thread's 16 rows in the tile */
+    if (r0 + rb >= N)
+        return;
+    uint32_t oh[2] = {0u, 0u}, op[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int sh = 4 * (cc & 1);
+        const uint32_t h = (th[(rb + i) * KP_LDS_ROW + (cc >> 1)] >> sh) & 15u;
+        const uint32_t p = (tp[(rb + i) * KP_LDS_ROW + (cc >> 1)] >> sh) & 15u;
+        oh[i >> 3] |= h << (4 * (i & 7));
+        op[i >> 3] |= p << (4 * (i & 7));
+    }
+    /* 4-byte stores: a K-major row is N / 2 bytes, a multiple of 4 (N % 8 == 0) */
+    const int64_t dst = (int64_t)(c0 + cc) * (N / 2) + (r0 + rb) / 2;
+    *(uint32_t *)(hole_k + dst) = oh[0];
+    *(uint32_t *)(plug_k + dst) = op[0];
+    if (r0 + rb + 16 <= N) { /* else the matrix ends after 8 of the 16 rows */
+        *(uint32_t *)(hole_k + dst + 4) = oh[1];
+        *(uint32_t *)(plug_k + dst + 4) = op[1];
+    }
+}
+
+__global__ __launch_bounds__(KM_T) void k_kmajor_scales(const float *__restrict__ absmax, float *__restrict__ scales_k,
+                                                        int N, int nb) {
+    const int64_t total = (int64_t)N * nb, stride = (int64_t)gridDim.x * KM_T;
+    for (int64_t o = (int64_t)blockIdx.x * KM_T + threadIdx.x; o < total; o += stride) {
+        const int64_t cb = o / N, r = o % N;
+        scales_k[o] = absmax[r * nb + cb];
+    }
+}
+
+/* ------------------------------------------------------------------ fold GEMV */
+#define KM_SUB 8                /* waves per workgroup = parts of a channel slice */
+#define KM_ROWS 2048            /* output rows per workgroup: 64 lanes x 32 rows */
+#define KM_WG (64 * KM_SUB)
+#define KM_U 8                  /* channels of loads in flight per wave (one 16-B load of x) */
+
+__device__ __forceinline__ float km_bf16(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+
+/* 32 consecutive floats (this lane's rows of one scale row) */
+__device__ __forceinline__ void km_load32(const float *__restrict__ p, float (&v)[32]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const glint_f32x4 t = *(const glint_f32x4 *)(p + 4 * i);
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+
+/* acc[j] = fmaf(table[code of row j], xv, acc[j]) for this lane's 32 rows. E[q]/O[q] hold
+ * the code bytes of the even/odd rows of word q (byte k -> rows 8 q + 2k, 8 q + 2k + 1).
+ * All 32 lookups are issued before the first FMA (sched_barrier), so their LDS latencies
+ * overlap instead of each FMA waiting for its own lookup. */
+__device__ __forceinline__ void km_lookup_fma(const float *lds, const uint32_t (&E)[4], const uint32_t (&O)[4],
+                                              uint32_t lane4, float xv, float (&acc)[32]) {
+    float tv[32];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        tv[8 * q + 0] = glint_lds_f32(lds, glint_cell_addr<0>(E[q], lane4));
+        tv[8 * q + 1] = glint_lds_f32(lds, glint_cell_addr<0>(O[q], lane4));
+        tv[8 * q + 2] = glint_lds_f32(lds, glint_cell_addr<1>(E[q], lane4));
+        tv[8 * q + 3] = glint_lds_f32(lds, glint_cell_addr<1>(O[q], lane4));
+        tv[8 * q + 4] = glint_lds_f32(lds, glint_cell_addr<2>(E[q], lane4));
+        tv[8 * q + 5] = glint_lds_f32(lds, glint_cell_addr<2>(O[q], lane4));
+        tv[8 * q + 6] = glint_lds_f32(lds, glint_cell_addr<3>(E[q], lane4));
+        tv[8 * q + 7] = glint_lds_f32(lds, glint_cell_addr<3>(O[q], lane4));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+        acc[j] = fmaf(tv[j], xv, acc[j]);
+}
+
+/* The workgroup's KM_SUB part sums (one per wave) meet in LDS and are added in order;
+ * the sum of rows r0 + rr goes to dst[rr] (plus dst[rr] first when ADD). */
+template <bool ADD>
+__device__ __forceinline__ void km_combine_parts(float *lds, const float (&tot)[32], int r0, int N, float *dst) {
+    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+    __syncthreads(); /* the lookup table is dead: the part sums go over it */
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        *(glint_f32x4 *)(lds + q * KM_ROWS + 32 * lane + 4 * i) =
+            glint_f32x4{tot[4 * i], tot[4 * i + 1], tot[4 * i + 2], tot[4 * i + 3]};
+    __syncthreads();
+    for (int rr = threadIdx.x; rr < KM_ROWS; rr += KM_WG) {
+        if (r0 + rr >= N)
+            break;
+        float v = lds[rr];
+#pragma unroll
+        for (int k = 1; k < KM_SUB; ++k)
+            v = v + lds[k * KM_ROWS + rr];
+        dst[rr] = ADD ? dst[rr] + v : v;
+    }
+}
+
+/* Workgroup (row block bx, channel slice by): wave q walks part q of the slice as runs of
+ * channels inside one 64-block; out[by N + r] (y when there is one slice) = the slice's
+ * sum for row r. N % 32 == 0; rows of lanes past N are clamped and not stored. */
+__global__ __launch_bounds__(KM_WG) void k_gemv_km_fold(const glint_u32x4 *__restrict__ hole_k,
+                                                        const float *__restrict__ scales_k,
+                                                        const uint16_t *__restrict__ x, float *__restrict__ out, int N,
+                                                        int ksl) {
+    __shared__ __attribute__((aligned(16))) float lds[KM_SUB * KM_ROWS]; /* PARENT table at offset 0, then parts */
+    for (int i = threadIdx.x; i < 16 * 64; i += KM_WG)
+        lds[i] = kParent[i >> 6];
+    __syncthreads();
+    const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane4 = (uint32_t)lane * 4u;
+    const int r0 = blockIdx.x * KM_ROWS;
+    const int rc = min(r0 + 32 * lane, N - 32); /* this lane's first row, clamped */
+    const int64_t rowv = N / 32;                /* 16-B vectors per K-major row */
+    const int sub = ksl / KM_SUB;
+    const int c0 = blockIdx.y * ksl + q * sub, c1 = c0 + sub;
+    float tot[32], acc[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+        tot[j] = 0.f;
+    for (int b = c0 >> 6; b <= (c1 - 1) >> 6; ++b) {
+        const int cs = max(c0, 64 * b), ce = min(c1, 64 * b + 64); /* multiples of 8 */
+        float sc[32]; /* issued before the run's loads, used after them */
+        km_load32(scales_k + (int64_t)b * N + rc, sc);
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+            acc[j] = 0.f;
+        for (int c = cs; c < ce; c += KM_U) {
+            glint_u32x4 wv[KM_U];
+#pragma unroll
+            for (int u = 0; u < KM_U; ++u)
+                wv[u] = __builtin_nontemporal_load(&hole_k[(int64_t)(c + u) * rowv + rc / 32]);
+            /* the batch's 8 x values in one wave-uniform 16-B load, waited for once before the
+             * lookups (a scalar load per channel would make every lookup wait for it) */
+            const glint_u32x4 xw = *(const glint_u32x4 *)(x + c);
+            const uint32_t xs[4] = {xw.x, xw.y, xw.z, xw.w};
+#pragma unroll
+            for (int u = 0; u < KM_U; ++u) {
+                const float xv = (u & 1) ? glint_bf16hi(xs[u >> 1]) : glint_bf16lo(xs[u >> 1]);
+                const uint32_t W[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+                uint32_t E[4], O[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    E[q] = W[q] & 0x0F0F0F0Fu;
+                    O[q] = (W[q] >> 4) & 0x0F0F0F0Fu;
+                }
+                km_lookup_fma(lds, E, O, lane4, xv, acc);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+            tot[j] = fmaf(acc[j], sc[j], tot[j]);
+    }
+    km_combine_parts<false>(lds, tot, r0, N, out + (int64_t)blockIdx.y * N + r0);
+}
+
+/* y[r] = ((part[r] + part[N + r]) + ...) + part[(ks - 1) N + r], plus y[r] first when ADD. */
+template <bool ADD>
+__global__ __launch_bounds__(KM_T) void k_km_combine(const float *__restrict__ part, float *__restrict__ y, int N, int ks) {
+    const int r = blockIdx.x * KM_T + threadIdx.x;
+    if (r >= N)
+        return;
+    float acc = part[r];
+    for (int s = 1; s < ks; ++s)
+        acc = acc + part[(int64_t)s * N + r];
+    y[r] = ADD ? y[r] + acc : acc;
+}
+
+/* ------------------------------------------------------------------ selection */
+#define SEL_T 1024
+#define SEL_MAX_K 32768
+
+__device__ __forceinline__ int sel_block_sum(int v, int *wsum) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0)
+        wsum[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int total = 0;
+#pragma unroll
+    for (int i = 0; i < SEL_T / 64; ++i)
+        total += wsum[i];
+    __syncthreads();
+    return total;
+}
+
+__global__ __launch_bounds__(SEL_T) void k_select_topk(const uint16_t *__restrict__ x, int K, int nsel,
+                                                       int32_t *__restrict__ idx, int32_t *__restrict__ cnt) {
+    __shared__ uint16_t keys[SEL_MAX_K];
+    __shared__ int wsum[SEL_T / 64];
+    const int t = threadIdx.x;
+    for (int i = t; i < K; i += SEL_T)
+        keys[i] = x[i] & 0x7FFF;
+    __syncthreads();
+    const int per = (K + SEL_T - 1) / SEL_T;
+    const int lo = min(t * per, K), hi = min(lo + per, K);
+    int thr = 0;
+    for (int bi = 0; bi < 15; ++bi) {
+        const int cand = thr | (1 << (14 - bi));
+        int c = 0;
+        for (int i = lo; i < hi; ++i)
+            c += keys[i] >= cand;
+        if (sel_block_sum(c, wsum) >= nsel)
+            thr = cand;
+    }
+    if (nsel == 0)
+        thr = 32768;
+    int mine = 0;
+    for (int i = lo; i < hi; ++i)
+        mine += keys[i] >= thr;
+    /* exclusive scan of mine over the block: inclusive within the wave, then wave offsets */
+    int inc = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(inc, o, 64);
+        if ((t & 63) >= o)
+            inc += v;
+    }
+    if ((t & 63) == 63)
+        wsum[t >> 6] = inc;
+    __syncthreads();
+    int base = 0, total = 0;
+#pragma unroll
+    for (int i = 0; i < SEL_T / 64; ++i) {
+        base += (i < (t >> 6)) ? wsum[i] : 0;
+        total += wsum[i];
+    }
+    int pos = base + inc - mine;
+    for (int i = lo; i < hi; ++i)
+        if (keys[i] >= thr)
+            idx[pos++] = i;
+    if (t == 0)
+        cnt[0] = total;
+}
+
+/* ---------------------------------------------------------------- correction */
+/* Workgroup (row block bx, list chunk by): the chunk is cut into KM_SUB parts, wave q walks
+ * part q as runs of consecutive list entries inside one 64-block (the list is ascending,
+ * so a block's channels are adjacent). Delta = CELLS - PARENT sits in LDS as 64 lane
+ * copies, addressed by the code byte (h << 4 | p). One chunk adds into y; several write
+ * part[by N + r] for k_km_combine<true>. */
+__global__ __launch_bounds__(KM_WG) void k_apply_corr_km(const glint_u32x4 *__restrict__ hole_k,
+                                                         const glint_u32x4 *__restrict__ plug_k,
+                                                         const float *__restrict__ scales_k,
+                                                         const uint16_t *__restrict__ x, const int32_t *__restrict__ idx,
+                                                         const int32_t *__restrict__ cnt, float *__restrict__ y,
+                                                         float *__restrict__ part, int N, int ks) {
+    __shared__ __attribute__((aligned(16))) float lds[KM_SUB * KM_ROWS]; /* delta table, then parts */
+    static_assert(KM_SUB * KM_ROWS >= GLINT_LDS_CELLS64_WORDS, "delta table fits the part buffer");
+    for (int i = threadIdx.x; i < GLINT_LDS_CELLS64_WORDS; i += KM_WG) {
+        const int hp = i >> 6;
+        lds[i] = (&kCells[0][0])[hp] - kParent[hp >> 4];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane4 = (uint32_t)lane * 4u;
+    const int r0 = blockIdx.x * KM_ROWS;
+    const int rc = min(r0 + 32 * lane, N - 32);
+    const int64_t rowv = N / 32;
+    const int cn = cnt[0];
+    const int chunk = (cn + ks - 1) / ks, sub = (chunk + KM_SUB - 1) / KM_SUB;
+    const int lo = blockIdx.y * chunk, hi = min(lo + chunk, cn);
+    const int i0 = min(lo + q * sub, hi), i1 = min(i0 + sub, hi);
+    float tot[32], acc[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+        tot[j] = acc[j] = 0.f;
+    int cur = -1;
+    auto flush = [&]() {
+        float sc[32];
+        km_load32(scales_k + (int64_t)cur * N + rc, sc);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            tot[j] = fmaf(acc[j], sc[j], tot[j]);
+            acc[j] = 0.f;
+        }
+    };
+    for (int i = i0; i < i1; ++i) {
+        const int c = idx[i];
+        const glint_u32x4 hv = hole_k[(int64_t)c * rowv + rc / 32], pv = plug_k[(int64_t)c * rowv + rc / 32];
+        if ((c >> 6) != cur) {
+            if (cur >= 0)
+                flush();
+            cur = c >> 6;
+        }
+        const float xv = km_bf16(x[c]);
+        const uint32_t Hs[4] = {hv.x, hv.y, hv.z, hv.w}, Ps[4] = {pv.x, pv.y, pv.z, pv.w};
+        uint32_t E[4], O[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            E[q] = glint_codes_even(Hs[q], Ps[q]);
+            O[q] = glint_codes_odd(Hs[q], Ps[q]);
+        }
+        km_lookup_fma(lds, E, O, lane4, xv, acc);
+    }
+    if (cur >= 0)
+        flush();
+    if (ks > 1)
+        km_combine_parts<false>(lds, tot, r0, N, part + (int64_t)blockIdx.y * N + r0);
+    else
+        km_combine_parts<true>(lds, tot, r0, N, y + r0);
+}
+
+/* -------------------------------------------------------------------- C ABI */
+static int km_launched() { return hipGetLastError() == hipSuccess ? 0 : -3; }
+
+GLINT_API int glint_kmajor_pack(const uint8_t *hole, const uint8_t *plug, const float *absmax, int N, int K,
+                                uint8_t *hole_k, uint8_t *plug_k, float *scales_k, hipStream_t stream) {
+    if (!hole || !plug || !absmax || !hole_k || !plug_k || !scales_k)
+        return -1;
+    if (N < 8 || (N % 8) != 0 || K < 64 || (K % 64) != 0 || !glint_aligned(hole, 8) || !glint_aligned(plug, 8) ||
+        !glint_aligned(hole_k, 4) || !glint_aligned(plug_k, 4))
+        return -2;
+    k_kmajor_pack_planes<<<dim3(K / 64, (N + KP_ROWS - 1) / KP_ROWS), KM_T, 0, stream>>>(hole, plug, hole_k, plug_k,
+                                                                                     N, K);
+    const int64_t total = (int64_t)N * (K / 64);
+    const unsigned g = (unsigned)std::min<int64_t>((total + KM_T - 1) / KM_T, 65535);
+    k_kmajor_scales<<<g, KM_T, 0, stream>>>(absmax, scales_k, N, K / 64);
+    return km_launched();
+}
+
+GLINT_API int glint_gemv_km_fold(const uint8_t *hole_k, const float *scales_k, const uint16_t *x, float *y, int N, int K,
+                                 int ksg, float *part, hipStream_t stream) {
+    if (!hole_k || !scales_k || !x || !y || (ksg > 1 && !part))
+        return -1;
+    if (N < 32 || (N % 32) != 0 || ksg < 1 || K < 64 || (K % (64 * ksg)) != 0 || !glint_aligned(hole_k, 16) ||
+        !glint_aligned(scales_k, 16) || !glint_aligned(x, 16))
+        return -2;
+    const dim3 grid((N + KM_ROWS - 1) / KM_ROWS, ksg);
+    k_gemv_km_fold<<<grid, KM_WG, 0, stream>>>((const glint_u32x4 *)hole_k, scales_k, x, ksg > 1 ? part : y, N, K / ksg);
+    if (ksg > 1)
+        k_km_combine<false><<<(N + KM_T - 1) / KM_T, KM_T, 0, stream>>>(part, y, N, ksg);
+    return km_launched();
+}
+
+GLINT_API int glint_select_topk(const uint16_t *x, int K, int nsel, int32_t *idx, int32_t *cnt, hipStream_t stream) {
+    if (!x || !idx || !cnt)
+        return -1;
+    if (K < 1 || K > SEL_MAX_K || nsel < 0)
+        return -2;
+    k_select_topk<<<1, SEL_T, 0, stream>>>(x, K, nsel, idx, cnt);
+    return km_launched();
+}
+
+GLINT_API int glint_apply_corr_km(const uint8_t *hole_k, const uint8_t *plug_k, const float *scales_k,
+                                  const uint16_t *x, const int32_t *idx, const int32_t *cnt, float *y, int N, int K,
+                                  int ks, float *part, hipStream_t stream) {
+    if (!hole_k || !plug_k || !scales_k || !x || !idx || !cnt || !y || (ks > 1 && !part))
+        return -1;
+    if (N < 32 || (N % 32) != 0 || K < 64 || (K % 64) != 0 || ks < 1 || !glint_aligned(hole_k, 16) ||
+        !glint_aligned(plug_k, 16) || !glint_aligned(scales_k, 16))
+        return -2;
+    const dim3 grid((N + KM_ROWS - 1) / KM_ROWS, ks);
+    k_apply_corr_km<<<grid, KM_WG, 0, stream>>>((const glint_u32x4 *)hole_k, (const glint_u32x4 *)plug_k, scales_k, x,
+                                                idx, cnt, y, part, N, ks);
+    if (ks > 1)
+        k_km_combine<true><<<(N + KM_T - 1) / KM_T, KM_T, 0, stream>>>(part, y, N, ks);
+    return km_launched();
+}

@@ -57,6 +57,10 @@ _ENCODE_SIGS = {
     "launch_glint_htile_s3_f32_stream": ([VP, VP, VP, VP, VP, I32, I32, I32, I32, VP], I32),
     "launch_glint_htile_s3_f32": ([VP, VP, VP, VP, VP, I32, I32, I32, I32], I32),
     "launch_glint_htile_bf16_stream": ([VP, VP, VP, VP, VP, I32, I32, I32, I32, VP], I32),
+    "glint_kmajor_pack": ([VP, VP, VP, I32, I32, VP, VP, VP, VP], I32),
+    "glint_gemv_km_fold": ([VP, VP, VP, VP, I32, I32, I32, VP, VP], I32),
+    "glint_select_topk": ([VP, I32, I32, VP, VP, VP], I32),
+    "glint_apply_corr_km": ([VP, VP, VP, VP, VP, VP, VP, I32, I32, I32, VP, VP], I32),
 }
 
 
@@ -236,6 +240,52 @@ def htile_bf16(hole, plug, absmax, x, N: int, K: int, blocksize: int = 64, out=N
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if out is None else out
     _check(encode_lib().launch_glint_htile_bf16_stream(_p(hole), _p(plug), _p(absmax), _p(x), _p(y), M, N, K,
                                                        blocksize, _stream(stream)), "launch_glint_htile_bf16_stream")
+    return y
+
+
+# ------------------------------------------------------- K-major decode path (glint_select.h)
+def kmajor_pack(hole, plug, absmax, N: int, K: int, stream=None):
+    """Row-major pin planes -> (hole_k, plug_k, scales_k) device tensors."""
+    torch = _torch()
+    hk = torch.empty(K * N // 2, dtype=torch.uint8, device=hole.device)
+    pk = torch.empty(K * N // 2, dtype=torch.uint8, device=hole.device)
+    sk = torch.empty(N * K // 64, dtype=torch.float32, device=hole.device)
+    _check(encode_lib().glint_kmajor_pack(_p(hole), _p(plug), _p(absmax), N, K, _p(hk), _p(pk), _p(sk),
+                                          _stream(stream)), "glint_kmajor_pack")
+    return hk, pk, sk
+
+
+def gemv_km_fold(hole_k, scales_k, x, N: int, K: int, ksg: int = 1, y=None, part=None, stream=None):
+    """Parent-only GEMV over the K-major hole: x bf16 [K] -> y f32 [N]."""
+    torch = _torch()
+    y = torch.empty(N, dtype=torch.float32, device=hole_k.device) if y is None else y
+    if ksg > 1 and part is None:
+        part = torch.empty(ksg * N, dtype=torch.float32, device=hole_k.device)
+    _check(encode_lib().glint_gemv_km_fold(_p(hole_k), _p(scales_k), _p(_as_u16(x)), _p(y), N, K, ksg,
+                                           _p(part) if part is not None else None, _stream(stream)),
+           "glint_gemv_km_fold")
+    return y
+
+
+def select_topk(x, nsel: int, idx=None, cnt=None, stream=None):
+    """Kept channels of x (ascending) and their count, both on the device."""
+    torch = _torch()
+    x = _as_u16(x)
+    K = x.numel()
+    idx = torch.empty(K, dtype=torch.int32, device=x.device) if idx is None else idx
+    cnt = torch.empty(1, dtype=torch.int32, device=x.device) if cnt is None else cnt
+    _check(encode_lib().glint_select_topk(_p(x), K, nsel, _p(idx), _p(cnt), _stream(stream)), "glint_select_topk")
+    return idx, cnt
+
+
+def apply_corr_km(hole_k, plug_k, scales_k, x, idx, cnt, y, N: int, K: int, ks: int = 1, part=None, stream=None):
+    """y += the plug correction over the selected channels (in place)."""
+    torch = _torch()
+    if ks > 1 and part is None:
+        part = torch.empty(ks * N, dtype=torch.float32, device=y.device)
+    _check(encode_lib().glint_apply_corr_km(_p(hole_k), _p(plug_k), _p(scales_k), _p(_as_u16(x)), _p(idx), _p(cnt),
+                                            _p(y), N, K, ks, _p(part) if part is not None else None,
+                                            _stream(stream)), "glint_apply_corr_km")
     return y
 
 

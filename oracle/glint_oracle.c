@@ -19,6 +19,13 @@
  *                      small integers (every f32 step exact, so fused, two-pass and the
  *                      integer formula agree bit for bit); the residual by the rounding
  *                      bound |r - rq sr| <= sr / 2 and the sign of the reconstruction;
+ *   oracle_kmajor_pack / oracle_gemv_km_fold / oracle_select_topk / oracle_apply_corr_km
+ *                      the K-major round trip against a numpy transpose; one-hot x (a single
+ *                      term, so y is PARENT[h] * s or delta * s exactly); the selection
+ *                      against a numpy sort (the nsel-th largest key, ties kept); two-hot x
+ *                      whose exact answers differ between a run (round(P1 + P2) * s) and two
+ *                      parts (round(P1 s) + round(P2 s)); fold plus the full correction
+ *                      against the f64 H-TILE sum;
  *   oracle_int8_pin_* / oracle_int8_tile_f64   BF16 rounding known answers (ties to even on
  *                      exact halfway products), the flat scale index on k_in % 64 != 0
  *                      against a numpy restatement, and exact integer results for
@@ -342,6 +349,132 @@ EXPORT void oracle_int8_tile_f64(const uint16_t *x, const int8_t *q, const float
             y[(int64_t)m * N + n] = acc;
             abs_sum[(int64_t)m * N + n] = aacc;
         }
+}
+
+/* ---------------------------------------------------------------- K-major decode path
+ * K-major layout (p7_glint_select_decode.mojo:126-142, p7_select_device.mojo:196-206):
+ * hole_k[c * N/2 + r/2] holds element (r, c), even r in the low nibble; plug_k the same;
+ * scales_k[(c / 64) * N + r] = absmax[r * K/64 + c / 64]. N even, K % 64 == 0, bs 64. */
+EXPORT void oracle_kmajor_pack(const uint8_t *hole, const uint8_t *plug, const float *absmax, int N, int K,
+                               uint8_t *hole_k, uint8_t *plug_k, float *scales_k) {
+    const int64_t half = N / 2;
+#pragma omp parallel for schedule(static)
+    for (int64_t g = 0; g < (int64_t)K * half; ++g) {
+        const int64_t c = g / half, r0 = 2 * (g % half);
+        const int64_t j0 = r0 * K + c, j1 = (r0 + 1) * K + c;
+        hole_k[g] = (uint8_t)(nib(hole, j0) | (nib(hole, j1) << 4));
+        plug_k[g] = (uint8_t)(nib(plug, j0) | (nib(plug, j1) << 4));
+    }
+    const int nb = K / 64;
+#pragma omp parallel for schedule(static)
+    for (int64_t g = 0; g < (int64_t)N * nb; ++g)
+        scales_k[(g % nb) * N + g / nb] = absmax[g];
+}
+
+static inline int nib_k(const uint8_t *pk, int64_t c, int64_t half, int r) {
+    return (pk[c * half + (r >> 1)] >> (4 * (r & 1))) & 15;
+}
+
+/* Summation orders of the K-major fold and correction. The reference fixes the terms
+ * (p7_glint_gemv_km.mojo:17-94: (PARENT[h] * scale) * x over slices of channels combined
+ * in order) and states that its slice order is a choice validated on its gate; this build
+ * fixes its own order, which the GPU kernels follow exactly:
+ * - a list of channels is cut into KM_SUB equal parts per workgroup;
+ * - each part is walked in order as runs of channels inside one 64-block:
+ *   acc = fmaf(v, x[c], acc) over a run from 0, then t = fmaf(acc, scale(r, block), t);
+ * - the KM_SUB part sums are added in order, then the outer slices in order. */
+#define KM_SUB 8
+
+/* t for channels [c0, c1) of row r; val(r, c) is PARENT[h] (fold) or CELLS[h][p] - PARENT[h]. */
+static float km_runs(const uint8_t *hole_k, const uint8_t *plug_k, const float *scales_k, const uint16_t *x,
+                     const int32_t *list, int i0, int i1, int N, int r, int corr) {
+    const int64_t half = N / 2;
+    float t = 0.f, acc = 0.f;
+    int cur = -1;
+    for (int i = i0; i < i1; ++i) {
+        const int c = list ? list[i] : i;
+        if ((c >> 6) != cur) {
+            if (cur >= 0)
+                t = fmaf(acc, scales_k[(int64_t)cur * N + r], t);
+            cur = c >> 6;
+            acc = 0.f;
+        }
+        const int h = nib_k(hole_k, c, half, r);
+        const float v = corr ? GLINT_CELLS[h][nib_k(plug_k, c, half, r)] - GLINT_PARENT[h] : GLINT_PARENT[h];
+        acc = fmaf(v, bf16_to_f32(x[c]), acc);
+    }
+    if (cur >= 0)
+        t = fmaf(acc, scales_k[(int64_t)cur * N + r], t);
+    return t;
+}
+
+/* Parent-only (fold) GEMV on the K-major hole: y[r] = sum_c PARENT[h] * scale * x[c] with
+ * K cut into ksg outer slices of KM_SUB parts each, in the order above. */
+EXPORT void oracle_gemv_km_fold(const uint8_t *hole_k, const float *scales_k, const uint16_t *x, int N, int K,
+                                int ksg, float *y) {
+    const int ksl = K / ksg, sub = ksl / KM_SUB;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < N; ++r) {
+        float tot = 0.f;
+        for (int g = 0; g < ksg; ++g) {
+            float wg = 0.f;
+            for (int q = 0; q < KM_SUB; ++q) {
+                const int c0 = g * ksl + q * sub;
+                const float t = km_runs(hole_k, NULL, scales_k, x, NULL, c0, c0 + sub, N, r, 0);
+                wg = (q == 0) ? t : wg + t;
+            }
+            tot = (g == 0) ? wg : tot + wg;
+        }
+        y[r] = tot;
+    }
+}
+
+/* Selection (p7_select_device.mojo:1-151, the rank rule): key = bf16 bits & 0x7FFF; T is
+ * the largest 15-bit value with #{key >= T} >= nsel, found bit by bit from the top;
+ * nsel == 0 selects nothing. Writes the kept channels in ascending order, returns the count. */
+EXPORT int oracle_select_topk(const uint16_t *x, int K, int nsel, int32_t *idx) {
+    int thr = 0;
+    for (int bi = 0; bi < 15; ++bi) {
+        const int cand = thr | (1 << (14 - bi));
+        int cnt = 0;
+        for (int i = 0; i < K; ++i)
+            cnt += (x[i] & 0x7FFF) >= cand;
+        if (cnt >= nsel)
+            thr = cand;
+    }
+    if (nsel == 0)
+        thr = 32768;
+    int n = 0;
+    for (int i = 0; i < K; ++i)
+        if ((x[i] & 0x7FFF) >= thr)
+            idx[n++] = i;
+    return n;
+}
+
+/* Plug correction over the selected channels (p7_select_device.mojo:208-236, 253-302):
+ * y[r] = y[r] + sum_i (CELLS[h][p] - PARENT[h]) * scale * x[c_i]. The list is cut into
+ * ks chunks of ceil(cnt / ks), each chunk into KM_SUB parts of ceil(chunk / KM_SUB), summed
+ * in the order above; y is updated in place. */
+EXPORT void oracle_apply_corr_km(const uint8_t *hole_k, const uint8_t *plug_k, const float *scales_k,
+                                 const uint16_t *x, const int32_t *idx, int cnt, int N, int K, int ks, float *y) {
+    (void)K;
+    const int chunk = (cnt + ks - 1) / ks, sub = (chunk + KM_SUB - 1) / KM_SUB;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < N; ++r) {
+        float tot = 0.f;
+        for (int s = 0; s < ks; ++s) {
+            const int lo = s * chunk, hi = lo + chunk < cnt ? lo + chunk : cnt;
+            float wg = 0.f;
+            for (int q = 0; q < KM_SUB; ++q) {
+                const int i0 = lo + q * sub < hi ? lo + q * sub : hi;
+                const int i1 = i0 + sub < hi ? i0 + sub : hi;
+                const float t = km_runs(hole_k, plug_k, scales_k, x, idx, i0, i1, N, r, 1);
+                wg = (q == 0) ? t : wg + t;
+            }
+            tot = (s == 0) ? wg : tot + wg;
+        }
+        y[r] = y[r] + tot;
+    }
 }
 
 EXPORT int oracle_threads(void) {

@@ -220,6 +220,10 @@ class Oracle:
             "oracle_quant_act_resid": ([vp, vp, vp, i32, i32, vp, vp], None),
             "oracle_int8_pin_dequant_bf16": ([vp, vp, i64, vp], None),
             "oracle_int8_tile_f64": ([vp, vp, vp, i32, i32, i32, vp, vp], None),
+            "oracle_kmajor_pack": ([vp, vp, vp, i32, i32, vp, vp, vp], None),
+            "oracle_gemv_km_fold": ([vp, vp, vp, i32, i32, i32, vp], None),
+            "oracle_select_topk": ([vp, i32, i32, vp], i32),
+            "oracle_apply_corr_km": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, vp], None),
             "oracle_threads": ([], i32),
         }
         for name, (args, res) in sig.items():
@@ -343,3 +347,36 @@ class Oracle:
         a = np.empty(M * N, np.float64)
         self.lib.oracle_int8_tile_f64(_ptr(x_u16), _ptr(q), _ptr(scale), M, N, K, _ptr(y), _ptr(a))
         return y.reshape(M, N), a.reshape(M, N)
+
+    def kmajor_pack(self, hole, plug, am, N: int, K: int):
+        hole, plug = np.ascontiguousarray(hole, np.uint8), np.ascontiguousarray(plug, np.uint8)
+        am = np.ascontiguousarray(am, np.float32)
+        assert N % 2 == 0 and K % 64 == 0 and hole.size >= N * K // 2 and am.size >= N * K // 64
+        hk = np.empty(K * N // 2, np.uint8)
+        pk = np.empty(K * N // 2, np.uint8)
+        sk = np.empty(N * K // 64, np.float32)
+        self.lib.oracle_kmajor_pack(_ptr(hole), _ptr(plug), _ptr(am), N, K, _ptr(hk), _ptr(pk), _ptr(sk))
+        return hk, pk, sk
+
+    def gemv_km_fold(self, hole_k, scales_k, x_u16, N: int, K: int, ksg: int = 1) -> np.ndarray:
+        hole_k = np.ascontiguousarray(hole_k, np.uint8)
+        scales_k = np.ascontiguousarray(scales_k, np.float32)
+        x_u16 = np.ascontiguousarray(x_u16, np.uint16)
+        assert K % (64 * ksg) == 0 and hole_k.size >= K * N // 2 and x_u16.size >= K
+        y = np.empty(N, np.float32)
+        self.lib.oracle_gemv_km_fold(_ptr(hole_k), _ptr(scales_k), _ptr(x_u16), N, K, ksg, _ptr(y))
+        return y
+
+    def select_topk(self, x_u16, K: int, nsel: int) -> np.ndarray:
+        x_u16 = np.ascontiguousarray(x_u16, np.uint16)
+        idx = np.empty(max(K, 1), np.int32)
+        n = self.lib.oracle_select_topk(_ptr(x_u16), K, nsel, _ptr(idx))
+        return idx[:n].copy()
+
+    def apply_corr_km(self, hole_k, plug_k, scales_k, x_u16, idx, N: int, K: int, y, ks: int = 1) -> np.ndarray:
+        arrs = [np.ascontiguousarray(a, t) for a, t in ((hole_k, np.uint8), (plug_k, np.uint8),
+                                                          (scales_k, np.float32), (x_u16, np.uint16))]
+        idx = np.ascontiguousarray(idx, np.int32)
+        out = np.array(y, dtype=np.float32, copy=True)
+        self.lib.oracle_apply_corr_km(*[_ptr(a) for a in arrs], _ptr(idx), idx.size, N, K, ks, _ptr(out))
+        return out

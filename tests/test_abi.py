@@ -11,7 +11,7 @@ from glint_amd import glint_hip
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADERS = {
-    "libglint_encode.so": ["glint_encode.h", "glint_htile.h"],
+    "libglint_encode.so": ["glint_encode.h", "glint_htile.h", "glint_select.h"],
     "libp7_kernels.so": ["int8_mma_gemm.h", "int8_tile_gemm.h", "p7_attach.h", "glint_plug_streamer.h"],
 }
 

@@ -1,0 +1,123 @@
+"""GPU parity for the K-major decode path (include/glint_select.h): layout conversion,
+fold GEMV, channel selection and plug correction, each bit for bit against the oracle
+(the kernels keep the oracle's summation orders), plus the chained decode step and the
+argument codes."""
+import numpy as np
+import pytest
+
+from glint_amd import glint_hip as H
+from oracle import glint_oracle as G
+from tests.gpu_util import dev, host, first_diff, torch_cuda
+
+pytestmark = pytest.mark.gpu
+
+
+def _pin(oracle, N, K, seed):
+    rng = np.random.default_rng(seed)
+    w = rng.normal(0, 0.02, N * K).astype(np.float32)
+    w[:64] = 0.0
+    w[rng.integers(0, N * K, 50)] *= 10
+    return oracle.encode_f32(w, 64)
+
+
+def _x(K, seed):
+    return G.f32_to_bf16_bits(np.random.default_rng(seed).normal(0, 1, K).astype(np.float32))
+
+
+PACK_SHAPES = [(8, 64), (24, 192), (104, 640), (1000, 320), (14336, 4096), (4096, 14336)]
+FOLD_SHAPES = [(32, 64), (96, 512), (1024, 320), (2080, 1024), (14336, 4096), (4096, 14336)]
+
+
+@pytest.mark.parametrize("N,K", PACK_SHAPES)
+def test_kmajor_pack_matches_oracle(oracle, N, K):
+    torch_cuda()
+    print(f"kmajor pack N={N} K={K}", flush=True)
+    h, p, am = _pin(oracle, N, K, N + K)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    dhk, dpk, dsk = H.kmajor_pack(dev(h), dev(p), dev(am), N, K)
+    assert host(dhk).tobytes() == hk.tobytes(), first_diff(host(dhk), hk)
+    assert host(dpk).tobytes() == pk.tobytes(), first_diff(host(dpk), pk)
+    assert host(dsk).tobytes() == sk.tobytes()
+
+
+@pytest.mark.parametrize("N,K", FOLD_SHAPES)
+def test_fold_matches_oracle(oracle, N, K):
+    torch_cuda()
+    print(f"fold N={N} K={K}", flush=True)
+    h, p, am = _pin(oracle, N, K, N + K)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    dhk, dsk = dev(hk), dev(sk)
+    x = _x(K, K)
+    dx = dev(x)
+    for ksg in (1, 2, 8):
+        if K % (64 * ksg):
+            continue
+        want = oracle.gemv_km_fold(hk, sk, x, N, K, ksg)
+        got = host(H.gemv_km_fold(dhk, dsk, dx, N, K, ksg))
+        assert got.tobytes() == want.tobytes(), (ksg, first_diff(got.view(np.uint32), want.view(np.uint32)))
+
+
+@pytest.mark.parametrize("K", [1, 64, 1000, 4096, 14336, 32768])
+def test_select_matches_oracle(oracle, K):
+    torch_cuda()
+    print(f"select K={K}", flush=True)
+    x = _x(K, 7 + K)
+    if K > 200:
+        x[100:160] = x[3]  # ties at many thresholds
+    dx = dev(x)
+    for nsel in sorted({0, 1, 2, K // 10, K // 2, K - 1, K, K + 3}):
+        if nsel < 0:
+            continue
+        want = oracle.select_topk(x, K, nsel)
+        idx, cnt = H.select_topk(dx, nsel)
+        n = int(host(cnt)[0])
+        assert n == want.size, (nsel, n, want.size)
+        assert np.array_equal(host(idx)[:n], want), nsel
+
+
+@pytest.mark.parametrize("N,K,frac,ks", [(96, 640, 0.1, 1), (1024, 320, 0.5, 3), (2080, 1024, 0.3, 2),
+                                         (14336, 4096, 0.1, 8), (4096, 14336, 0.05, 1), (4096, 14336, 1.0, 8)])
+def test_decode_step_matches_oracle(oracle, N, K, frac, ks):
+    """fold -> select (on the device) -> correction, every stage bit-exact; with every
+    channel selected the result is the H-TILE GEMV within the f32 bound."""
+    torch = torch_cuda()
+    print(f"decode step N={N} K={K} frac={frac} ks={ks}", flush=True)
+    h, p, am = _pin(oracle, N, K, 3 * N + K)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    x = _x(K, 11 + K)
+    nsel = int(np.ceil(frac * K))
+    ksg = 4 if K % 256 == 0 else 1
+    y0 = oracle.gemv_km_fold(hk, sk, x, N, K, ksg)
+    sel = oracle.select_topk(x, K, nsel)
+    want = oracle.apply_corr_km(hk, pk, sk, x, sel, N, K, y0, ks)
+    dhk, dpk, dsk, dx = dev(hk), dev(pk), dev(sk), dev(x)
+    y = H.gemv_km_fold(dhk, dsk, dx, N, K, ksg)
+    idx, cnt = H.select_topk(dx, nsel)
+    H.apply_corr_km(dhk, dpk, dsk, dx, idx, cnt, y, N, K, ks)
+    got = host(y)
+    assert got.tobytes() == want.tobytes(), first_diff(got.view(np.uint32), want.view(np.uint32))
+    if frac == 1.0:
+        ref, absum = oracle.htile_f64(h, p, am, x, 1, N, K, 64)
+        assert np.all(np.abs(got.astype(np.float64) - ref[0]) <= (K + 4) * 2.0 ** -23 * absum[0] * 2)
+    del torch
+
+
+def test_argument_codes():
+    torch = torch_cuda()
+    lib = H.encode_lib()
+    b = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    f = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    i = torch.zeros(64, dtype=torch.int32, device="cuda")
+    P = lambda t: t.data_ptr()
+    assert lib.glint_kmajor_pack(None, P(b), P(f), 8, 64, P(b), P(b), P(f), None) == -1
+    assert lib.glint_kmajor_pack(P(b), P(b), P(f), 12, 64, P(b), P(b), P(f), None) == -2  # N % 8
+    assert lib.glint_kmajor_pack(P(b), P(b), P(f), 8, 96, P(b), P(b), P(f), None) == -2  # K % 64
+    assert lib.glint_gemv_km_fold(P(b), P(f), P(b), P(f), 32, 128, 2, None, None) == -1  # part needed
+    assert lib.glint_gemv_km_fold(P(b), P(f), P(b), P(f), 32, 192, 2, P(f), None) == -2  # K % (64 ksg)
+    assert lib.glint_gemv_km_fold(P(b), P(f), P(b), P(f), 40, 128, 1, None, None) == -2  # N % 32
+    assert lib.glint_select_topk(P(b), 0, 1, P(i), P(i), None) == -2
+    assert lib.glint_select_topk(P(b), 40000, 1, P(i), P(i), None) == -2
+    assert lib.glint_select_topk(P(b), 64, -1, P(i), P(i), None) == -2
+    assert lib.glint_apply_corr_km(P(b), P(b), P(f), P(b), P(i), P(i), P(f), 32, 64, 2, None, None) == -1
+    assert lib.glint_apply_corr_km(P(b), P(b), P(f), P(b), P(i), P(i), P(f), 48, 64, 1, None, None) == -2
+    torch.cuda.synchronize()

@@ -447,6 +447,115 @@ def test_int8_tile_f64_is_exact_on_dyadic_data(oracle):
     assert np.array_equal(y, want) and np.array_equal(a, want_abs)
 
 
+# ------------------------------------------------------------- K-major decode path
+def _pin_planes(oracle, N, K, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.normal(0, 0.02, N * K)).astype(np.float32)
+    w[: 64] = 0.0
+    return oracle.encode_f32(w, 64)
+
+
+def test_kmajor_pack_is_the_transpose(oracle):
+    """hole_k[c N/2 + r/2] is element (r, c), even r low (p7_glint_select_decode.mojo:126-142);
+    scales_k[(c/64) N + r] = absmax[r K/64 + c/64] (p7_select_device.mojo:196-206), checked
+    against a numpy transpose of the unpacked planes."""
+    N, K = 24, 192
+    h, p, am = _pin_planes(oracle, N, K, 1)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    for src, dst in ((h, hk), (p, pk)):
+        nib = G.unpack_nibbles(src, N * K).reshape(N, K).T.reshape(-1)
+        assert np.array_equal(G.pack_nibbles(nib), dst)
+    assert np.array_equal(sk, am.reshape(N, K // 64).T.reshape(-1))
+
+
+def test_fold_and_correction_on_one_hot_x(oracle):
+    """x = e_c: the fold is PARENT[h(r, c)] * scale(r, c) exactly and the correction over
+    [c] adds (CELLS[h][p] - PARENT[h]) * scale exactly (one nonzero term), for every slice
+    and chunk count."""
+    N, K = 16, 256
+    h, p, am = _pin_planes(oracle, N, K, 2)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    H = G.unpack_nibbles(h, N * K).reshape(N, K)
+    Pn = G.unpack_nibbles(p, N * K).reshape(N, K)
+    A = am.reshape(N, K // 64)
+    for c in (0, 63, 64, 200, 255):
+        x = np.zeros(K, np.uint16)
+        x[c] = 0x3F80  # 1.0
+        want_fold = (G.PARENT_F32[H[:, c]] * A[:, c // 64]).astype(np.float32)
+        for ksg in (1, 2, 4):
+            assert oracle.gemv_km_fold(hk, sk, x, N, K, ksg).tobytes() == want_fold.tobytes()
+        d = (G.CELLS_F32[H[:, c], Pn[:, c]] - G.PARENT_F32[H[:, c]]).astype(np.float32)
+        want_corr = (np.zeros(N, np.float32) + (d * A[:, c // 64]).astype(np.float32))  # y starts at +0
+        for ks in (1, 3):
+            got = oracle.apply_corr_km(hk, pk, sk, x, np.array([c], np.int32), N, K, np.zeros(N, np.float32), ks)
+            assert got.tobytes() == want_corr.tobytes()
+
+
+def test_fold_order_runs_and_parts(oracle):
+    """Two channels of one 64-block in one part form a run: round(round(P1 + P2) * s). In
+    different parts (K/ksg/8 channels each) they are two terms: round(round(P1 s) + round(P2 s)).
+    Both are computed exactly in float64 (a sum or product of two f32 is exact there) and
+    rounded once, so a different order shows."""
+    N, K = 8, 1024
+    h, p, am = _pin_planes(oracle, N, K, 6)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    Hn = G.unpack_nibbles(h, N * K).reshape(N, K)
+    A = am.reshape(N, K // 64).astype(np.float64)
+    P = G.PARENT_F32.astype(np.float64)
+    f32 = lambda v: np.asarray(v, np.float64).astype(np.float32)
+    ksg = 2  # parts of 1024 / 2 / 8 = 64 channels: block b is part b within its slice
+    for c1, c2, same_part in ((130, 140, True), (190, 200, False)):
+        x = np.zeros(K, np.uint16)
+        x[c1] = x[c2] = 0x3F80
+        got = oracle.gemv_km_fold(hk, sk, x, N, K, ksg)
+        b1, b2 = c1 // 64, c2 // 64
+        if same_part:
+            assert b1 == b2
+            want = f32(f32(P[Hn[:, c1]] + P[Hn[:, c2]]).astype(np.float64) * A[:, b1])
+        else:
+            assert b1 != b2
+            t1, t2 = f32(P[Hn[:, c1]] * A[:, b1]), f32(P[Hn[:, c2]] * A[:, b2])
+            want = f32(t1.astype(np.float64) + t2.astype(np.float64))
+        assert got.tobytes() == want.tobytes(), (c1, c2)
+
+
+def test_select_matches_a_sort(oracle):
+    """The kept set is every channel whose key (bf16 bits & 0x7FFF) is at least the nsel-th
+    largest key, ties all kept, in ascending order; nsel = 0 keeps nothing and nsel >= K
+    keeps everything (p7_select_device.mojo:1-151)."""
+    rng = np.random.default_rng(3)
+    K = 1000
+    x = G.f32_to_bf16_bits(rng.normal(0, 1, K).astype(np.float32))
+    x[100:140] = x[7]  # a block of ties
+    x[500] |= 0x8000   # sign does not matter
+    keys = x & 0x7FFF
+    desc = np.sort(keys)[::-1]
+    for nsel in (0, 1, 2, 30, 33, 500, K - 1, K, K + 5):
+        got = oracle.select_topk(x, K, nsel)
+        if nsel == 0:
+            want = np.zeros(0, np.int32)
+        elif nsel >= K:
+            want = np.arange(K, dtype=np.int32)
+        else:
+            want = np.flatnonzero(keys >= desc[nsel - 1]).astype(np.int32)
+        assert np.array_equal(got, want), nsel
+        assert nsel == 0 or got.size >= min(nsel, K)
+
+
+def test_fold_plus_full_correction_is_the_htile_sum(oracle):
+    """PARENT + (CELLS - PARENT) = CELLS: fold plus the correction over every channel is the
+    H-TILE GEMV up to f32 rounding, bounded by (K + 4) 2^-23 sum |terms| against float64."""
+    N, K = 32, 512
+    h, p, am = _pin_planes(oracle, N, K, 4)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    x = G.f32_to_bf16_bits(np.random.default_rng(5).normal(0, 1, K).astype(np.float32))
+    ref, absum = oracle.htile_f64(h, p, am, x, 1, N, K, 64)
+    for ksg, ks in ((1, 1), (4, 8)):
+        y = oracle.gemv_km_fold(hk, sk, x, N, K, ksg)
+        y = oracle.apply_corr_km(hk, pk, sk, x, np.arange(K, dtype=np.int32), N, K, y, ks)
+        assert np.all(np.abs(y.astype(np.float64) - ref[0]) <= (K + 4) * 2.0 ** -23 * absum[0] * 2)
+
+
 # ------------------------------------------------------- the pins catch planted mistakes
 def test_planted_mistakes_are_caught():
     """Mutations of the numpy oracle that a plausible bug would introduce must fail
