@@ -53,6 +53,18 @@ def timed(torch, fns, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / steps
 
 
+def settle(torch, fns, seconds: float = 0.05):
+    """Untimed launches for about `seconds` before a timed loop, so the GPU is at its
+    steady clock and power state when the warmup steps and the timed steps run."""
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(100):
+            fns[i % len(fns)]()
+            i += 1
+        torch.cuda.synchronize()
+
+
 def bound(fn, *args):
     """A zero-argument call of the C-ABI function `fn` with its arguments converted once
     (tensors to device pointers, ints to C ints), so the timed loop pays only the ctypes
@@ -99,6 +111,7 @@ def bench_gemv(torch, H, steps, warmup, headline_only=False):
     y = torch.empty(N, dtype=torch.bfloat16, device="cuda")
     lib, st = H.encode_lib(), stream_handle(torch)
     fns = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, y, 1, N, K, 64, st) for p in pins]
+    settle(torch, fns)
     ms = timed(torch, fns, steps, warmup)
     if headline_only:
         return {"ms": ms, "bytes": per, "gbs": per / ms / 1e6, "copies": copies, "rotation_bytes": copies * per}, pins, x
