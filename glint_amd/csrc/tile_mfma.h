@@ -14,8 +14,8 @@
  * K quarter t % 4 (so BN * 4 == threads), and stages BM * 8 / threads 16-B chunks of x.
  * Each operand has two LDS buffers: step kb runs its MFMAs from buffer kb & 1, then the
  * threads write step kb + 1 into the other (its global loads went out two steps earlier),
- * so a K step needs one barrier. LDS rows are 80 BF16 (160 B): with 72-element rows the
- * bank-conflict counter read 4x higher for the same work.
+ * so a K step needs one barrier. LDS rows are 64 BF16 with an XOR swizzle of their 16-byte
+ * chunks (tile_ofs).
  *
  * MFMA operand layout (16x16x32 bf16): lane l supplies row l % 16, k [(l / 16) * 8, +8)
  * of each operand; accumulator i of lane l is D[(l / 16) * 4 + i][l % 16].
@@ -34,7 +34,14 @@ __device__ __forceinline__ uint32_t glint_cvt_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(glint_f32x2{lo, hi}, glint_bf16x2));
 }
 
-#define TILE_LDW 80 /* BF16 per LDS row: 64 + 16 */
+/* 128-byte LDS rows (64 BF16), 16-byte chunk c of row r stored at chunk c ^ f(r) with
+ * f(r) = ((r >> 1) ^ ((r & 1) << 2)) & 7: the 16 rows of a fragment read (one chunk) then
+ * hit distinct banks in every group of 8 lanes and in every group of 16. (Measured no
+ * faster than 160-byte padded rows, with 20% less LDS.) */
+#define TILE_LDW 64
+__device__ __forceinline__ int tile_ofs(int r, int c) {
+    return r * TILE_LDW + ((c ^ (((r >> 1) ^ ((r & 1) << 2)) & 7)) << 3);
+}
 
 struct TileOutBF16 {
     typedef uint16_t T;
@@ -158,12 +165,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
     auto produce = [&](int buf, const Stage &st) {
         uint32_t packed[8];
         p.produce(st.w, packed, lane);
-        glint_u32x4 *dst = (glint_u32x4 *)(sW[buf] + wr * TILE_LDW + wq * 16);
-        dst[0] = glint_u32x4{packed[0], packed[1], packed[2], packed[3]};
-        dst[1] = glint_u32x4{packed[4], packed[5], packed[6], packed[7]};
+        *(glint_u32x4 *)(sW[buf] + tile_ofs(wr, 2 * wq)) = glint_u32x4{packed[0], packed[1], packed[2], packed[3]};
+        *(glint_u32x4 *)(sW[buf] + tile_ofs(wr, 2 * wq + 1)) = glint_u32x4{packed[4], packed[5], packed[6], packed[7]};
 #pragma unroll
         for (int i = 0; i < XV; ++i)
-            *(glint_u32x4 *)(sX[buf] + (xr + (T / 8) * i) * TILE_LDW + xc * 8) = st.x[i];
+            *(glint_u32x4 *)(sX[buf] + tile_ofs(xr + (T / 8) * i, xc)) = st.x[i];
     };
     /* step kb: MFMAs from buffer kb & 1, step kb + 1 (in `next`) into the other buffer, then
      * `next` is refilled with step kb + 3 */
@@ -171,20 +177,18 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
         const int cur = kb & 1;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const int kofs = ks * 32 + (lane >> 4) * 8;
+            /* rows (16-row tile base) + lane % 16, chunk 4 ks + lane / 16; the swizzle does not
+             * change when a row moves by a multiple of 16 */
+            const int fofs = tile_ofs(lane & 15, 4 * ks + (lane >> 4));
             glint_bf16x8 af[TM], bfr[TN];
 #pragma unroll
             for (int a = 0; a < TM; ++a)
-                af[a] = __builtin_bit_cast(glint_bf16x8, *(const glint_u32x4 *)(sX[cur] +
-                                                                               (wm * TM * 16 + a * 16 + (lane & 15)) *
-                                                                                   TILE_LDW +
-                                                                               kofs));
+                af[a] = __builtin_bit_cast(glint_bf16x8,
+                                           *(const glint_u32x4 *)(sX[cur] + (wm * TM * 16 + a * 16) * TILE_LDW + fofs));
 #pragma unroll
             for (int b = 0; b < TN; ++b)
-                bfr[b] = __builtin_bit_cast(glint_bf16x8, *(const glint_u32x4 *)(sW[cur] +
-                                                                                (wn * TN * 16 + b * 16 + (lane & 15)) *
-                                                                                    TILE_LDW +
-                                                                                kofs));
+                bfr[b] = __builtin_bit_cast(glint_bf16x8,
+                                            *(const glint_u32x4 *)(sW[cur] + (wn * TN * 16 + b * 16) * TILE_LDW + fofs));
 #pragma unroll
             for (int a = 0; a < TM; ++a)
 #pragma unroll
