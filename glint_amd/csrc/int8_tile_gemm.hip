@@ -78,6 +78,132 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
         }
 }
 
+/* ---------------------------------------------------------- small m: GEMV-shaped */
+/* m <= 4, k_in % 2048 == 0, k_in / 2048 <= 8 (the decode shapes). Like the GLINT decode
+ * GEMV: the row is cut into S = k_in / 2048 slices, wave (s, g) keeps slice s of the m
+ * activation rows in registers (32 f32 per lane per row) and streams weight rows
+ * r0 + g, r0 + g + G, ... of its workgroup's row range: per row each lane reads 32 int8
+ * (two 16-B loads, one 64-block, so one scale). Weights are rounded to BF16 exactly as the
+ * tile kernels do (v_cvt_pk_bf16_f32 of q * scale); products accumulate with f32 FMAs.
+ * Three rows are in flight per wave; loads are unconditional (rows clamped at the end).
+ * A row's S slice sums (DPP within the wave) meet in LDS and are added in slice order. */
+#define I8V_THREADS 512
+#define I8V_DEPTH 3
+#define I8V_RED_MAX 8192 /* floats of row partials a workgroup may park in LDS */
+
+struct I8Row {
+    glint_u32x4 q0, q1;
+    float s;
+};
+
+template <int MR>
+__global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *__restrict__ q,
+                                                             const float *__restrict__ scale,
+                                                             const glint_u32x4 *__restrict__ x, float *__restrict__ y,
+                                                             int N, int K, int G, int rows_per_wg) {
+    extern __shared__ __attribute__((aligned(16))) float red[]; /* [rows][S][MR] */
+    const int lane = threadIdx.x & 63;
+    const int S = K >> 11;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int s = w % S, g = w / S;
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int nrows = max(min(rows_per_wg, N - r0), 0);
+    const int my = g < nrows ? (nrows - g + G - 1) / G : 0;
+    const int64_t kv = K >> 4;                     /* 16-B vectors per weight row */
+    const int64_t j = (int64_t)(s * 64 + lane) * 2; /* this lane's two vectors in a row */
+    auto row_of = [&](int i) -> int64_t { return (int64_t)min(r0 + g + min(i, max(my - 1, 0)) * G, N - 1); };
+    auto load = [&](int i, I8Row &r) {
+        const int64_t n = row_of(i);
+        r.q0 = __builtin_nontemporal_load(&q[n * kv + j]);
+        r.q1 = __builtin_nontemporal_load(&q[n * kv + j + 1]);
+        r.s = scale[n * (K >> 6) + (j >> 2)];
+    };
+    /* x: this lane's 32 activations of each of the MR rows, as f32 */
+    float xr[MR][32];
+#pragma unroll
+    for (int mr = 0; mr < MR; ++mr)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const glint_u32x4 v = x[(int64_t)mr * (K >> 3) + (s * 64 + lane) * 4 + h];
+            const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xr[mr][8 * h + 2 * e] = glint_bf16lo(d[e]);
+                xr[mr][8 * h + 2 * e + 1] = glint_bf16hi(d[e]);
+            }
+        }
+    I8Row buf[I8V_DEPTH];
+#pragma unroll
+    for (int d = 0; d < I8V_DEPTH; ++d)
+        load(d, buf[d]);
+    auto compute = [&](int i, const I8Row &r) {
+        const uint32_t W[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        float part[MR];
+#pragma unroll
+        for (int mr = 0; mr < MR; ++mr)
+            part[mr] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const float lo = (float)(int8_t)(W[e] >> (16 * b)) * r.s;
+                const float hi = (float)(int8_t)(W[e] >> (16 * b + 8)) * r.s;
+                const uint32_t pk = glint_cvt_bf16x2(lo, hi);
+                const float wl = glint_bf16lo(pk), wh = glint_bf16hi(pk);
+#pragma unroll
+                for (int mr = 0; mr < MR; ++mr) {
+                    part[mr] = fmaf(wl, xr[mr][4 * e + 2 * b], part[mr]);
+                    part[mr] = fmaf(wh, xr[mr][4 * e + 2 * b + 1], part[mr]);
+                }
+            }
+#pragma unroll
+        for (int mr = 0; mr < MR; ++mr) {
+            float v = glint_row16_sum(part[mr]);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (lane == 0)
+                red[((g + i * G) * S + s) * MR + mr] = v;
+        }
+    };
+    int i = 0;
+    for (; i + I8V_DEPTH <= my; i += I8V_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < I8V_DEPTH; ++d) {
+            compute(i + d, buf[d]);
+            load(i + d + I8V_DEPTH, buf[d]);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < I8V_DEPTH - 1; ++d)
+        if (i + d < my)
+            compute(i + d, buf[d]);
+    __syncthreads();
+    for (int t = threadIdx.x; t < nrows * MR; t += blockDim.x) {
+        const int row = t / MR, mr = t % MR;
+        float sum = red[(row * S) * MR + mr];
+        for (int k = 1; k < S; ++k)
+            sum += red[(row * S + k) * MR + mr];
+        y[(int64_t)mr * N + r0 + row] = sum;
+    }
+}
+
+template <int MR>
+static void i8tile_launch_gemv(const uint16_t *x, const Int8PinLinear &w, float *y, hipStream_t st) {
+    const int S = w.k_in / 2048, G = (I8V_THREADS / 64) / S, threads = 64 * S * G;
+    auto kern = k_i8tile_gemv<MR>;
+    const int64_t resident = glint_resident_grid((const void *)kern, threads, I8V_RED_MAX * 4);
+    const int64_t per_wave = ((int64_t)w.n_out + G * resident - 1) / (G * resident);
+    int64_t rows_per_wg = G * per_wave;
+    const int64_t cap = (I8V_RED_MAX / (S * MR)) / G * G;
+    if (rows_per_wg > cap)
+        rows_per_wg = cap;
+    const unsigned grid = (unsigned)((w.n_out + rows_per_wg - 1) / rows_per_wg);
+    const size_t lds = (size_t)rows_per_wg * S * MR * sizeof(float);
+    glint_set_lds_limit((const void *)kern, I8V_RED_MAX * 4);
+    kern<<<grid, threads, lds, st>>>((const glint_u32x4 *)w.q, w.scale, (const glint_u32x4 *)x, y, w.n_out, w.k_in, G,
+                                     (int)rows_per_wg);
+}
+
 template <int BM, int BN, int WM, int WN>
 static void i8tile_launch_fast(const uint16_t *x, const Int8PinLinear &w, float *y, int m, hipStream_t st) {
     const Int8PinTileProducer p{(const glint_u32x4 *)w.q, w.scale, w.n_out, w.k_in};
@@ -100,7 +226,16 @@ GLINT_API int int8_tile_gemm_bf16(const void *x_bf16, Int8PinLinear w, float *y,
     const uint16_t *x = (const uint16_t *)x_bf16;
     const bool fast = (w.k_in % INT8_PIN_BLOCK) == 0 && glint_aligned(x, 16) && glint_aligned(w.q, 16) &&
                       glint_aligned(w.scale, 4);
-    if (fast) {
+    if (fast && m <= 4 && (w.k_in % 2048) == 0 && w.k_in / 2048 <= I8V_THREADS / 64) {
+        if (m == 1)
+            i8tile_launch_gemv<1>(x, w, y, stream);
+        else if (m == 2)
+            i8tile_launch_gemv<2>(x, w, y, stream);
+        else if (m == 3)
+            i8tile_launch_gemv<3>(x, w, y, stream);
+        else
+            i8tile_launch_gemv<4>(x, w, y, stream);
+    } else if (fast) {
         if (m >= 256)
             i8tile_launch_fast<256, 128, 4, 2>(x, w, y, m, stream);
         else if (m > 64)

@@ -84,6 +84,39 @@ def test_large_m_tiles(oracle, m, n, k):
         _check(oracle, y[rows], xs, q, s, rows.size, n, k, "large (row sample)")
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (1, 4096, 14336), (2, 1000, 2048), (3, 129, 16384),
+                                   (4, 520, 6144), (1, 1, 2048)])
+def test_small_m_gemv_path(oracle, m, n, k):
+    """m <= 4 with k_in % 2048 == 0 takes the GEMV-shaped kernel: same bound as the tiles."""
+    print(f"int8_tile gemv m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(m * 31 + n + k)
+    x, q, s = _case(rng, m, n, k)
+    y = host(H.int8_tile_gemm(dev(x), dev(q), dev(s), n, k, m=m))
+    if n * k <= 1 << 26:
+        _check(oracle, y, x, q, s, m, n, k, "gemv")
+    else:  # a column sample: rows of W
+        cols = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, 40)]))
+        qs = q.reshape(n, k)[cols].reshape(-1)
+        ss = s.reshape(n, k // 64)[cols].reshape(-1)
+        _check(oracle, y.reshape(m, n)[:, cols], x, qs, ss, m, cols.size, k, "gemv (row sample)")
+
+
+def test_small_m_gemv_one_hot_is_exact(oracle):
+    """x = e_c on the GEMV path: y[n] = BF16(q[n, c] * scale) for every row."""
+    n, k = 300, 2048
+    rng = np.random.default_rng(8)
+    q = rng.integers(-127, 128, n * k, dtype=np.int8)
+    s = np.ldexp(1.0 + rng.random(n * k // 64), rng.integers(-12, -4, n * k // 64)).astype(np.float32)
+    w = oracle.int8_pin_dequant_bf16(q, s).reshape(n, k)
+    dq, ds = dev(q), dev(s)
+    for c in (0, 1, 63, 64, 1000, 2047):
+        x = np.zeros(k, np.uint16)
+        x[c] = 0x3F80
+        y = host(H.int8_tile_gemm(dev(x), dq, ds, n, k, m=1))
+        want = (w[:, c].astype(np.uint32) << 16).view(np.float32)
+        assert y.view(np.uint32).tobytes() == want.view(np.uint32).tobytes(), c
+
+
 @pytest.mark.parametrize("k,aligned", [(64, True), (128, True), (640, True), (100, False), (37, False)])
 def test_one_hot_rows_give_the_dequantized_weights_exactly(oracle, k, aligned):
     """x = I (m = k one-hot rows): y[m, n] = BF16(q[n, m] * scale) exactly, since every sum
