@@ -362,6 +362,18 @@ def bench_kmajor(torch, H, steps: int = 100, copies: int = 20):
             "select_ms": ms_sel, "corr_ms": ms_corr, "selected": int(cnt.item())}
 
 
+def bench_copy_ceiling(torch, mib: int = 1024):
+    """A plain device-to-device copy (torch's copy kernel) of `mib` MiB: the mixed
+    read+write rate this HBM reaches with the simplest access pattern, the practical
+    ceiling next to 8 TB/s for encode and expand (which read and write)."""
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    ms = timed(torch, [lambda: dst.copy_(src)], 20, 3)
+    del src, dst
+    return {"bytes_moved": 2 * n, "ms": ms, "gbs": 2 * n / ms / 1e6, "frac": 2 * n / ms / 1e6 / HBM_PEAK_GBS}
+
+
 def bench_pin_tools(tensors: int = 16):
     """The pin tools' device path end to end: convert a synthetic two-shard BF16 model
     (tensors x 4096 x 4096) from safetensors files to a pin and unpin it back to BF16.
@@ -571,6 +583,8 @@ def main() -> int:
     torch.cuda.empty_cache()
     extra = {}
     if not args.quick:
+        extra["hbm_copy_1gib"] = bench_copy_ceiling(torch)
+        log(f"device copy 1 GiB {extra['hbm_copy_1gib']['gbs']:.0f} GB/s (read + write)")
         extra["encode_4096x4096"] = bench_encode_4096(torch, H)
         log(f"encode 4096^2 {extra['encode_4096x4096']['encode_bf16_in_gbs']:.0f} GB/s bf16-in")
         extra["model_encode"] = bench_model_encode(torch, H, passes=3)

@@ -87,8 +87,12 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
  * tile kernels do (v_cvt_pk_bf16_f32 of q * scale); products accumulate with f32 FMAs.
  * Three rows are in flight per wave; loads are unconditional (rows clamped at the end).
  * A row's S slice sums (DPP within the wave) meet in LDS and are added in slice order. */
+#ifndef I8V_THREADS
 #define I8V_THREADS 512
+#endif
+#ifndef I8V_DEPTH
 #define I8V_DEPTH 3
+#endif
 #define I8V_RED_MAX 8192 /* floats of row partials a workgroup may park in LDS */
 
 struct I8Row {
