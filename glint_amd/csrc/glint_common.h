@@ -218,6 +218,23 @@ static inline int64_t glint_resident_grid(const void *kernel, int threads, size_
     return blocks;
 }
 
+/* CUs of the current device (256 if the runtime cannot say), cached per device. */
+static inline int glint_cu_count() {
+    static std::mutex mu;
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
 /* Raise a kernel's dynamic-LDS limit to `bytes` on the current device (needed above
  * 64 KiB); remembered per (kernel, device). Returns 0 or -1. */
 static inline int glint_set_lds_limit(const void *kernel, size_t bytes) {

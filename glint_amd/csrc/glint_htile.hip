@@ -476,6 +476,12 @@ __global__ __launch_bounds__(256) void k_htile_generic(const uint8_t *__restrict
 /* Prefill GEMM, large M: the shared double-buffered tile kernel with 256 (M) x 128 (N)
  * blocks over 8 waves in 4 x 2 (wave tile 64 x 64); each thread dequantizes 16 weights
  * (8 B of each plane) per K step through the 32-copy cell table. */
+#ifndef TILE_R_SMALL
+#define TILE_R_SMALL 4 /* register stages (K steps of loads in flight) of the 64- and 128-row tiles */
+#endif
+#ifndef TILE_R_BIG
+#define TILE_R_BIG 2 /* the same for the 256 x 128 tiles */
+#endif
 #define MF2_BM 256
 #define MF2_BN 128
 #ifndef MF2_MIN_M
@@ -510,14 +516,11 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         const uint16_t *xb = (const uint16_t *)x;
         uint16_t *yb = (uint16_t *)y;
         if (M <= 64)
-            k_tile_mfma<64, 64, 2, 2, GlintTileProducer, TileOutBF16>
-                <<<dim3((N + 63) / 64, (M + 63) / 64), 256, 0, st>>>(p, xb, yb, M, N, K);
+            tile_mfma_launch<64, 64, 2, 2, TILE_R_SMALL, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
         else if (M < MF2_MIN_M)
-            k_tile_mfma<128, 64, 2, 2, GlintTileProducer, TileOutBF16>
-                <<<dim3((N + 63) / 64, (M + 127) / 128), 256, 0, st>>>(p, xb, yb, M, N, K);
+            tile_mfma_launch<128, 64, 2, 2, TILE_R_SMALL, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
         else
-            k_tile_mfma<MF2_BM, MF2_BN, 4, 2, GlintTileProducer, TileOutBF16>
-                <<<dim3((N + MF2_BN - 1) / MF2_BN, (M + MF2_BM - 1) / MF2_BM), 512, 0, st>>>(p, xb, yb, M, N, K);
+            tile_mfma_launch<MF2_BM, MF2_BN, 4, 2, TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
     } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS / 64) {
         const int S = K / (64 * GEMV_X_EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
         /* K / 8 chunks of x over 64 S G threads: 4 / G per thread */

@@ -208,14 +208,13 @@ static void i8tile_launch_gemv(const uint16_t *x, const Int8PinLinear &w, float 
                                      (int)rows_per_wg);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int R>
 static void i8tile_launch_fast(const uint16_t *x, const Int8PinLinear &w, float *y, int m, hipStream_t st) {
     const Int8PinTileProducer p{(const glint_u32x4 *)w.q, w.scale, w.n_out, w.k_in};
-    const unsigned gx = (unsigned)((w.n_out + BN - 1) / BN);
     for (int64_t r0 = 0; r0 < m; r0 += (int64_t)I8_MAX_YBLOCKS * BM) {
         const int mm = (int)std::min<int64_t>((int64_t)I8_MAX_YBLOCKS * BM, m - r0);
-        k_tile_mfma<BM, BN, WM, WN, Int8PinTileProducer, TileOutF32><<<dim3(gx, (mm + BM - 1) / BM), 64 * WM * WN, 0, st>>>(
-            p, x + r0 * w.k_in, y + r0 * w.n_out, mm, w.n_out, w.k_in);
+        tile_mfma_launch<BM, BN, WM, WN, R, Int8PinTileProducer, TileOutF32>(p, x + r0 * w.k_in, y + r0 * w.n_out, mm,
+                                                                            w.n_out, w.k_in, st);
     }
 }
 
@@ -241,11 +240,11 @@ GLINT_API int int8_tile_gemm_bf16(const void *x_bf16, Int8PinLinear w, float *y,
             i8tile_launch_gemv<4>(x, w, y, stream);
     } else if (fast) {
         if (m >= 256)
-            i8tile_launch_fast<256, 128, 4, 2>(x, w, y, m, stream);
+            i8tile_launch_fast<256, 128, 4, 2, 2>(x, w, y, m, stream);
         else if (m > 64)
-            i8tile_launch_fast<128, 64, 2, 2>(x, w, y, m, stream);
+            i8tile_launch_fast<128, 64, 2, 2, 4>(x, w, y, m, stream);
         else
-            i8tile_launch_fast<64, 64, 2, 2>(x, w, y, m, stream);
+            i8tile_launch_fast<64, 64, 2, 2, 4>(x, w, y, m, stream);
     } else {
         const unsigned gx = (unsigned)((w.n_out + I8G_N - 1) / I8G_N);
         for (int64_t r0 = 0; r0 < m; r0 += (int64_t)I8_MAX_YBLOCKS * I8G_M) {

@@ -133,3 +133,58 @@ def test_bf16_prefill_tiles_rel_frobenius(oracle, M, N, K):
     # every row and column was written (no stale tile): max error per row bounded too
     row_rel = torch.linalg.norm(y - ref, dim=1) / torch.linalg.norm(ref, dim=1)
     assert float(row_rel.max()) <= 1e-2
+
+
+SPLIT_SHAPES = [(64, 64, 2368), (40, 200, 1088), (64, 14336, 4096), (64, 4096, 14336), (200, 512, 8192),
+                (512, 4096, 14336)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
+def test_bf16_split_k(oracle, M, N, K):
+    """Shapes whose output tiles alone would leave most of the device idle split K over
+    several workgroups per tile (K = 64 * 37 gives a ragged last split); the last workgroup
+    of a tile adds the partial tiles in split order. Checked: relative Frobenius error
+    against fp32 on the expanded weights (a lost or doubled partial fails it), every row
+    bounded, bitwise-equal repeats, and bitwise-equal results from two streams running at
+    once (each stream has its own partials and counters)."""
+    torch = torch_cuda()
+    print(f"split-K M={M} N={N} K={K}", flush=True)
+    hole, plug, am = _encoded_weight(oracle, N, K, 3005 + K)
+    g = torch.Generator(device="cuda").manual_seed(3006 + M)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    y = H.htile_bf16(hole, plug, am, x, N, K, 64)
+    w = H.expand_f32(hole, plug, am, N * K, 64).reshape(N, K)
+    ref = x.float() @ w.T
+    yf = y.float()
+    rel = float(torch.linalg.norm(yf - ref) / torch.linalg.norm(ref))
+    assert rel <= 4e-3, rel
+    row_rel = torch.linalg.norm(yf - ref, dim=1) / torch.linalg.norm(ref, dim=1)
+    assert float(row_rel.max()) <= 1e-2
+    del w, ref
+    again = H.htile_bf16(hole, plug, am, x, N, K, 64)
+    assert torch.equal(again.view(torch.int16), y.view(torch.int16))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for s in (s1, s2, s1, s2):
+        with torch.cuda.stream(s):
+            outs.append(H.htile_bf16(hole, plug, am, x, N, K, 64, stream=s))
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o.view(torch.int16), y.view(torch.int16))
+
+
+def test_bf16_split_k_workspace_growth(oracle):
+    """A small split launch, then a larger one (the stream's workspace grows), then the small
+    one again: the repeat equals the first result bit for bit (counters were left at zero)."""
+    torch = torch_cuda()
+    res = []
+    for (M, N, K) in [(64, 64, 2368), (64, 4096, 14336), (64, 64, 2368)]:
+        print(f"split-K growth M={M} N={N} K={K}", flush=True)
+        hole, plug, am = _encoded_weight(oracle, N, K, 3100 + N)
+        g = torch.Generator(device="cuda").manual_seed(3101)
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        res.append(H.htile_bf16(hole, plug, am, x, N, K, 64))
+    torch.cuda.synchronize()
+    assert torch.equal(res[0].view(torch.int16), res[2].view(torch.int16))

@@ -70,7 +70,7 @@ def test_unaligned_pointers(oracle, x_off, q_off, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(256, 129, 1024), (300, 1000, 576), (513, 64, 64), (2048, 384, 640),
-                                   (1024, 4096, 4096)])
+                                   (1024, 4096, 4096), (64, 14336, 4096), (64, 4096, 14336), (100, 200, 8192)])
 def test_large_m_tiles(oracle, m, n, k):
     print(f"int8_tile large m={m} n={n} k={k}", flush=True)
     rng = np.random.default_rng(m + n + k)
