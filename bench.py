@@ -111,7 +111,7 @@ def bench_gemv(torch, H, steps, warmup, headline_only=False):
     y = torch.empty(N, dtype=torch.bfloat16, device="cuda")
     lib, st = H.encode_lib(), stream_handle(torch)
     fns = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, y, 1, N, K, 64, st) for p in pins]
-    settle(torch, fns)
+    settle(torch, fns, 0.2)
     ms = timed(torch, fns, steps, warmup)
     if headline_only:
         return {"ms": ms, "bytes": per, "gbs": per / ms / 1e6, "copies": copies, "rotation_bytes": copies * per}, pins, x
@@ -549,8 +549,8 @@ def load_traffic():
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--quick", action="store_true", help="headline GEMV only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",

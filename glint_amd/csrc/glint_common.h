@@ -39,6 +39,29 @@ __device__ __forceinline__ void glint_fill_cells_lds(float *ltab, float *stage) 
     __syncthreads();
 }
 
+/* The same 32-copy table, filled straight from the constant table with 16-B stores:
+ * thread t writes runs r = t, t + blockDim.x, ... of 4 words; run r holds 4 copies of cell
+ * r / 8. A thread's loads all go out before its stores. Ends with a barrier. */
+__device__ __forceinline__ void glint_fill_cells_lds_direct(float *ltab) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    constexpr int RUNS = GLINT_LDS_CELLS_WORDS / 4;
+    if (blockDim.x == 256) {
+        float v[RUNS / 256];
+#pragma unroll
+        for (int k = 0; k < RUNS / 256; ++k)
+            v[k] = (&kCells[0][0])[((int)threadIdx.x + 256 * k) >> 3];
+#pragma unroll
+        for (int k = 0; k < RUNS / 256; ++k)
+            ((f32x4 *)ltab)[threadIdx.x + 256 * k] = f32x4{v[k], v[k], v[k], v[k]};
+    } else {
+        for (int r = threadIdx.x; r < RUNS; r += blockDim.x) {
+            const float v = (&kCells[0][0])[r >> 3];
+            ((f32x4 *)ltab)[r] = f32x4{v, v, v, v};
+        }
+    }
+    __syncthreads();
+}
+
 /* 64-copy layout for the streaming kernels: word (c << 6) | lane, i.e. byte address
  * c * 256 + lane * 4 (64 KiB). Every lane reads its own copy, each copy lives in one
  * bank, and the byte address of code byte k of a word E is one v_perm_b32 that drops

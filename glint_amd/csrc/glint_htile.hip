@@ -12,10 +12,12 @@
  *   read, 1 f32 FMA; per row one FMA by the block absmax and 4 DPP adds.
  * k_htile_gemv_b64 — decode for the other K % 64 == 0: x staged in LDS as f32 planes,
  *   (task, step) items double-buffered in registers.
- * k_tile_mfma<..., GlintTileProducer> (tile_mfma.h) — prefill (M > 1, bf16 out, bs = 64): BF16
- *   MFMA on double-buffered LDS-dequantized weight tiles, f32 accumulation; 256 x 128 tiles
- *   over 8 waves for M >= 256, 128 x 64 / 64 x 64 over 4 waves below. The tile kernel is
- *   shared with the INT8-pin W8A16 GEMM.
+ * Prefill (M > 1, bf16 out, bs = 64; tile_mfma.h): BF16 MFMA on double-buffered
+ *   LDS-dequantized weight tiles, f32 accumulation, K split across workgroups when the
+ *   tiles alone would leave CUs idle (fixed-order reduction). k_tile_mfma: 256 x 128 tiles
+ *   over 8 waves for M >= 256; k_tile_ss: 64 x 64 / 128 x 64 over 4 waves below, with the
+ *   weights loaded a whole 128-B line per 8 lanes. Both are shared with the INT8-pin
+ *   W8A16 GEMM.
  * k_htile_generic — every other shape (any M, K, bs, alignment): 64x32 output tiles,
  *   weights decoded to f32 in LDS per 32-wide K step, f32 FMAs in k order.
  */
@@ -476,11 +478,11 @@ __global__ __launch_bounds__(256) void k_htile_generic(const uint8_t *__restrict
 /* Prefill GEMM, large M: the shared double-buffered tile kernel with 256 (M) x 128 (N)
  * blocks over 8 waves in 4 x 2 (wave tile 64 x 64); each thread dequantizes 16 weights
  * (8 B of each plane) per K step through the 32-copy cell table. */
-#ifndef TILE_R_SMALL
-#define TILE_R_SMALL 4 /* register stages (K steps of loads in flight) of the 64- and 128-row tiles */
+#ifndef TILE_RX
+#define TILE_RX 4 /* x register stages of k_tile_ss (M < 256) */
 #endif
 #ifndef TILE_R_BIG
-#define TILE_R_BIG 2 /* the same for the 256 x 128 tiles */
+#define TILE_R_BIG 2 /* register stages (K steps of loads in flight) of the 256 x 128 tiles */
 #endif
 #define MF2_BM 256
 #define MF2_BN 128
@@ -516,9 +518,9 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         const uint16_t *xb = (const uint16_t *)x;
         uint16_t *yb = (uint16_t *)y;
         if (M <= 64)
-            tile_mfma_launch<64, 64, 2, 2, TILE_R_SMALL, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
+            tile_ss_launch<64, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
         else if (M < MF2_MIN_M)
-            tile_mfma_launch<128, 64, 2, 2, TILE_R_SMALL, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
+            tile_ss_launch<128, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
         else
             tile_mfma_launch<MF2_BM, MF2_BN, 4, 2, TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
     } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS / 64) {

@@ -2,10 +2,13 @@
  *
  * y[m, n] = sum_k x[m, k] * bf16(q[n, k] * scale[(n * k_in + k) / 64]), f32 out.
  *
- * k_tile_mfma<..., Int8PinTileProducer, TileOutF32> (tile_mfma.h) — k_in % 64 == 0 with
- *   16-B aligned x and q: each thread turns 16 int8 weights of one row (one 16-B load) into
- *   BF16 RNE((float)q * scale) in LDS, and v_mfma_f32_16x16x32_bf16 accumulates in f32.
- *   Tiles: 256 x 128 over 8 waves for m >= 256, 128 x 64 for m > 64, 64 x 64 below.
+ * k_tile_mfma / k_tile_ss<..., Int8PinTileProducer, TileOutF32> (tile_mfma.h) — k_in % 64
+ *   == 0 with 16-B aligned x and q, m > 4: threads turn 16 int8 weights of one row into
+ *   BF16 RNE((float)q * scale) in LDS, and v_mfma_f32_16x16x32_bf16 accumulates in f32;
+ *   K is split across workgroups (fixed-order reduction) when the tiles leave CUs idle.
+ *   Tiles: 256 x 128 over 8 waves for m >= 256 (k_tile_mfma), 128 x 64 for m > 64 and
+ *   64 x 64 below (k_tile_ss: weight loads cover whole 128-B lines).
+ * k_i8tile_gemv<MR> — m <= 4, k_in % 2048 == 0: the GEMV-shaped kernel, f32 FMAs.
  * k_i8tile_generic — any k_in and alignment: 64 (n) x 32 (m) output tiles, weights
  *   dequantized to BF16 and widened to f32 in LDS per 32-wide K step, f32 FMAs in k order.
  *   A row's scale index is the flat (n * k_in + k) / 64, so a K step may span two blocks.
@@ -218,6 +221,16 @@ static void i8tile_launch_fast(const uint16_t *x, const Int8PinLinear &w, float 
     }
 }
 
+template <int BM>
+static void i8tile_launch_ss(const uint16_t *x, const Int8PinLinear &w, float *y, int m, hipStream_t st) {
+    const Int8PinTileProducer p{(const glint_u32x4 *)w.q, w.scale, w.n_out, w.k_in};
+    for (int64_t r0 = 0; r0 < m; r0 += (int64_t)I8_MAX_YBLOCKS * BM) {
+        const int mm = (int)std::min<int64_t>((int64_t)I8_MAX_YBLOCKS * BM, m - r0);
+        tile_ss_launch<BM, 4, Int8PinTileProducer, TileOutF32>(p, x + r0 * w.k_in, y + r0 * w.n_out, mm, w.n_out,
+                                                               w.k_in, st);
+    }
+}
+
 GLINT_API int int8_tile_gemm_bf16(const void *x_bf16, Int8PinLinear w, float *y, int m, hipStream_t stream) {
     const hipError_t pending = hipGetLastError();
     if (pending != hipSuccess)
@@ -242,9 +255,9 @@ GLINT_API int int8_tile_gemm_bf16(const void *x_bf16, Int8PinLinear w, float *y,
         if (m >= 256)
             i8tile_launch_fast<256, 128, 4, 2, 2>(x, w, y, m, stream);
         else if (m > 64)
-            i8tile_launch_fast<128, 64, 2, 2, 4>(x, w, y, m, stream);
+            i8tile_launch_ss<128>(x, w, y, m, stream);
         else
-            i8tile_launch_fast<64, 64, 2, 2, 4>(x, w, y, m, stream);
+            i8tile_launch_ss<64>(x, w, y, m, stream);
     } else {
         const unsigned gx = (unsigned)((w.n_out + I8G_N - 1) / I8G_N);
         for (int64_t r0 = 0; r0 < m; r0 += (int64_t)I8_MAX_YBLOCKS * I8G_M) {

@@ -10,7 +10,9 @@
  *                                                 their latency overlaps the step's MFMAs)
  *   finish(const Regs &, const float (&v)[16], uint32_t (&)[8])
  *                                                 the 16 weights as BF16 pairs (lo = even k)
- *   LDS_WORDS, setup(float *lds)                  LDS the producer needs (filled before step 0)
+ *   LDS_WORDS, setup(float *lds, float *stage)    LDS the producer needs, filled before step 0
+ *                                                 (stage: 256 words of scratch LDS, free again
+ *                                                 after setup returns)
  *
  * Block tile BM x BN x 64 (K) over WM x WN waves; each wave owns a (BM / WM) x (BN / WN)
  * tile of v_mfma_f32_16x16x32_bf16 accumulators (f32). Thread t produces W row t / 4,
@@ -70,20 +72,22 @@ struct TileOutF32 {
     static __device__ __forceinline__ void store(T *y, int64_t i, float v) { y[i] = v; }
 };
 
-/* GLINT planes, bs = 64: weight = CELLS[h][p] * absmax, through the 32-copy LDS table. */
+/* GLINT planes, bs = 64: weight = CELLS[h][p] * absmax, through the 32-copy LDS cell
+ * table (lane l reads copy l % 32). A 64-copy table, whose lookup address is one
+ * v_perm_b32, measured 3% slower here: its fill doubles and the LDS budget tightens. */
 struct GlintTileProducer {
     const glint_u32x2 *hole, *plug; /* 8 B = 16 elements of each plane */
     const float *absmax;
     int N, K;
     float *ltab;
-    static constexpr int LDS_WORDS = GLINT_LDS_CELLS_WORDS + 256;
+    static constexpr int LDS_WORDS = GLINT_LDS_CELLS_WORDS;
     struct Regs {
         glint_u32x2 h, p;
         float a;
     };
-    __device__ __forceinline__ void setup(float *lds) {
+    __device__ __forceinline__ void setup(float *lds, float *) {
         ltab = lds;
-        glint_fill_cells_lds(lds, lds + GLINT_LDS_CELLS_WORDS);
+        glint_fill_cells_lds_direct(lds);
     }
     __device__ __forceinline__ void load(Regs &r, int row, int quarter, int kb) const {
         const int64_t q = (int64_t)row * (K >> 4) + kb * 4 + quarter;
@@ -93,12 +97,12 @@ struct GlintTileProducer {
     }
     /* v[8 q + 2 b] / v[8 q + 2 b + 1]: cells of the even / odd element of byte b of word q */
     __device__ __forceinline__ void lookup(const Regs &r, float (&v)[16], int lane) const {
-        const uint32_t lb = lane & 31;
         const uint32_t H[2] = {r.h.x, r.h.y}, P[2] = {r.p.x, r.p.y};
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const uint32_t E = glint_codes_even(H[q], P[q]);
             const uint32_t O = glint_codes_odd(H[q], P[q]);
+            const uint32_t lb = lane & 31;
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
                 v[8 * q + 2 * b] = ltab[(((E >> (8 * b)) & 0xFFu) << 5) | lb];
@@ -107,6 +111,35 @@ struct GlintTileProducer {
         }
     }
     __device__ __forceinline__ void finish(const Regs &r, const float (&v)[16], uint32_t (&packed)[8]) const {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            packed[i] = glint_cvt_bf16x2(v[2 * i] * r.a, v[2 * i + 1] * r.a);
+    }
+
+    /* Super-step interface (k_tile_ss): piece c (0..7) of a row's super-step (4 K steps, 256
+     * elements) is elements [32 c, +32): 16 B of each plane and one absmax. Its groups h = 0, 1
+     * (16 elements each) lie in K step c / 2, quarters 2 (c & 1) + h. `step` is the piece's
+     * K step, already clamped into the matrix by the caller. */
+    struct SRegs {
+        glint_u32x4 h, p;
+        float a;
+    };
+    static __device__ __forceinline__ int sstep(int c, int) { return c >> 1; }
+    static __device__ __forceinline__ int squarter(int c, int h) { return ((c & 1) << 1) | h; }
+    __device__ __forceinline__ void sload(SRegs &r, int row, int step0, int c, int last) const {
+        const int kb = min(step0 + (c >> 1), last);
+        const int64_t i = (int64_t)row * (K >> 5) + kb * 2 + (c & 1);
+        r.h = __builtin_nontemporal_load((const glint_u32x4 *)hole + i);
+        r.p = __builtin_nontemporal_load((const glint_u32x4 *)plug + i);
+        r.a = absmax[(int64_t)row * (K >> 6) + kb];
+    }
+    __device__ __forceinline__ void slookup(const SRegs &r, int h, float (&v)[16], int lane) const {
+        Regs g;
+        g.h = h ? glint_u32x2{r.h.z, r.h.w} : glint_u32x2{r.h.x, r.h.y};
+        g.p = h ? glint_u32x2{r.p.z, r.p.w} : glint_u32x2{r.p.x, r.p.y};
+        lookup(g, v, lane);
+    }
+    __device__ __forceinline__ void sfinish(const SRegs &r, int, const float (&v)[16], uint32_t (&packed)[8]) const {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             packed[i] = glint_cvt_bf16x2(v[2 * i] * r.a, v[2 * i + 1] * r.a);
@@ -124,7 +157,7 @@ struct Int8PinTileProducer {
         glint_u32x4 w;
         float s;
     };
-    __device__ __forceinline__ void setup(float *) {}
+    __device__ __forceinline__ void setup(float *, float *) {}
     __device__ __forceinline__ void load(Regs &r, int row, int quarter, int kb) const {
         r.w = __builtin_nontemporal_load(&q[(int64_t)row * (K >> 4) + kb * 4 + quarter]);
         r.s = scale[(int64_t)row * (K >> 6) + kb];
@@ -140,7 +173,97 @@ struct Int8PinTileProducer {
         for (int i = 0; i < 8; ++i)
             packed[i] = glint_cvt_bf16x2(v[2 * i] * r.s, v[2 * i + 1] * r.s);
     }
+
+    /* Super-step interface (k_tile_ss): piece c (0..7) of a row's 256-byte super-step is the
+     * 16 bytes at 16 c and at 128 + 16 c (each load instruction then covers whole 128-B
+     * lines); group h lies in K step c / 4 + 2 h, quarter c & 3. */
+    struct SRegs {
+        glint_u32x4 w[2];
+        float s[2];
+    };
+    static __device__ __forceinline__ int sstep(int c, int h) { return (c >> 2) + 2 * h; }
+    static __device__ __forceinline__ int squarter(int c, int) { return c & 3; }
+    __device__ __forceinline__ void sload(SRegs &r, int row, int step0, int c, int last) const {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int kb = min(step0 + sstep(c, h), last);
+            r.w[h] = __builtin_nontemporal_load(&q[(int64_t)row * (K >> 4) + kb * 4 + (c & 3)]);
+            r.s[h] = scale[(int64_t)row * (K >> 6) + kb];
+        }
+    }
+    __device__ __forceinline__ void slookup(const SRegs &r, int h, float (&v)[16], int) const {
+        const uint32_t W[4] = {r.w[h].x, r.w[h].y, r.w[h].z, r.w[h].w};
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            v[i] = (float)(int8_t)(W[i >> 2] >> (8 * (i & 3)));
+    }
+    __device__ __forceinline__ void sfinish(const SRegs &r, int h, const float (&v)[16], uint32_t (&packed)[8]) const {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            packed[i] = glint_cvt_bf16x2(v[2 * i] * r.s[h], v[2 * i + 1] * r.s[h]);
+    }
 };
+
+/* Split-K epilogue (gridDim.z > 1). Partials and counters are accessed with device-scope
+ * relaxed atomics, which are coherent across the XCDs' separate L2 caches without the L2
+ * write-back and invalidate that device-scope fences cost. Ordering: a workgroup's partial
+ * stores have completed (vmcnt 0) before the barrier that precedes its counter increment,
+ * and the reducer issues its partial loads after it has seen the final count. Partial
+ * element e of thread t sits at e T + t. Returns true in the last workgroup of the tile,
+ * whose acc then holds the z-ordered sum; the others return false and store nothing.
+ * s_last: one word of LDS that nothing else uses any more. */
+template <int NA, int NB, int T>
+__device__ __forceinline__ bool tile_splitk_epilogue(glint_f32x4 (&acc)[NA][NB], float *__restrict__ part,
+                                                     unsigned *ctr, unsigned &s_last) {
+    constexpr int NV = NA * NB * 4;
+    const int tid = threadIdx.x;
+    const unsigned tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const size_t tsz = (size_t)NV * T, zstride = (size_t)gridDim.x * gridDim.y * tsz;
+    float *mine = part + blockIdx.z * zstride + tile * tsz;
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                __hip_atomic_store(mine + ((a * NB + b) * 4 + i) * T + tid, acc[a][b][i], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0);
+    __syncthreads();
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&ctr[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.z - 1;
+    __syncthreads();
+    if (!s_last)
+        return false;
+    /* The partials are read in rounds of CH accumulators, all TILE_SPLIT_MAX splits of a
+     * round in flight at once (z clamped; a split past gridDim.z is loaded and ignored). */
+    constexpr int CH = NV < 16 ? NV : 16;
+    const unsigned zl = gridDim.z - 1;
+    const float *base = part + tile * tsz;
+#pragma unroll
+    for (int c0 = 0; c0 < NV; c0 += CH) {
+        float v[TILE_SPLIT_MAX][CH];
+#pragma unroll
+        for (int z = 0; z < TILE_SPLIT_MAX; ++z)
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+                v[z][c] = __hip_atomic_load(base + min((unsigned)z, zl) * zstride + (size_t)(c0 + c) * T + tid,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int e = c0 + c, a = e / (NB * 4), b = (e / 4) % NB, i = e % 4;
+            float sum = blockIdx.z == 0 ? acc[a][b][i] : v[0][c];
+#pragma unroll
+            for (int z = 1; z < TILE_SPLIT_MAX; ++z)
+                if ((unsigned)z <= zl)
+                    sum += (unsigned)z == blockIdx.z ? acc[a][b][i] : v[z][c];
+            acc[a][b][i] = sum;
+        }
+    }
+    if (tid == 0)
+        __hip_atomic_store(&ctr[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
 
 template <int BM, int BN, int WM, int WN, int R, class P, class Out>
 __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t *__restrict__ x,
@@ -157,7 +280,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
     __shared__ float ptab[P::LDS_WORDS > 0 ? P::LDS_WORDS : 1];
     __shared__ __attribute__((aligned(16))) uint16_t sX[2][BM * TILE_LDW];
     __shared__ __attribute__((aligned(16))) uint16_t sW[2][BN * TILE_LDW];
-    __shared__ unsigned s_last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -237,7 +359,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
         __syncthreads();
     };
 
-    p.setup(ptab);
+    p.setup(ptab, (float *)&sX[0][0]); /* sX is free until the first x store */
 #pragma unroll
     for (int i = 0; i < R; ++i)
         gload(i, st[i]);
@@ -259,60 +381,165 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
         if (j + u < ns)
             step(j + u, u);
 
-    if (gridDim.z > 1) {
-        /* Partials and counters are accessed with device-scope relaxed atomics, which are
-         * coherent across the XCDs' separate L2 caches without the L2 write-back and
-         * invalidate that device-scope fences cost. Ordering: a workgroup's partial stores
-         * have completed (vmcnt 0) before the barrier that precedes its counter increment,
-         * and the reducer issues its partial loads after it has seen the final count.
-         * Partial element e of thread t sits at e T + t. */
-        const unsigned tile = blockIdx.y * gridDim.x + blockIdx.x;
-        const size_t tsz = (size_t)BM * BN, zstride = (size_t)gridDim.x * gridDim.y * tsz;
-        float *mine = part + blockIdx.z * zstride + tile * tsz;
+    if (gridDim.z > 1 && !tile_splitk_epilogue<TM, TN, T>(acc, part, ctr, *(unsigned *)&sX[0][0]))
+        return;
 #pragma unroll
-        for (int a = 0; a < TM; ++a)
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm * TM * 16 + a * 16 + (lane >> 4) * 4 + i;
+                const int n = n0 + wn * TN * 16 + b * 16 + (lane & 15);
+                if (m < M && n < N)
+                    Out::store(y, (int64_t)m * N + n, acc[a][b][i]);
+            }
+}
+
+/* Tile GEMM for BN = 64 W rows (M up to a few hundred) with the weights streamed in
+ * super-steps of 4 K steps (256 elements): per super-step a thread loads 16-B pieces of two
+ * W rows such that 8 consecutive lanes cover a whole 128-B line of a plane (P::sload). Loads
+ * that cover whole lines stream at about twice the rate of the per-step 8-byte pieces
+ * k_tile_mfma uses, which bounded it at small M. The 4 groups of 16 weights a thread holds
+ * are dequantized one per K step into a double-buffered 4-step W tile in LDS (super-step
+ * s + 1 while s is multiplied); x keeps the per-step ring (RX stages) and double buffer
+ * of k_tile_mfma. Block tile BM x 64 over 2 x 2 waves (BM = 64 or 128); W rows 8 w +
+ * lane / 8 and 32 more (wave w), piece lane % 8. Clamping and split K as in k_tile_mfma. */
+template <int BM, int RX, class P, class Out>
+__global__ __launch_bounds__(256) void k_tile_ss(P p, const uint16_t *__restrict__ x, typename Out::T *__restrict__ y,
+                                                 int M, int N, int K, int kps, float *__restrict__ part,
+                                                 unsigned *ctr) {
+    constexpr int T = 256, BN = 64, WN = 2, TM = BM / 32, TN = 2, XV = BM * 8 / T;
+    constexpr int U = 8; /* steps per unrolled round: two super-steps, RX | 8 */
+    static_assert((BM == 64 || BM == 128) && (RX == 2 || RX == 4 || RX == 8), "tile shape, x stages");
+    __shared__ float ptab[P::LDS_WORDS > 0 ? P::LDS_WORDS : 1];
+    __shared__ __attribute__((aligned(16))) uint16_t sX[2][BM * TILE_LDW];
+    __shared__ __attribute__((aligned(16))) uint16_t sW[2][4][BN * TILE_LDW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kb0 = blockIdx.z * kps;
+    const int ns = min(K >> 6, kb0 + kps) - kb0; /* >= 1: the host sizes gridDim.z */
+    const int last = kb0 + ns - 1;               /* W loads past the split clamp here */
+    const int c = lane & 7;
+    int lrow[2], wrow[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+        lrow[rr] = wave * 8 + (lane >> 3) + 32 * rr;
+        wrow[rr] = min(n0 + lrow[rr], N - 1);
+    }
+    const int xr = tid >> 3, xc = tid & 7; /* x chunk i: row xr + 32 i, columns 8 xc */
+    glint_f32x4 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+            acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
+
+    typename P::SRegs sw[2][2]; /* [super-stage][row set] */
+    glint_u32x4 xs[RX][XV];
+    auto gload_w = [&](int ss, typename P::SRegs (&sg)[2]) {
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+            p.sload(sg[rr], wrow[rr], kb0 + 4 * ss, c, last);
+    };
+    auto gload_x = [&](int j, glint_u32x4 (&xg)[XV]) {
+        const int kb = kb0 + min(j, ns - 1);
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int m = min(m0 + xr + 32 * i, M - 1);
+            xg[i] = *(const glint_u32x4 *)(x + (int64_t)m * K + (int64_t)kb * 64 + xc * 8);
+        }
+    };
+    auto store_x = [&](int buf, const glint_u32x4 (&xg)[XV]) {
+#pragma unroll
+        for (int i = 0; i < XV; ++i)
+            *(glint_u32x4 *)(sX[buf] + tile_ofs(xr + 32 * i, xc)) = xg[i];
+    };
+    /* group t of a super-stage: row set t / 2, half t % 2. The 16-B chunks of W step slot s
+     * are additionally XORed with s: the 8 lanes of a store instruction (one row, 4 slots)
+     * then hit 8 distinct bank groups, and a fragment read (one slot) is unchanged. */
+    auto finish_w = [&](int buf, const typename P::SRegs (&sg)[2], int t, const float (&v)[16]) {
+        uint32_t pk[8];
+        p.sfinish(sg[t >> 1], t & 1, v, pk);
+        const int slot = P::sstep(c, t & 1), qq = P::squarter(c, t & 1);
+        uint16_t *w = sW[buf][slot];
+        *(glint_u32x4 *)(w + tile_ofs(lrow[t >> 1], (2 * qq) ^ slot)) = glint_u32x4{pk[0], pk[1], pk[2], pk[3]};
+        *(glint_u32x4 *)(w + tile_ofs(lrow[t >> 1], (2 * qq + 1) ^ slot)) = glint_u32x4{pk[4], pk[5], pk[6], pk[7]};
+    };
+    /* local step j, u = j % 8: super-step j / 4 (LDS tile (u / 4) & 1, slot t = u % 4). First
+     * the LDS stores for later steps go out (group t of super-step j / 4 + 1, looked up in
+     * the previous step, and x of step j + 1), so their latency hides behind this step's
+     * reads and MFMAs; then the fragments, the table reads of the next group, the MFMAs.
+     * After group 3 the super-stage is refilled two super-steps ahead. */
+    float v[16]; /* table reads of the next group to store */
+    auto step = [&](int j, int u) {
+        const int t = u & 3, sb = (u >> 2) & 1;
+        typename P::SRegs(&nw)[2] = sw[sb ^ 1];
+        finish_w(sb ^ 1, nw, t, v); /* past the end: clamped data nobody reads */
+        store_x((u & 1) ^ 1, xs[(u + 1) % RX]);
+        glint_bf16x8 af[2][TM], bfr[2][TN];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int fofs = tile_ofs(lane & 15, 4 * ks + (lane >> 4));
+            const int wofs = tile_ofs(lane & 15, (4 * ks + (lane >> 4)) ^ t);
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+                af[ks][a] = __builtin_bit_cast(
+                    glint_bf16x8, *(const glint_u32x4 *)(sX[u & 1] + (wm * TM * 16 + a * 16) * TILE_LDW + fofs));
 #pragma unroll
             for (int b = 0; b < TN; ++b)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    __hip_atomic_store(mine + ((a * TN + b) * 4 + i) * T + tid, acc[a][b][i], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0);
-        __syncthreads();
-        if (tid == 0)
-            s_last = __hip_atomic_fetch_add(&ctr[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                     gridDim.z - 1;
-        __syncthreads();
-        if (!s_last)
-            return;
-        /* The partials are read in rounds of CH accumulators, all TILE_SPLIT_MAX splits of a
-         * round in flight at once (z clamped; a split past gridDim.z is loaded and ignored). */
-        constexpr int CH = NV < 16 ? NV : 16;
-        const unsigned zl = gridDim.z - 1;
-        const float *base = part + tile * tsz;
-#pragma unroll
-        for (int c0 = 0; c0 < NV; c0 += CH) {
-            float v[TILE_SPLIT_MAX][CH];
-#pragma unroll
-            for (int z = 0; z < TILE_SPLIT_MAX; ++z)
-#pragma unroll
-                for (int c = 0; c < CH; ++c)
-                    v[z][c] = __hip_atomic_load(base + min((unsigned)z, zl) * zstride + (size_t)(c0 + c) * T + tid,
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const int e = c0 + c, a = e / (TN * 4), b = (e / 4) % TN, i = e % 4;
-                float s = blockIdx.z == 0 ? acc[a][b][i] : v[0][c];
-#pragma unroll
-                for (int z = 1; z < TILE_SPLIT_MAX; ++z)
-                    if ((unsigned)z <= zl)
-                        s += (unsigned)z == blockIdx.z ? acc[a][b][i] : v[z][c];
-                acc[a][b][i] = s;
-            }
+                bfr[ks][b] = __builtin_bit_cast(
+                    glint_bf16x8, *(const glint_u32x4 *)(sW[sb][t] + (wn * TN * 16 + b * 16) * TILE_LDW + wofs));
         }
-        if (tid == 0)
-            __hip_atomic_store(&ctr[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t < 3)
+            p.slookup(nw[(t + 1) >> 1], (t + 1) & 1, v, lane);
+        else
+            p.slookup(sw[sb][0], 0, v, lane); /* group 0 of super-step j / 4 + 2 */
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+                for (int b = 0; b < TN; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][a], bfr[ks][b], acc[a][b], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t == 3)
+            gload_w((j >> 2) + 3, nw);
+        gload_x(j + 1 + RX, xs[(u + 1) % RX]);
+        __syncthreads();
+    };
+
+    p.setup(ptab, (float *)&sX[0][0]); /* sX is free until the first x store */
+    gload_w(0, sw[0]);
+    gload_w(1, sw[1]);
+#pragma unroll
+    for (int i = 0; i < RX; ++i)
+        gload_x(i, xs[i]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        p.slookup(sw[0][t >> 1], t & 1, v, lane);
+        finish_w(0, sw[0], t, v);
     }
+    p.slookup(sw[1][0], 0, v, lane);
+    gload_w(2, sw[0]);
+    store_x(0, xs[0]);
+    gload_x(RX, xs[0]);
+    __syncthreads();
+    int j = 0;
+    for (; j + U <= ns; j += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            step(j + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < U; ++u)
+        if (j + u < ns)
+            step(j + u, u);
+
+    if (gridDim.z > 1 && !tile_splitk_epilogue<TM, TN, T>(acc, part, ctr, *(unsigned *)&sX[0][0]))
+        return;
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
@@ -390,25 +617,40 @@ static inline int glint_split_kps(int64_t tiles, int64_t slots, int nK, int min_
     return (int)((nK + ks - 1) / ks);
 }
 
-/* Launch k_tile_mfma over an M x N output, splitting K when the tiles alone would leave
- * resident slots idle. K % 64 == 0, M, N >= 1. */
-template <int BM, int BN, int WM, int WN, int R, class P, class Out>
-static void tile_mfma_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st) {
-    constexpr int T = 64 * WM * WN;
-    auto kern = k_tile_mfma<BM, BN, WM, WN, R, P, Out>;
-    const int nS = K >> 6; /* 64-wide K steps */
-    const unsigned gx = (unsigned)((N + BN - 1) / BN), gy = (unsigned)((M + BM - 1) / BM);
+/* Split plan for a gx x gy tile grid over nS K steps: fills the CUs once (a second resident
+ * workgroup per CU measured slower: they contend for the LDS). Sets kps and ks and binds the
+ * stream's workspace; without one (capture) it runs unsplit. */
+static inline void tile_split_plan(hipStream_t st, unsigned gx, unsigned gy, int nS, size_t tile_floats, int &kps,
+                                   int &ks, GlintSplitWs &ws) {
     const int64_t tiles = (int64_t)gx * gy;
-    /* one workgroup per CU: a second resident workgroup measured slower (they contend for
-     * the LDS), so the split count aims at filling the CUs once */
-    int kps = glint_split_kps(tiles, glint_cu_count(), nS, TILE_SPLIT_MIN_STEPS);
-    int ks = (nS + kps - 1) / kps;
-    GlintSplitWs ws{nullptr, nullptr};
-    if (ks > 1 && !glint_split_ws(st, (size_t)ks * tiles * BM * BN, (size_t)tiles, ws)) {
+    kps = glint_split_kps(tiles, glint_cu_count(), nS, TILE_SPLIT_MIN_STEPS);
+    ks = (nS + kps - 1) / kps;
+    ws = GlintSplitWs{nullptr, nullptr};
+    if (ks > 1 && !glint_split_ws(st, (size_t)ks * tiles * tile_floats, (size_t)tiles, ws)) {
         kps = nS;
         ks = 1;
     }
-    kern<<<dim3(gx, gy, (unsigned)ks), T, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
+}
+
+/* Launch k_tile_mfma over an M x N output. K % 64 == 0, M, N >= 1. */
+template <int BM, int BN, int WM, int WN, int R, class P, class Out>
+static void tile_mfma_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st) {
+    const unsigned gx = (unsigned)((N + BN - 1) / BN), gy = (unsigned)((M + BM - 1) / BM);
+    int kps, ks;
+    GlintSplitWs ws;
+    tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * BN, kps, ks, ws);
+    k_tile_mfma<BM, BN, WM, WN, R, P, Out><<<dim3(gx, gy, (unsigned)ks), 64 * WM * WN, 0, st>>>(p, x, y, M, N, K, kps,
+                                                                                              ws.part, ws.ctr);
+}
+
+/* Launch k_tile_ss over an M x N output. K % 64 == 0, M, N >= 1. */
+template <int BM, int RX, class P, class Out>
+static void tile_ss_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st) {
+    const unsigned gx = (unsigned)((N + 63) / 64), gy = (unsigned)((M + BM - 1) / BM);
+    int kps, ks;
+    GlintSplitWs ws;
+    tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * 64, kps, ks, ws);
+    k_tile_ss<BM, RX, P, Out><<<dim3(gx, gy, (unsigned)ks), 256, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
 }
 
 #endif
