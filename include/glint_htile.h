@@ -27,8 +27,11 @@ int launch_glint_htile_s3_f32(const uint8_t *d_hole, const uint8_t *d_plug, cons
 /* ---- Additive (no reference counterpart). ----
  * BF16 output with f32 accumulation: the decode GEMV (small M, HBM-bound) and the
  * prefill GEMM (larger M: BF16 MFMA on LDS-dequantized weight tiles). Contract: within
- * 1e-2 relative Frobenius error of an f32 GEMM on the expanded weights.
- * Same return codes. */
+ * 1e-2 relative Frobenius error of an f32 GEMM on the expanded weights; results are
+ * deterministic (split K adds its partial tiles in a fixed order).
+ * At M > 1 the first call on a stream at a given size may allocate the stream's split-K
+ * workspace (hipMalloc, at most 32 MiB, kept until exit); during graph capture it is not
+ * grown and the GEMM runs unsplit. Same return codes. */
 int launch_glint_htile_bf16_stream(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax,
                                    const void *d_x_bf16, uint16_t *d_y_bf16,
                                    int M, int N, int K, int blocksize, struct ihipStream_t *stream);
