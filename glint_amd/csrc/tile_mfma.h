@@ -59,6 +59,9 @@ __device__ __forceinline__ uint32_t glint_cvt_bf16x2(float lo, float hi) {
 /* s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt [3:0] and [15:14] = 0,
  * expcnt [6:4] and lgkmcnt [11:8] at their maxima). On gfx9 stores count in vmcnt too. */
 #define GLINT_WAIT_VMCNT0 0x0F70
+#ifndef TILE_INTERLEAVE
+#define TILE_INTERLEAVE 1 /* k_tile_mfma: second K slice's fragment reads between the first's MFMAs */
+#endif
 __device__ __forceinline__ int tile_ofs(int r, int c) {
     return r * TILE_LDW + ((c ^ (((r >> 1) ^ ((r & 1) << 2)) & 7)) << 3);
 }
@@ -329,10 +332,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
         const int cur = u & 1;
         Stage &nx = st[(u + 1) % R];
         glint_bf16x8 af[2][TM], bfr[2][TN];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            /* rows (16-row tile base) + lane % 16, chunk 4 ks + lane / 16; the swizzle does not
-             * change when a row moves by a multiple of 16 */
+        /* rows (16-row tile base) + lane % 16, chunk 4 ks + lane / 16; the swizzle does not
+         * change when a row moves by a multiple of 16 */
+        auto frags = [&](int ks) {
             const int fofs = tile_ofs(lane & 15, 4 * ks + (lane >> 4));
 #pragma unroll
             for (int a = 0; a < TM; ++a)
@@ -342,17 +344,37 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
             for (int b = 0; b < TN; ++b)
                 bfr[ks][b] = __builtin_bit_cast(
                     glint_bf16x8, *(const glint_u32x4 *)(sW[cur] + (wn * TN * 16 + b * 16) * TILE_LDW + fofs));
-        }
-        float v[16];
-        p.lookup(nx.w, v, lane);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        };
+        auto mfmas = [&](int ks) {
 #pragma unroll
             for (int a = 0; a < TM; ++a)
 #pragma unroll
                 for (int b = 0; b < TN; ++b)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][a], bfr[ks][b], acc[a][b], 0, 0, 0);
+        };
+        float v[16];
+        if (TILE_INTERLEAVE) {
+            /* the second K slice's fragment reads go out between the first slice's MFMAs */
+            frags(0);
+            p.lookup(nx.w, v, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(0);
+            frags(1);
+#pragma unroll
+            for (int i = 0; i < TM + TN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, (TM * TN) / (TM + TN), 0); /* MFMA */
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                     /* LDS read */
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(1);
+        } else {
+            frags(0);
+            frags(1);
+            p.lookup(nx.w, v, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(0);
+            mfmas(1);
+        }
         __builtin_amdgcn_sched_barrier(0);
         store(cur ^ 1, nx, v); /* past the end: a clamped copy nobody reads */
         gload(j + 1 + R, nx);
