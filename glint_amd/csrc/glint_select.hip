@@ -88,7 +88,7 @@ __global__ __launch_bounds__(KM_T) void k_kmajor_scales(const float *__restrict_
 #define KM_SUB 8                /* waves per workgroup = parts of a channel slice */
 #define KM_ROWS 2048            /* output rows per workgroup: 64 lanes x 32 rows */
 #define KM_WG (64 * KM_SUB)
-#define KM_U 8                  /* channels of loads in flight per wave (one 16-B load of x) */
+#define KM_U 4                  /* channels per batch (two batches in flight per wave) */
 
 __device__ __forceinline__ float km_bf16(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
@@ -165,43 +165,60 @@ __global__ __launch_bounds__(KM_WG) void k_gemv_km_fold(const glint_u32x4 *__res
     const int64_t rowv = N / 32;                /* 16-B vectors per K-major row */
     const int sub = ksl / KM_SUB;
     const int c0 = blockIdx.y * ksl + q * sub, c1 = c0 + sub;
-    float tot[32], acc[32];
+    float tot[32], acc[32], sc[32];
 #pragma unroll
     for (int j = 0; j < 32; ++j)
         tot[j] = 0.f;
-    for (int b = c0 >> 6; b <= (c1 - 1) >> 6; ++b) {
-        const int cs = max(c0, 64 * b), ce = min(c1, 64 * b + 64); /* multiples of 8 */
-        float sc[32]; /* issued before the run's loads, used after them */
-        km_load32(scales_k + (int64_t)b * N + rc, sc);
+    /* Batches of KM_U channels (a batch never crosses a 64-block: parts are multiples of
+     * KM_U and blocks multiples of 64), the next batch's loads in flight while this one is
+     * looked up. A run is the batches of one block: acc restarts at its first batch and is
+     * folded into tot by the block scale after its last, in channel order. */
+    auto load_batch = [&](int c, glint_u32x4 (&wv)[KM_U]) {
+        c = min(c, c1 - KM_U); /* past the part: a clamped reload nobody uses */
 #pragma unroll
-        for (int j = 0; j < 32; ++j)
-            acc[j] = 0.f;
-        for (int c = cs; c < ce; c += KM_U) {
-            glint_u32x4 wv[KM_U];
+        for (int u = 0; u < KM_U; ++u)
+            wv[u] = __builtin_nontemporal_load(&hole_k[(int64_t)(c + u) * rowv + rc / 32]);
+    };
+    glint_u32x4 wa[KM_U], wb[KM_U];
+    auto batch = [&](int c, const glint_u32x4 (&wv)[KM_U]) {
+        if (c == c0 || (c & 63) == 0) { /* a run starts: its block scales, acc from zero */
+            km_load32(scales_k + (int64_t)(c >> 6) * N + rc, sc);
 #pragma unroll
-            for (int u = 0; u < KM_U; ++u)
-                wv[u] = __builtin_nontemporal_load(&hole_k[(int64_t)(c + u) * rowv + rc / 32]);
-            /* the batch's 8 x values in one wave-uniform 16-B load, waited for once before the
-             * lookups (a scalar load per channel would make every lookup wait for it) */
-            const glint_u32x4 xw = *(const glint_u32x4 *)(x + c);
-            const uint32_t xs[4] = {xw.x, xw.y, xw.z, xw.w};
-#pragma unroll
-            for (int u = 0; u < KM_U; ++u) {
-                const float xv = (u & 1) ? glint_bf16hi(xs[u >> 1]) : glint_bf16lo(xs[u >> 1]);
-                const uint32_t W[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-                uint32_t E[4], O[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    E[q] = W[q] & 0x0F0F0F0Fu;
-                    O[q] = (W[q] >> 4) & 0x0F0F0F0Fu;
-                }
-                km_lookup_fma(lds, E, O, lane4, xv, acc);
-            }
+            for (int j = 0; j < 32; ++j)
+                acc[j] = 0.f;
         }
+        /* the batch's 4 x values in one wave-uniform 8-B load, waited for once before the
+         * lookups (a scalar load per channel would make every lookup wait for it) */
+        const glint_u32x2 xw = *(const glint_u32x2 *)(x + c);
+        const uint32_t xs[2] = {xw.x, xw.y};
 #pragma unroll
-        for (int j = 0; j < 32; ++j)
-            tot[j] = fmaf(acc[j], sc[j], tot[j]);
+        for (int u = 0; u < KM_U; ++u) {
+            const float xv = (u & 1) ? glint_bf16hi(xs[u >> 1]) : glint_bf16lo(xs[u >> 1]);
+            const uint32_t W[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+            uint32_t E[4], O[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                E[q] = W[q] & 0x0F0F0F0Fu;
+                O[q] = (W[q] >> 4) & 0x0F0F0F0Fu;
+            }
+            km_lookup_fma(lds, E, O, lane4, xv, acc);
+        }
+        if (c + KM_U == c1 || ((c + KM_U) & 63) == 0) { /* the run ends */
+#pragma unroll
+            for (int j = 0; j < 32; ++j)
+                tot[j] = fmaf(acc[j], sc[j], tot[j]);
+        }
+    };
+    load_batch(c0, wa);
+    int c = c0;
+    for (; c + 2 * KM_U <= c1; c += 2 * KM_U) {
+        load_batch(c + KM_U, wb);
+        batch(c, wa);
+        load_batch(c + 2 * KM_U, wa);
+        batch(c + KM_U, wb);
     }
+    if (c < c1)
+        batch(c, wa);
     km_combine_parts<false>(lds, tot, r0, N, out + (int64_t)blockIdx.y * N + r0);
 }
 
@@ -211,8 +228,19 @@ __global__ __launch_bounds__(KM_T) void k_km_combine(const float *__restrict__ p
     const int r = blockIdx.x * KM_T + threadIdx.x;
     if (r >= N)
         return;
+    /* slices in groups of 8 with all 8 loads in flight, added in slice order */
     float acc = part[r];
-    for (int s = 1; s < ks; ++s)
+    int s = 1;
+    for (; s + 8 <= ks; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = part[(int64_t)(s + i) * N + r];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            acc = acc + v[i];
+    }
+    for (; s < ks; ++s)
         acc = acc + part[(int64_t)s * N + r];
     y[r] = ADD ? y[r] + acc : acc;
 }
