@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
 #define I8V_THREADS 512
 #endif
 #ifndef I8V_DEPTH
-#define I8V_DEPTH 3
+#define I8V_DEPTH 2 /* rows of loads in flight per wave */
 #endif
 #define I8V_RED_MAX 8192 /* floats of row partials a workgroup may park in LDS */
 
@@ -149,12 +149,17 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
 #pragma unroll
         for (int mr = 0; mr < MR; ++mr)
             part[mr] = 0.0f;
+        /* q s as fma(q + 128, s, -128 s): q + 128 is an unsigned byte (flip the sign bit,
+         * then v_cvt_f32_ubyte) and -128 s is exact, so the one rounding gives the f32
+         * product q s exactly as a multiply would */
+        const float ns = -128.0f * r.s;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const float lo = (float)(int8_t)(W[e] >> (16 * b)) * r.s;
-                const float hi = (float)(int8_t)(W[e] >> (16 * b + 8)) * r.s;
+                const uint32_t u = W[e] ^ 0x80808080u;
+                const float lo = fmaf((float)((u >> (16 * b)) & 0xFFu), r.s, ns);
+                const float hi = fmaf((float)((u >> (16 * b + 8)) & 0xFFu), r.s, ns);
                 const uint32_t pk = glint_cvt_bf16x2(lo, hi);
                 const float wl = glint_bf16lo(pk), wh = glint_bf16hi(pk);
 #pragma unroll
