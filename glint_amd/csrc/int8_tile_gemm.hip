@@ -149,25 +149,39 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
 #pragma unroll
         for (int mr = 0; mr < MR; ++mr)
             part[mr] = 0.0f;
+        auto accumulate = [&](auto weights) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    float lo, hi;
+                    weights(W[e], b, lo, hi);
+                    const uint32_t pk = glint_cvt_bf16x2(lo, hi);
+                    const float wl = glint_bf16lo(pk), wh = glint_bf16hi(pk);
+#pragma unroll
+                    for (int mr = 0; mr < MR; ++mr) {
+                        part[mr] = fmaf(wl, xr[mr][4 * e + 2 * b], part[mr]);
+                        part[mr] = fmaf(wh, xr[mr][4 * e + 2 * b + 1], part[mr]);
+                    }
+                }
+        };
         /* q s as fma(q + 128, s, -128 s): q + 128 is an unsigned byte (flip the sign bit,
          * then v_cvt_f32_ubyte) and -128 s is exact, so the one rounding gives the f32
-         * product q s exactly as a multiply would */
+         * product q s exactly as a multiply would. When -128 s is not finite (s infinite,
+         * NaN or above 2^120) the lane multiplies instead. */
         const float ns = -128.0f * r.s;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                const uint32_t u = W[e] ^ 0x80808080u;
-                const float lo = fmaf((float)((u >> (16 * b)) & 0xFFu), r.s, ns);
-                const float hi = fmaf((float)((u >> (16 * b + 8)) & 0xFFu), r.s, ns);
-                const uint32_t pk = glint_cvt_bf16x2(lo, hi);
-                const float wl = glint_bf16lo(pk), wh = glint_bf16hi(pk);
-#pragma unroll
-                for (int mr = 0; mr < MR; ++mr) {
-                    part[mr] = fmaf(wl, xr[mr][4 * e + 2 * b], part[mr]);
-                    part[mr] = fmaf(wh, xr[mr][4 * e + 2 * b + 1], part[mr]);
-                }
-            }
+        if (__builtin_isfinite(ns)) {
+            accumulate([&](uint32_t w, int b, float &lo, float &hi) {
+                const uint32_t u = w ^ 0x80808080u;
+                lo = fmaf((float)((u >> (16 * b)) & 0xFFu), r.s, ns);
+                hi = fmaf((float)((u >> (16 * b + 8)) & 0xFFu), r.s, ns);
+            });
+        } else {
+            accumulate([&](uint32_t w, int b, float &lo, float &hi) {
+                lo = (float)(int8_t)(w >> (16 * b)) * r.s;
+                hi = (float)(int8_t)(w >> (16 * b + 8)) * r.s;
+            });
+        }
 #pragma unroll
         for (int mr = 0; mr < MR; ++mr) {
             float v = glint_row16_sum(part[mr]);

@@ -117,6 +117,34 @@ def test_small_m_gemv_one_hot_is_exact(oracle):
         assert y.view(np.uint32).tobytes() == want.view(np.uint32).tobytes(), c
 
 
+def test_small_m_gemv_extreme_scales_are_exact(oracle):
+    """The GEMV path forms q s as fma(q + 128, s, -128 s), which is the f32 product
+    exactly while -128 s is finite. Blocks with s = 2^121 (-128 s overflows: the lane must
+    take the plain multiply; q is kept in {-1, 0, 1} so q s stays finite), the smallest
+    subnormal, subnormal products and zero: one-hot x gives y[n] = BF16(q[n, c] * s) bit
+    for bit."""
+    n, k = 64, 2048
+    rng = np.random.default_rng(9)
+    q = rng.integers(-127, 128, n * k, dtype=np.int8)
+    s = np.ldexp(1.0 + rng.random(n * k // 64), rng.integers(-12, -4, n * k // 64)).astype(np.float32)
+    special = [np.float32(2.0 ** 121), np.float32(-(2.0 ** 121)), np.float32(2.0 ** -149), np.float32(2.0 ** -140),
+               np.float32(3.0 * 2.0 ** -135), np.float32(0.0)]
+    for i, v in enumerate(special):
+        for blk in range(i, n * k // 64, 7 * len(special)):
+            s[blk] = v
+            if abs(v) > 1.0:
+                q[blk * 64:(blk + 1) * 64] = rng.integers(-1, 2, 64, dtype=np.int8)
+    w = oracle.int8_pin_dequant_bf16(q, s).reshape(n, k)
+    dq, ds = dev(q), dev(s)
+    for c in (0, 5, 64, 1000, 2047):
+        x = np.zeros(k, np.uint16)
+        x[c] = 0x3F80
+        y = host(H.int8_tile_gemm(dev(x), dq, ds, n, k, m=1))
+        want = (w[:, c].astype(np.uint32) << 16).view(np.float32) + np.float32(0.0)  # the sum starts at +0
+        assert y.view(np.uint32).tobytes() == want.view(np.uint32).tobytes(), \
+            (c, first_diff(y.view(np.uint32), want.view(np.uint32)))
+
+
 @pytest.mark.parametrize("k,aligned", [(64, True), (128, True), (640, True), (100, False), (37, False)])
 def test_one_hot_rows_give_the_dequantized_weights_exactly(oracle, k, aligned):
     """x = I (m = k one-hot rows): y[m, n] = BF16(q[n, m] * scale) exactly, since every sum
