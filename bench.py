@@ -298,7 +298,8 @@ def bench_prefill(torch, H, steps: int, copies: int = 6):
             x = torch.randn(M, K, device="cuda", generator=gx).to(torch.bfloat16)
             y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
             calls = [lambda pin=pin: H.htile_bf16(pin[0], pin[1], pin[2], x, N, K, 64, out=y) for pin in cps]
-            ms = timed(torch, calls, steps, copies)
+            settle(torch, calls, 0.05)
+            ms = timed(torch, calls, steps * (3 if M <= 64 else 1), copies)
             fl = 2.0 * M * N * K
             byt = N * K * (1 + 4 / 64) + 2 * M * K + 2 * M * N
             out[f"M{M}_{name}"] = {"ms": ms, "tflops": fl / ms / 1e9, "mfma_frac": fl / ms / 1e9 / BF16_PEAK_TFLOPS,
@@ -315,7 +316,9 @@ def bench_int8(torch, H, steps: int):
     sa = torch.rand(M, device="cuda", generator=g) * 0.019 + 1e-3
     sb = torch.rand(N, device="cuda", generator=g) * 0.019 + 1e-3
     out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-    ms = timed(torch, [lambda: H.int8_gemm_scaled_bf16(A, B, sa, sb, out=out)], steps, 2)
+    call = lambda: H.int8_gemm_scaled_bf16(A, B, sa, sb, out=out)
+    settle(torch, [call], 0.05)
+    ms = timed(torch, [call], steps, 2)
     ops = 2.0 * M * N * K
     return {"ms": ms, "tops": ops / ms / 1e9, "mfma_frac": ops / ms / 1e9 / I8_PEAK_TOPS, "shape": [M, N, K]}
 
@@ -333,7 +336,9 @@ def bench_w8a16(torch, H, steps: int, copies: int = 6):
         x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
         y = torch.empty(M, N, dtype=torch.float32, device="cuda")
         calls = [lambda w=w: H.int8_tile_gemm(x, w[0], w[1], N, K, y=y) for w in ws]
-        ms = timed(torch, calls, steps, copies)
+        settle(torch, calls, 0.05)
+        # a few-microsecond call needs many steps before launch jitter averages out
+        ms = timed(torch, calls, steps * (30 if M == 1 else 3 if M <= 64 else 1), copies)
         fl = 2.0 * M * N * K
         byt = N * K * (1 + 4 / 64) + 2 * M * K + 4 * M * N
         out[f"M{M}_{N}x{K}"] = {"ms": ms, "tflops": fl / ms / 1e9, "mfma_frac": fl / ms / 1e9 / BF16_PEAK_TFLOPS,

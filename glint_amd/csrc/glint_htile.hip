@@ -483,6 +483,9 @@ __global__ __launch_bounds__(256) void k_htile_generic(const uint8_t *__restrict
 #ifndef TILE_RX
 #define TILE_RX 4 /* x register stages of k_tile_ss (M < 256) */
 #endif
+#ifndef TILE_BIG
+#define TILE_BIG 1 /* M >= 256 takes the 256 x 256 k_tile_big */
+#endif
 #ifndef TILE_R_BIG
 #define TILE_R_BIG 2 /* register stages (K steps of loads in flight) of the 256 x 128 tiles */
 #endif
@@ -523,6 +526,8 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             tile_ss_launch<64, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
         else if (M < MF2_MIN_M)
             tile_ss_launch<128, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
+        else if (TILE_BIG && tile_big_fits(M, N, K) && tile_big_pays(M, N))
+            tile_big_launch<TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
         else
             tile_mfma_launch<MF2_BM, MF2_BN, 4, 2, TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
     } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS / 64) {

@@ -58,7 +58,11 @@ __device__ __forceinline__ uint32_t glint_cvt_bf16x2(float lo, float hi) {
 
 /* s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt [3:0] and [15:14] = 0,
  * expcnt [6:4] and lgkmcnt [11:8] at their maxima). On gfx9 stores count in vmcnt too. */
+/* dword 3 of a raw buffer resource on gfx9-family parts: 32-bit data format, no swizzle */
+#define GLINT_BUF_DWORD3 0x00020000
 #define GLINT_WAIT_VMCNT0 0x0F70
+/* s_waitcnt immediate for vmcnt(n) alone, n < 64 */
+#define GLINT_WAIT_VMCNT(n) (0x0F70 | ((n) & 15) | ((((n) >> 4) & 3) << 14))
 #ifndef TILE_INTERLEAVE
 #define TILE_INTERLEAVE 1 /* k_tile_mfma: second K slice's fragment reads between the first's MFMAs */
 #endif
@@ -84,6 +88,7 @@ struct GlintTileProducer {
     int N, K;
     float *ltab;
     static constexpr int LDS_WORDS = GLINT_LDS_CELLS_WORDS;
+    static constexpr int LOADS = 3; /* global load instructions per load() */
     struct Regs {
         glint_u32x2 h, p;
         float a;
@@ -97,6 +102,15 @@ struct GlintTileProducer {
         r.h = __builtin_nontemporal_load(&hole[q]);
         r.p = __builtin_nontemporal_load(&plug[q]);
         r.a = absmax[(int64_t)row * (K >> 6) + kb];
+    }
+    /* load() with the row given as base = row * K / 16 (8-B units), for N * K < 2^36: one
+     * 32-bit register per row instead of two 64-bit offsets */
+    __device__ __forceinline__ uint32_t row_base(int row) const { return (uint32_t)row * (uint32_t)(K >> 4); }
+    __device__ __forceinline__ void load_at(Regs &r, uint32_t base, int quarter, int kb) const {
+        const uint32_t q = base + (uint32_t)(kb * 4 + quarter);
+        r.h = __builtin_nontemporal_load(&hole[q]);
+        r.p = __builtin_nontemporal_load(&plug[q]);
+        r.a = absmax[(base >> 2) + (uint32_t)kb];
     }
     /* v[8 q + 2 b] / v[8 q + 2 b + 1]: cells of the even / odd element of byte b of word q */
     __device__ __forceinline__ void lookup(const Regs &r, float (&v)[16], int lane) const {
@@ -156,6 +170,7 @@ struct Int8PinTileProducer {
     const float *scale;
     int N, K;
     static constexpr int LDS_WORDS = 0;
+    static constexpr int LOADS = 2; /* global load instructions per load() */
     struct Regs {
         glint_u32x4 w;
         float s;
@@ -575,6 +590,178 @@ __global__ __launch_bounds__(256) void k_tile_ss(P p, const uint16_t *__restrict
             }
 }
 
+/* 256 x 256 block tile (M >= 256): 8 waves in 2 (M) x 4 (N), wave tile 128 x 64 (8 x 4 MFMA
+ * tiles, 128 accumulator registers per lane), so each MFMA operand byte read from LDS feeds
+ * 1.33x the MACs of a 64 x 64 wave tile. The x tile reaches LDS without passing through
+ * registers: each wave issues 4 buffer loads with the lds bit per step (8 rows x 128 B
+ * each), every lane loading the 16-B chunk that belongs at its LDS slot under the row
+ * swizzle. That keeps x out of the register budget the accumulators need. The x load for
+ * step j + 1 goes out at the start of step j and is waited for (s_waitcnt) before the
+ * step's closing barrier; W goes through R register stages and the producer as in
+ * k_tile_mfma (each thread makes 16 weights of two rows, t / 4 and t / 4 + 128). LDS:
+ * 2 x 32 KiB of x, 2 x 32 KiB of W, the producer's table (160 KiB in all). The producer
+ * must provide row_base / load_at (32-bit row offsets). */
+template <int R, class P, class Out>
+__global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restrict__ x, typename Out::T *__restrict__ y,
+                                                  int M, int N, int K, int kps, float *__restrict__ part,
+                                                  unsigned *ctr) {
+    constexpr int T = 512, BM = 256, BN = 256, TM = 8, TN = 4;
+    constexpr int U = (R % 2) ? 2 * R : R;
+    static_assert(R >= 2 && R <= 4, "register stages");
+    __shared__ float ptab[P::LDS_WORDS > 0 ? P::LDS_WORDS : 1];
+    /* four separate arrays, not [2][...]: the compiler then knows the x DMA into one buffer
+     * does not alias reads of the others, and does not wait for the DMA before them */
+    __shared__ __attribute__((aligned(16))) uint16_t sX0[BM * TILE_LDW], sX1[BM * TILE_LDW];
+    __shared__ __attribute__((aligned(16))) uint16_t sW0[BN * TILE_LDW], sW1[BN * TILE_LDW];
+    auto sX = [&](int b) { return b ? sX1 : sX0; };
+    auto sW = [&](int b) { return b ? sW1 : sW0; };
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kb0 = blockIdx.z * kps;
+    const int ns = min(K >> 6, kb0 + kps) - kb0; /* >= 1: the host sizes gridDim.z */
+    const int wr = tid >> 2, wq = tid & 3;
+    glint_f32x4 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+            acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
+
+    struct Stage {
+        typename P::Regs w[2];
+    };
+    Stage st[R];
+    const uint32_t wbase[2] = {p.row_base(min(n0 + wr, N - 1)), p.row_base(min(n0 + wr + 128, N - 1))};
+    auto gload = [&](int j, Stage &sg) {
+        const int kb = kb0 + min(j, ns - 1);
+        p.load_at(sg.w[0], wbase[0], wq, kb);
+        p.load_at(sg.w[1], wbase[1], wq, kb);
+    };
+    /* x DMA: wave w, instruction q covers rows 8 (4 w + q) .. +7; lane l takes row
+     * 8 (4 w + q) + l / 8, LDS slot l % 8, i.e. logical chunk (l % 8) ^ f(row) */
+    /* x DMA through a buffer resource (a MUBUF load with the lds bit: the compiler tracks its
+     * counter precisely, where the global form makes it wait for every load to finish).
+     * Wave w, instruction q covers rows 8 (4 w + q) .. +7; lane l takes row 8 (4 w + q) + l / 8,
+     * LDS slot l % 8, i.e. logical chunk (l % 8) ^ f(row). Offsets in bytes: M * K * 2 < 2^32
+     * (the host checks), and every row is clamped into the matrix. */
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), GLINT_BUF_DWORD3);
+    uint32_t xvo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = 8 * (4 * wave + q) + (lane >> 3);
+        const int chunk = ((lane & 7) ^ (((r >> 1) ^ ((r & 1) << 2)) & 7));
+        xvo[q] = ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)chunk * 8u) * 2u;
+    }
+    auto xdma = [&](int j, int buf) {
+        const uint32_t kb = (uint32_t)(kb0 + min(j, ns - 1));
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xres, (__attribute__((address_space(3))) void *)(sX(buf) + 8 * (4 * wave + q) * TILE_LDW), 16, xvo[q],
+                kb * 128u, 0, 0);
+    };
+    auto store_row = [&](int buf, const typename P::Regs &rg, int row, const float (&v)[16]) {
+        uint32_t pk[8];
+        p.finish(rg, v, pk);
+        *(glint_u32x4 *)(sW(buf) + tile_ofs(row, 2 * wq)) = glint_u32x4{pk[0], pk[1], pk[2], pk[3]};
+        *(glint_u32x4 *)(sW(buf) + tile_ofs(row, 2 * wq + 1)) = glint_u32x4{pk[4], pk[5], pk[6], pk[7]};
+    };
+    /* one K slice: the 4 B fragments, then per A tile one fragment read and its 4 MFMAs, so
+     * at most one A fragment is live (the accumulators hold 128 registers) */
+    auto kslice = [&](int cur, int ks) {
+        const int fofs = tile_ofs(lane & 15, 4 * ks + (lane >> 4));
+        glint_bf16x8 bfr[TN];
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+            bfr[b] = __builtin_bit_cast(glint_bf16x8,
+                                        *(const glint_u32x4 *)(sW(cur) + (wn * TN * 16 + b * 16) * TILE_LDW + fofs));
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const glint_bf16x8 af = __builtin_bit_cast(
+                glint_bf16x8, *(const glint_u32x4 *)(sX(cur) + (wm * TM * 16 + a * 16) * TILE_LDW + fofs));
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[b], acc[a][b], 0, 0, 0);
+        }
+    };
+    /* step j (j % U == u): the x DMA of step j + 1 into the other buffer (last read before
+     * the previous barrier); each K slice's MFMAs run while one W row of step j + 1 is looked
+     * up; then W row stores, the stage refill, the wait for the DMA, the barrier */
+    /* an empty asm that "redefines" a stage's registers where the step consumes them: without
+     * it the compiler computes a stage's lookup indices a step early, right after its loads
+     * were issued, and waits for them there */
+    auto pin = [&](typename P::Regs &rg) {
+        uint32_t *w = (uint32_t *)&rg;
+#pragma unroll
+        for (int i = 0; i < (int)(sizeof(rg) / 4); ++i)
+            asm volatile("" : "+v"(w[i]));
+    };
+    auto step = [&](int j, int u) {
+        const int cur = u & 1;
+        Stage &nx = st[(u + 1) % R];
+        xdma(j + 1, cur ^ 1);
+        pin(nx.w[0]);
+        pin(nx.w[1]);
+        float v[16];
+        p.lookup(nx.w[0], v, lane);
+        kslice(cur, 0);
+        store_row(cur ^ 1, nx.w[0], wr, v); /* past the end: clamped data nobody reads */
+        __builtin_amdgcn_sched_barrier(0); /* keep the halves apart: registers are at the limit */
+        p.lookup(nx.w[1], v, lane);
+        kslice(cur, 1);
+        store_row(cur ^ 1, nx.w[1], wr + 128, v);
+        gload(j + 1 + R, nx);
+        /* the x DMA of step j + 1 is older than the W loads just issued (two loads of
+         * P::LOADS instructions): wait until only those are outstanding */
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT(2 * P::LOADS));
+        __syncthreads();
+    };
+
+    p.setup(ptab, (float *)sX1); /* sX1 is free until step 0's x DMA */
+    xdma(0, 0);
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+        gload(i, st[i]);
+    {
+        float v[16];
+        p.lookup(st[0].w[0], v, lane);
+        store_row(0, st[0].w[0], wr, v);
+        p.lookup(st[0].w[1], v, lane);
+        store_row(0, st[0].w[1], wr + 128, v);
+    }
+    gload(R, st[0]);
+    /* only the refill just issued stays outstanding: the loop then enters with the counter
+     * state of its own back edge, and the compiler adds no full wait inside it */
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT(2 * P::LOADS));
+    __syncthreads();
+    int j = 0;
+    for (; j + U <= ns; j += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            step(j + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < U; ++u)
+        if (j + u < ns)
+            step(j + u, u);
+
+    if (gridDim.z > 1 && !tile_splitk_epilogue<TM, TN, T>(acc, part, ctr, *(unsigned *)sX0))
+        return;
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm * TM * 16 + a * 16 + (lane >> 4) * 4 + i;
+                const int n = n0 + wn * TN * 16 + b * 16 + (lane & 15);
+                if (m < M && n < N)
+                    Out::store(y, (int64_t)m * N + n, acc[a][b][i]);
+            }
+}
+
 /* ---------------------------------------------------------- split-K host side */
 #ifndef TILE_SPLIT_MIN_STEPS
 #define TILE_SPLIT_MIN_STEPS 8 /* fewest 64-wide K steps per split */
@@ -663,6 +850,26 @@ static void tile_mfma_launch(const P &p, const uint16_t *x, typename Out::T *y, 
     tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * BN, kps, ks, ws);
     k_tile_mfma<BM, BN, WM, WN, R, P, Out><<<dim3(gx, gy, (unsigned)ks), 64 * WM * WN, 0, st>>>(p, x, y, M, N, K, kps,
                                                                                               ws.part, ws.ctr);
+}
+
+/* Launch k_tile_big over an M x N output. K % 64 == 0, M, N >= 1, M * K < 2^31 and
+ * N * K < 2^36 (its 32-bit offsets; tile_big_fits). */
+static inline bool tile_big_fits(int M, int N, int K) {
+    return (int64_t)M * K < ((int64_t)1 << 31) && (int64_t)N * K < ((int64_t)1 << 36);
+}
+/* The 256 x 256 tile beats the 256 x 128 one once it has about 3/4 of a tile per CU (measured
+ * at M = 512 .. 8192 on the 14336 x 4096 and 4096 x 14336 shapes: 9-14% faster there, up to
+ * 1.8x slower with fewer tiles, where split K cannot fill the device as well). */
+static inline bool tile_big_pays(int M, int N) {
+    return (int64_t)((M + 255) / 256) * ((N + 255) / 256) * 4 >= (int64_t)3 * glint_cu_count();
+}
+template <int R, class P, class Out>
+static void tile_big_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st) {
+    const unsigned gx = (unsigned)((N + 255) / 256), gy = (unsigned)((M + 255) / 256);
+    int kps, ks;
+    GlintSplitWs ws;
+    tile_split_plan(st, gx, gy, K >> 6, (size_t)256 * 256, kps, ks, ws);
+    k_tile_big<R, P, Out><<<dim3(gx, gy, (unsigned)ks), 512, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
 }
 
 /* Launch k_tile_ss over an M x N output. K % 64 == 0, M, N >= 1. */

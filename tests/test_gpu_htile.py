@@ -115,11 +115,13 @@ def test_bf16_path_rel_frobenius(oracle, M):
     assert rel <= 4e-3  # BF16 rounding of the output alone is ~2^-9
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 1024, 4096), (300, 1000, 576), (513, 1100, 1024), (2048, 384, 640)])
+@pytest.mark.parametrize("M,N,K", [(256, 1024, 4096), (300, 1000, 576), (513, 1100, 1024), (2048, 384, 640),
+                                   (2000, 6100, 1088), (4096, 4096, 576)])
 def test_bf16_prefill_tiles_rel_frobenius(oracle, M, N, K):
-    """The large-M prefill tiles (256 x 128, double-buffered K steps): ragged M and N, an
-    odd number of K steps; bf16 out within 4e-3 relative Frobenius of fp32 on the expanded
-    weights (the contract asks 1e-2)."""
+    """The large-M prefill tiles (256 x 128, and 256 x 256 with x loaded straight into LDS
+    once there are at least 3/4 as many 256 x 256 tiles as CUs: the last two shapes on a
+    256-CU part): ragged M and N, an odd number of K steps; bf16 out within 4e-3 relative
+    Frobenius of fp32 on the expanded weights (the contract asks 1e-2)."""
     torch = torch_cuda()
     print(f"prefill M={M} N={N} K={K}", flush=True)
     hole, plug, am = _encoded_weight(oracle, N, K, 3003)
