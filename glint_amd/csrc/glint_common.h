@@ -6,6 +6,16 @@
 #include <stdint.h>
 #include <stddef.h>
 
+/* s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt [3:0] and [15:14] = 0,
+ * expcnt [6:4] and lgkmcnt [11:8] at their maxima). On gfx9 stores count in vmcnt too. */
+#define GLINT_WAIT_VMCNT0 0x0F70
+/* s_waitcnt immediate for vmcnt(n) alone, n < 64 */
+#define GLINT_WAIT_VMCNT(n) (0x0F70 | ((n) & 15) | ((((n) >> 4) & 3) << 14))
+/* s_waitcnt immediate for vmcnt(n) and lgkmcnt(0), n < 64 */
+#define GLINT_WAIT_VMCNT_LGKM0(n) (0x0070 | ((n) & 15) | ((((n) >> 4) & 3) << 14))
+/* dword 3 of a raw buffer resource on gfx9-family parts: 32-bit data format, no swizzle */
+#define GLINT_BUF_DWORD3 0x00020000
+
 #define GLINT_API extern "C" __attribute__((visibility("default")))
 
 /* ------------------------------------------------------------------ tables */

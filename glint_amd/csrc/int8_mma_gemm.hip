@@ -412,6 +412,150 @@ __global__ __launch_bounds__(512) void k_int8_gemm_256(const int8_t *__restrict_
             }
 }
 
+/* The same 256 x 256 tile and wave layout with both operands going HBM -> LDS directly
+ * (buffer loads with the lds bit), through a ring of G3_NBUF K-step buffers: the loads of
+ * step kb + G3_NBUF - 1 go out at the start of step kb, into the buffer step kb - 1 used.
+ * No staging registers and no LDS store instructions; each DMA instruction writes 1 KB of
+ * consecutive LDS (16 rows, every lane the 16-B chunk the row swizzle puts in its slot).
+ * Per step a wave waits for its own loads of the step (s_waitcnt), then the barrier makes
+ * every wave's visible. Byte offsets are 32-bit: M * K and N * K < 2^31 (the host checks).
+ * The four A and four B buffers are separate arrays, so the compiler sees that a DMA into
+ * one does not alias fragment reads of another. */
+#define G3_NBUF 4
+#ifndef G3_THREADS
+#define G3_THREADS 512
+#endif
+template <bool SCALED>
+__global__ __launch_bounds__(G3_THREADS) void k_int8_gemm_dma(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
+                                                        const float *__restrict__ sa, const float *__restrict__ sb,
+                                                        void *__restrict__ C, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) int8_t sA0[G2_BM * G2_LDS_ROW], sA1[G2_BM * G2_LDS_ROW],
+        sA2[G2_BM * G2_LDS_ROW], sA3[G2_BM * G2_LDS_ROW];
+    __shared__ __attribute__((aligned(16))) int8_t sB0[G2_BN * G2_LDS_ROW], sB1[G2_BN * G2_LDS_ROW],
+        sB2[G2_BN * G2_LDS_ROW], sB3[G2_BN * G2_LDS_ROW];
+    auto bufA = [&](int i) { return i == 0 ? sA0 : (i == 1 ? sA1 : (i == 2 ? sA2 : sA3)); };
+    auto bufB = [&](int i) { return i == 0 ? sB0 : (i == 1 ? sB1 : (i == 2 ? sB2 : sB3)); };
+    /* NW waves in 2 (M) x NW / 2 (N); wave tile 128 x TN * 16; each wave loads RPW rows of
+     * each operand per step in QN instructions */
+    constexpr int T = G3_THREADS;
+    constexpr int NW = T / 64, WNW = NW / 2, TM = 8, TN = 16 / WNW, RPW = 256 / NW, QN = RPW / 16;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WNW, wn = wave % WNW;
+    const int m0 = blockIdx.y * G2_BM, n0 = blockIdx.x * G2_BN;
+    const int nkb = K / 64;
+    glint_i32x4 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+            acc[a][b] = glint_i32x4{0, 0, 0, 0};
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)A, (short)0, (int)((uint32_t)M * (uint32_t)K), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)B, (short)0, (int)((uint32_t)N * (uint32_t)K), GLINT_BUF_DWORD3);
+    /* wave w, instruction q: rows RPW w + 16 q .. +15 of both tiles; lane l takes row
+     * RPW w + 16 q + l / 4, LDS slot l % 4, i.e. logical chunk (l % 4) ^ f(row) */
+    uint32_t avo[QN], bvo[QN];
+#pragma unroll
+    for (int q = 0; q < QN; ++q) {
+        const int r = RPW * wave + 16 * q + (lane >> 2);
+        const int c = (lane & 3) ^ (((r >> 1) ^ ((r >> 3) & 1)) & 3);
+        avo[q] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)c * 16u;
+        bvo[q] = (uint32_t)min(n0 + r, N - 1) * (uint32_t)K + (uint32_t)c * 16u;
+    }
+    /* step kb's 2 QN loads per wave into ring slot buf; steps past the end reload the last */
+    auto dma = [&](int kb, int buf) {
+        const uint32_t so = (uint32_t)min(kb, nkb - 1) * 64u;
+#pragma unroll
+        for (int q = 0; q < QN; ++q) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void *)(bufA(buf) + (RPW * wave + 16 * q) * G2_LDS_ROW), 16,
+                avo[q], so, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void *)(bufB(buf) + (RPW * wave + 16 * q) * G2_LDS_ROW), 16,
+                bvo[q], so, 0, 0);
+        }
+    };
+    const int fr_ofs = g2_lds_ofs(lane & 15, lane >> 4);
+    /* step kb from ring slot u = kb % G3_NBUF (a constant after unrolling) */
+    auto step = [&](int kb, int u) {
+        /* this wave's loads of step kb are done once only the later steps' 2 QN each remain,
+         * and its fragment reads of step kb - 1 are done (their slot is refilled next) */
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(2 * QN * (G3_NBUF - 2)));
+        /* A barrier with fences that order global memory only. __syncthreads() orders LDS as
+         * well, and the compiler then waits for every LDS DMA in flight (vmcnt(0)) at each
+         * step, which empties the ring. The fences still keep the compiler from moving memory
+         * accesses across the barrier; the explicit wait above gives the LDS ordering. */
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
+        __builtin_amdgcn_s_barrier(); /* every wave's loads of step kb landed; slot (u + 3) % 4 is free */
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
+        dma(kb + G3_NBUF - 1, (u + G3_NBUF - 1) % G3_NBUF);
+        __builtin_amdgcn_sched_barrier(0); /* issue the loads first, not after the MFMAs */
+        const int8_t *ta = bufA(u), *tb = bufB(u);
+        glint_i32x4 bf[TN];
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+            bf[b] = *(const glint_i32x4 *)(tb + (wn * TN * 16 + b * 16) * G2_LDS_ROW + fr_ofs);
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const glint_i32x4 af = *(const glint_i32x4 *)(ta + (wm * 128 + a * 16) * G2_LDS_ROW + fr_ofs);
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+                acc[a][b] = glint_mfma_i8(af, bf[b], acc[a][b]);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < G3_NBUF - 1; ++i)
+        dma(i, i);
+    int kb = 0;
+    for (; kb + G3_NBUF <= nkb; kb += G3_NBUF) {
+#pragma unroll
+        for (int u = 0; u < G3_NBUF; ++u)
+            step(kb + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < G3_NBUF; ++u)
+        if (kb + u < nkb)
+            step(kb + u, u);
+    /* the ring's last loads (reloads past the end) must land before the workgroup's LDS is
+     * released */
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0);
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = m0 + wm * 128 + a * 16 + (lane >> 4) * 4 + i;
+                const int c = n0 + wn * TN * 16 + b * 16 + (lane & 15);
+                if (r < M && c < N) {
+                    if (SCALED)
+                        ((uint16_t *)C)[(int64_t)r * N + c] = glint_f32_to_bf16(((float)acc[a][b][i] * sa[r]) * sb[c]);
+                    else
+                        ((int32_t *)C)[(int64_t)r * N + c] = acc[a][b][i];
+                }
+            }
+}
+
+#ifndef G3_DMA
+#define G3_DMA 1
+#endif
+static inline bool g3_fits(int M, int N, int K) {
+    return G3_DMA && (int64_t)M * K < ((int64_t)1 << 31) && (int64_t)N * K < ((int64_t)1 << 31);
+}
+#ifndef G2_MIN_FILL
+#define G2_MIN_FILL 1
+#endif
+/* The 256 x 256 tiles need at least 3/4 as many tiles as CUs; with fewer, the 128 x 128
+ * kernel's 4x more tiles fill the device better (512 x 8192 x 8192: 64 tiles of 256 x 256
+ * on 256 CUs). */
+static inline bool g2_pays(int M, int N) {
+    if (M < G2_BM || N < G2_BN)
+        return false;
+    return !G2_MIN_FILL ||
+           (int64_t)((M + G2_BM - 1) / G2_BM) * ((N + G2_BN - 1) / G2_BN) * 4 >= (int64_t)3 * glint_cu_count();
+}
+
 /* ------------------------------------------------------------------ C ABI */
 static bool q_args_ok(const void *x, const void *y, const void *xq, const void *sx, const Int8MmaLinear &w, int m) {
     return x && y && xq && sx && w.q && w.scale && m >= 1 && w.n_out >= 1 && w.k_in >= 64 && (w.k_in % 64) == 0 &&
@@ -502,7 +646,12 @@ GLINT_API int glint_int8_gemm_i32(const int8_t *A, const int8_t *B, int32_t *C, 
                                   struct ihipStream_t *stream) {
     if (!A || !B || !C || M < 1 || N < 1 || K < 64 || (K % 64) != 0 || !glint_aligned(A, 16) || !glint_aligned(B, 16))
         return (int)hipErrorInvalidValue;
-    if (M >= G2_BM && N >= G2_BN)
+    const bool big = g2_pays(M, N);
+    if (big && g3_fits(M, N, K))
+        k_int8_gemm_dma<false><<<dim3((N + G2_BN - 1) / G2_BN, (M + G2_BM - 1) / G2_BM), G3_THREADS, 0,
+                                             (hipStream_t)stream>>>(
+            A, B, nullptr, nullptr, C, M, N, K);
+    else if (big)
         k_int8_gemm_256<false><<<dim3((N + G2_BN - 1) / G2_BN, (M + G2_BM - 1) / G2_BM), 512, 0, (hipStream_t)stream>>>(
             A, B, nullptr, nullptr, C, M, N, K);
     else
@@ -516,7 +665,12 @@ GLINT_API int glint_int8_gemm_scaled_bf16(const int8_t *A, const int8_t *B, cons
     if (!A || !B || !sa || !sb || !out || M < 1 || N < 1 || K < 64 || (K % 64) != 0 || !glint_aligned(A, 16) ||
         !glint_aligned(B, 16))
         return (int)hipErrorInvalidValue;
-    if (M >= G2_BM && N >= G2_BN)
+    const bool big = g2_pays(M, N);
+    if (big && g3_fits(M, N, K))
+        k_int8_gemm_dma<true><<<dim3((N + G2_BN - 1) / G2_BN, (M + G2_BM - 1) / G2_BM), G3_THREADS, 0,
+                                            (hipStream_t)stream>>>(
+            A, B, sa, sb, out, M, N, K);
+    else if (big)
         k_int8_gemm_256<true><<<dim3((N + G2_BN - 1) / G2_BN, (M + G2_BM - 1) / G2_BM), 512, 0, (hipStream_t)stream>>>(
             A, B, sa, sb, out, M, N, K);
     else

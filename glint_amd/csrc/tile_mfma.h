@@ -56,13 +56,6 @@ __device__ __forceinline__ uint32_t glint_cvt_bf16x2(float lo, float hi) {
 #define TILE_SPLIT_MAX 4 /* most K splits per output tile */
 #endif
 
-/* s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt [3:0] and [15:14] = 0,
- * expcnt [6:4] and lgkmcnt [11:8] at their maxima). On gfx9 stores count in vmcnt too. */
-/* dword 3 of a raw buffer resource on gfx9-family parts: 32-bit data format, no swizzle */
-#define GLINT_BUF_DWORD3 0x00020000
-#define GLINT_WAIT_VMCNT0 0x0F70
-/* s_waitcnt immediate for vmcnt(n) alone, n < 64 */
-#define GLINT_WAIT_VMCNT(n) (0x0F70 | ((n) & 15) | ((((n) >> 4) & 3) << 14))
 #ifndef TILE_INTERLEAVE
 #define TILE_INTERLEAVE 1 /* k_tile_mfma: second K slice's fragment reads between the first's MFMAs */
 #endif

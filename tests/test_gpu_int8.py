@@ -69,8 +69,8 @@ def test_flat_entry_and_refusal():
 @pytest.mark.parametrize("M,N,K", [(128, 128, 64), (200, 130, 192), (256, 512, 1024), (2048, 256, 8192),
                                    (257, 300, 640), (512, 1024, 2048), (300, 257, 64), (1000, 520, 128)])
 def test_int8_gemm_exact(oracle, M, N, K):
-    """Below 256 rows or columns the 128 x 128 tile kernel runs, above the 256 x 256 one
-    (ragged edges, one and odd numbers of K steps)."""
+    """The 128 x 128 tile kernel (every shape here has fewer 256 x 256 tiles than 3/4 of the
+    CUs): ragged edges, one and odd numbers of K steps."""
     print(f"int8_gemm M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M + N + K)
     A = rng.integers(-127, 128, (M, K), dtype=np.int8)
@@ -85,9 +85,36 @@ def test_int8_gemm_exact(oracle, M, N, K):
     assert np.array_equal(out, oracle.int8_scale_bf16(ref, sa, sb, M, N))
 
 
-def test_int8_gemm_extremes(oracle):
-    """All -127 / all 127 at the largest K of the benchmark: |C| = K * 127^2 = 132 million."""
-    M, N, K = 256, 256, 8192
+@pytest.mark.parametrize("M,N,K", [(4096, 3100, 640), (3000, 4100, 64)])
+def test_int8_gemm_dma_tiles_exact(oracle, M, N, K):
+    """The 256 x 256 kernel whose operands go HBM -> LDS directly (a 4-deep ring of K steps)
+    runs once there are at least 3/4 as many 256 x 256 tiles as CUs: both shapes on a
+    256-CU part, with ragged M and N, 10 K steps (not a multiple of the ring) and a single
+    one. Exact int32 against the oracle on the first and last 256-row bands; every row and
+    column through exact int64 row and column sums (sum_n C[m, n] = A[m] . sum_n B[n])."""
+    print(f"int8_gemm dma M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + 3 * N + K)
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = rng.uniform(1e-3, 2e-2, M).astype(np.float32)
+    sb = rng.uniform(1e-3, 2e-2, N).astype(np.float32)
+    dA, dB = dev(A).reshape(M, K), dev(B).reshape(N, K)
+    C = host(H.int8_gemm_i32(dA, dB))
+    out = host(H.int8_gemm_scaled_bf16(dA, dB, dev(sa), dev(sb)), np.uint16)
+    for r0, r1 in ((0, 256), (M - 256, M)):
+        ref = oracle.int8_gemm_i32(A[r0:r1], B, r1 - r0, N, K)
+        assert np.array_equal(C[r0:r1], ref), (r0, first_diff(C[r0:r1], ref))
+        assert np.array_equal(out[r0:r1], oracle.int8_scale_bf16(ref, sa[r0:r1], sb, r1 - r0, N)), r0
+    A64, B64 = A.astype(np.int64), B.astype(np.int64)
+    assert np.array_equal(C.astype(np.int64).sum(axis=1), A64 @ B64.sum(axis=0))
+    assert np.array_equal(C.astype(np.int64).sum(axis=0), B64 @ A64.sum(axis=0))
+
+
+@pytest.mark.parametrize("M,N", [(256, 256), (4096, 3328)])
+def test_int8_gemm_extremes(oracle, M, N):
+    """All -127 / all 127 at the largest K of the benchmark: |C| = K * 127^2 = 132 million,
+    on the 128 x 128 kernel and on the 256 x 256 one (208 tiles)."""
+    K = 8192
     A = np.full((M, K), -127, np.int8)
     B = np.full((N, K), 127, np.int8)
     B[1::2] = -127
