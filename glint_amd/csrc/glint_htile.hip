@@ -483,9 +483,6 @@ __global__ __launch_bounds__(256) void k_htile_generic(const uint8_t *__restrict
 #ifndef TILE_RX
 #define TILE_RX 4 /* x register stages of k_tile_ss (M < 256) */
 #endif
-#ifndef TILE_BIG
-#define TILE_BIG 1 /* M >= 256 takes the 256 x 256 k_tile_big */
-#endif
 #ifndef TILE_R_BIG
 #define TILE_R_BIG 2 /* register stages (K steps of loads in flight) of the 256 x 128 tiles */
 #endif

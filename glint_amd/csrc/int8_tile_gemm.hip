@@ -240,6 +240,25 @@ static void i8tile_launch_fast(const uint16_t *x, const Int8PinLinear &w, float 
     }
 }
 
+/* The 256 x 256 prefill tile (x straight into LDS), where it has enough tiles */
+static bool i8tile_launch_big(const uint16_t *x, const Int8PinLinear &w, float *y, int m, hipStream_t st) {
+    if (!TILE_BIG || !tile_big_fits(std::min(m, I8_MAX_YBLOCKS * 256), w.n_out, w.k_in) ||
+        !tile_big_pays(std::min(m, I8_MAX_YBLOCKS * 256), w.n_out))
+        return false;
+    const Int8PinTileProducer p{(const glint_u32x4 *)w.q, w.scale, w.n_out, w.k_in};
+    for (int64_t r0 = 0; r0 < m; r0 += (int64_t)I8_MAX_YBLOCKS * 256) {
+        const int mm = (int)std::min<int64_t>((int64_t)I8_MAX_YBLOCKS * 256, m - r0);
+        if (tile_big_pays(mm, w.n_out))
+            tile_big_launch<2, Int8PinTileProducer, TileOutF32>(p, x + r0 * w.k_in, y + r0 * w.n_out, mm, w.n_out,
+                                                                w.k_in, st);
+        else
+            tile_mfma_launch<256, 128, 4, 2, 2, Int8PinTileProducer, TileOutF32>(p, x + r0 * w.k_in,
+                                                                                y + r0 * w.n_out, mm, w.n_out,
+                                                                                w.k_in, st);
+    }
+    return true;
+}
+
 template <int BM>
 static void i8tile_launch_ss(const uint16_t *x, const Int8PinLinear &w, float *y, int m, hipStream_t st) {
     const Int8PinTileProducer p{(const glint_u32x4 *)w.q, w.scale, w.n_out, w.k_in};
@@ -271,7 +290,9 @@ GLINT_API int int8_tile_gemm_bf16(const void *x_bf16, Int8PinLinear w, float *y,
         else
             i8tile_launch_gemv<4>(x, w, y, stream);
     } else if (fast) {
-        if (m >= 256)
+        if (m >= 256 && i8tile_launch_big(x, w, y, m, stream))
+            ;
+        else if (m >= 256)
             i8tile_launch_fast<256, 128, 4, 2, 2>(x, w, y, m, stream);
         else if (m > 64)
             i8tile_launch_ss<128>(x, w, y, m, stream);

@@ -98,6 +98,7 @@ struct GlintTileProducer {
     }
     /* load() with the row given as base = row * K / 16 (8-B units), for N * K < 2^36: one
      * 32-bit register per row instead of two 64-bit offsets */
+    static constexpr int REG_WORDS = 5; /* h, p, a: the leading words of Regs */
     __device__ __forceinline__ uint32_t row_base(int row) const { return (uint32_t)row * (uint32_t)(K >> 4); }
     __device__ __forceinline__ void load_at(Regs &r, uint32_t base, int quarter, int kb) const {
         const uint32_t q = base + (uint32_t)(kb * 4 + quarter);
@@ -172,6 +173,13 @@ struct Int8PinTileProducer {
     __device__ __forceinline__ void load(Regs &r, int row, int quarter, int kb) const {
         r.w = __builtin_nontemporal_load(&q[(int64_t)row * (K >> 4) + kb * 4 + quarter]);
         r.s = scale[(int64_t)row * (K >> 6) + kb];
+    }
+    /* load() with the row given as base = row * K / 16 (16-B units), for N * K < 2^36 */
+    static constexpr int REG_WORDS = 5; /* w, s: the leading words of Regs */
+    __device__ __forceinline__ uint32_t row_base(int row) const { return (uint32_t)row * (uint32_t)(K >> 4); }
+    __device__ __forceinline__ void load_at(Regs &r, uint32_t base, int quarter, int kb) const {
+        r.w = __builtin_nontemporal_load(&q[base + (uint32_t)(kb * 4 + quarter)]);
+        r.s = scale[(base >> 2) + (uint32_t)kb];
     }
     __device__ __forceinline__ void lookup(const Regs &r, float (&v)[16], int) const {
         const uint32_t W[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
@@ -593,7 +601,7 @@ __global__ __launch_bounds__(256) void k_tile_ss(P p, const uint16_t *__restrict
  * step's closing barrier; W goes through R register stages and the producer as in
  * k_tile_mfma (each thread makes 16 weights of two rows, t / 4 and t / 4 + 128). LDS:
  * 2 x 32 KiB of x, 2 x 32 KiB of W, the producer's table (160 KiB in all). The producer
- * must provide row_base / load_at (32-bit row offsets). */
+ * must provide row_base / load_at (32-bit row offsets) and REG_WORDS. */
 template <int R, class P, class Out>
 __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restrict__ x, typename Out::T *__restrict__ y,
                                                   int M, int N, int K, int kps, float *__restrict__ part,
@@ -688,7 +696,7 @@ __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restric
     auto pin = [&](typename P::Regs &rg) {
         uint32_t *w = (uint32_t *)&rg;
 #pragma unroll
-        for (int i = 0; i < (int)(sizeof(rg) / 4); ++i)
+        for (int i = 0; i < P::REG_WORDS; ++i)
             asm volatile("" : "+v"(w[i]));
     };
     auto step = [&](int j, int u) {
@@ -850,6 +858,9 @@ static void tile_mfma_launch(const P &p, const uint16_t *x, typename Out::T *y, 
 static inline bool tile_big_fits(int M, int N, int K) {
     return (int64_t)M * K < ((int64_t)1 << 31) && (int64_t)N * K < ((int64_t)1 << 36);
 }
+#ifndef TILE_BIG
+#define TILE_BIG 1 /* M >= 256 may take the 256 x 256 k_tile_big (tile_big_pays) */
+#endif
 /* The 256 x 256 tile beats the 256 x 128 one once it has about 3/4 of a tile per CU (measured
  * at M = 512 .. 8192 on the 14336 x 4096 and 4096 x 14336 shapes: 9-14% faster there, up to
  * 1.8x slower with fewer tiles, where split K cannot fill the device as well). */

@@ -10,7 +10,7 @@ The checks restate the reference's own test (tests/test_int8_tile_gemm.cu):
 
 Two bit-exact checks of the dequantization are added: one-hot activations make
 y = W^T exactly, on both the MFMA path and the generic path. Large-M shapes cover the
-256 x 128 tiles.
+256 x 128 and 256 x 256 tiles.
 """
 import ctypes
 
@@ -70,8 +70,11 @@ def test_unaligned_pointers(oracle, x_off, q_off, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(256, 129, 1024), (300, 1000, 576), (513, 64, 64), (2048, 384, 640),
-                                   (1024, 4096, 4096), (64, 14336, 4096), (64, 4096, 14336), (100, 200, 8192)])
+                                   (1024, 4096, 4096), (64, 14336, 4096), (64, 4096, 14336), (100, 200, 8192),
+                                   (2000, 6400, 576), (4096, 4096, 640)])
 def test_large_m_tiles(oracle, m, n, k):
+    """The last two shapes have at least 3/4 as many 256 x 256 tiles as a 256-CU part has
+    CUs, so they run the 256 x 256 tile with x loaded straight into LDS."""
     print(f"int8_tile large m={m} n={n} k={k}", flush=True)
     rng = np.random.default_rng(m + n + k)
     x, q, s = _case(rng, m, n, k)
@@ -145,11 +148,14 @@ def test_small_m_gemv_extreme_scales_are_exact(oracle):
             (c, first_diff(y.view(np.uint32), want.view(np.uint32)))
 
 
-@pytest.mark.parametrize("k,aligned", [(64, True), (128, True), (640, True), (100, False), (37, False)])
+@pytest.mark.parametrize("k,aligned", [(64, True), (128, True), (640, True), (100, False), (37, False),
+                                       (4096, True)])
 def test_one_hot_rows_give_the_dequantized_weights_exactly(oracle, k, aligned):
     """x = I (m = k one-hot rows): y[m, n] = BF16(q[n, m] * scale) exactly, since every sum
-    has one nonzero term. Pins the in-register dequantization bit for bit."""
-    n = 100
+    has one nonzero term. Pins the in-register dequantization bit for bit; k = 4096 with
+    n = 3100 (208 tiles of 256 x 256) runs the 256 x 256 tile whose x goes straight into
+    LDS, so it pins that tile's x placement too."""
+    n = 3100 if k == 4096 else 100
     print(f"int8_tile one-hot k={k}", flush=True)
     rng = np.random.default_rng(k)
     q = rng.integers(-127, 128, n * k, dtype=np.int8)
