@@ -88,13 +88,17 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
  * r0 + g, r0 + g + G, ... of its workgroup's row range: per row each lane reads 32 int8
  * (two 16-B loads, one 64-block, so one scale). Weights are rounded to BF16 exactly as the
  * tile kernels do (v_cvt_pk_bf16_f32 of q * scale); products accumulate with f32 FMAs.
- * Three rows are in flight per wave; loads are unconditional (rows clamped at the end).
+ * Two rows are in flight per wave (four at m = 1, k_in <= 4096); loads are unconditional
+ * (rows clamped at the end).
  * A row's S slice sums (DPP within the wave) meet in LDS and are added in slice order. */
 #ifndef I8V_THREADS
 #define I8V_THREADS 512
 #endif
 #ifndef I8V_DEPTH
-#define I8V_DEPTH 2 /* rows of loads in flight per wave */
+#define I8V_DEPTH 2 /* rows of loads in flight per wave (I8V_DEPTH_M1 for m = 1, k_in <= 4096) */
+#endif
+#ifndef I8V_DEPTH_M1
+#define I8V_DEPTH_M1 4
 #endif
 #define I8V_RED_MAX 8192 /* floats of row partials a workgroup may park in LDS */
 
@@ -103,7 +107,7 @@ struct I8Row {
     float s;
 };
 
-template <int MR>
+template <int MR, int DEPTH>
 __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *__restrict__ q,
                                                              const float *__restrict__ scale,
                                                              const glint_u32x4 *__restrict__ x, float *__restrict__ y,
@@ -139,9 +143,9 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
                 xr[mr][8 * h + 2 * e + 1] = glint_bf16hi(d[e]);
             }
         }
-    I8Row buf[I8V_DEPTH];
+    I8Row buf[DEPTH];
 #pragma unroll
-    for (int d = 0; d < I8V_DEPTH; ++d)
+    for (int d = 0; d < DEPTH; ++d)
         load(d, buf[d]);
     auto compute = [&](int i, const I8Row &r) {
         const uint32_t W[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
@@ -192,15 +196,15 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
         }
     };
     int i = 0;
-    for (; i + I8V_DEPTH <= my; i += I8V_DEPTH) {
+    for (; i + DEPTH <= my; i += DEPTH) {
 #pragma unroll
-        for (int d = 0; d < I8V_DEPTH; ++d) {
+        for (int d = 0; d < DEPTH; ++d) {
             compute(i + d, buf[d]);
-            load(i + d + I8V_DEPTH, buf[d]);
+            load(i + d + DEPTH, buf[d]);
         }
     }
 #pragma unroll
-    for (int d = 0; d < I8V_DEPTH - 1; ++d)
+    for (int d = 0; d < DEPTH - 1; ++d)
         if (i + d < my)
             compute(i + d, buf[d]);
     __syncthreads();
@@ -216,7 +220,9 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
 template <int MR>
 static void i8tile_launch_gemv(const uint16_t *x, const Int8PinLinear &w, float *y, hipStream_t st) {
     const int S = w.k_in / 2048, G = (I8V_THREADS / 64) / S, threads = 64 * S * G;
-    auto kern = k_i8tile_gemv<MR>;
+    /* 4 rows in flight measured 14% faster at m = 1, k_in = 4096 (14.6 against 17.0 us on
+     * 14336 x 4096) and 2-5% slower at k_in = 14336 or m = 4 */
+    auto kern = (MR == 1 && S <= 2) ? k_i8tile_gemv<MR, I8V_DEPTH_M1> : k_i8tile_gemv<MR, I8V_DEPTH>;
     const int64_t resident = glint_resident_grid((const void *)kern, threads, I8V_RED_MAX * 4);
     const int64_t per_wave = ((int64_t)w.n_out + G * resident - 1) / (G * resident);
     int64_t rows_per_wg = G * per_wave;
