@@ -5,8 +5,8 @@
  *
  * k_kmajor_pack_planes — 64 rows x 64 channels per workgroup through LDS: 8-byte loads of
  *   the row-major planes, 4-byte stores of the K-major rows.
- * k_gemv_km_fold — a lane owns 32 output rows (16 B of a K-major hole row), so a wave
- *   reads 1 KiB contiguous per channel; the 8 waves of a workgroup take 8 parts of the
+ * k_gemv_km_fold — a lane owns KM_FOLD_RPL = 8 output rows (4 B of a K-major hole row), so
+ *   a wave reads 256 B contiguous per channel; the 8 waves of a workgroup take 8 parts of the
  *   workgroup's channel slice (grid.y) and meet in LDS. Per element: one v_perm for the
  *   address, one lookup in the 64-copy PARENT table, one FMA by the wave-uniform x[c];
  *   the block scale is applied once per run of channels inside a 64-block.
@@ -16,6 +16,7 @@
  *   device), with the 256-entry delta table (CELLS - PARENT) in 64 lane copies.
  */
 #include <algorithm>
+#include <type_traits>
 
 #include "glint_common.h"
 #include "glint_select.h"
@@ -89,27 +90,33 @@ __global__ __launch_bounds__(KM_T) void k_kmajor_scales(const float *__restrict_
 #define KM_ROWS 2048            /* output rows per workgroup: 64 lanes x 32 rows */
 #define KM_WG (64 * KM_SUB)
 #define KM_U 4                  /* channels per batch (two batches in flight per wave) */
+#ifndef KM_FOLD_RPL
+#define KM_FOLD_RPL 8 /* fold: output rows per lane (8, 16 or 32); the correction uses 32 */
+#endif
 
 __device__ __forceinline__ float km_bf16(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
-/* 32 consecutive floats (this lane's rows of one scale row) */
-__device__ __forceinline__ void km_load32(const float *__restrict__ p, float (&v)[32]) {
+/* RPL consecutive floats (this lane's rows of one scale row) */
+template <int RPL>
+__device__ __forceinline__ void km_load(const float *__restrict__ p, float (&v)[RPL]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < RPL / 4; ++i) {
         const glint_f32x4 t = *(const glint_f32x4 *)(p + 4 * i);
         v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
     }
 }
 
-/* acc[j] = fmaf(table[code of row j], xv, acc[j]) for this lane's 32 rows. E[q]/O[q] hold
+/* acc[j] = fmaf(table[code of row j], xv, acc[j]) for this lane's RPL rows. E[q]/O[q] hold
  * the code bytes of the even/odd rows of word q (byte k -> rows 8 q + 2k, 8 q + 2k + 1).
- * All 32 lookups are issued before the first FMA (sched_barrier), so their LDS latencies
+ * All RPL lookups are issued before the first FMA (sched_barrier), so their LDS latencies
  * overlap instead of each FMA waiting for its own lookup. */
-__device__ __forceinline__ void km_lookup_fma(const float *lds, const uint32_t (&E)[4], const uint32_t (&O)[4],
-                                              uint32_t lane4, float xv, float (&acc)[32]) {
-    float tv[32];
+template <int RPL>
+__device__ __forceinline__ void km_lookup_fma(const float *lds, const uint32_t (&E)[RPL / 8],
+                                              const uint32_t (&O)[RPL / 8], uint32_t lane4, float xv,
+                                              float (&acc)[RPL]) {
+    float tv[RPL];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < RPL / 8; ++q) {
         tv[8 * q + 0] = glint_lds_f32(lds, glint_cell_addr<0>(E[q], lane4));
         tv[8 * q + 1] = glint_lds_f32(lds, glint_cell_addr<0>(O[q], lane4));
         tv[8 * q + 2] = glint_lds_f32(lds, glint_cell_addr<1>(E[q], lane4));
@@ -121,28 +128,29 @@ __device__ __forceinline__ void km_lookup_fma(const float *lds, const uint32_t (
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < 32; ++j)
+    for (int j = 0; j < RPL; ++j)
         acc[j] = fmaf(tv[j], xv, acc[j]);
 }
 
 /* The workgroup's KM_SUB part sums (one per wave) meet in LDS and are added in order;
  * the sum of rows r0 + rr goes to dst[rr] (plus dst[rr] first when ADD). */
-template <bool ADD>
-__device__ __forceinline__ void km_combine_parts(float *lds, const float (&tot)[32], int r0, int N, float *dst) {
+template <bool ADD, int RPL>
+__device__ __forceinline__ void km_combine_parts(float *lds, const float (&tot)[RPL], int r0, int N, float *dst) {
+    constexpr int ROWS = 64 * RPL;
     const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
     __syncthreads(); /* the lookup table is dead: the part sums go over it */
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        *(glint_f32x4 *)(lds + q * KM_ROWS + 32 * lane + 4 * i) =
+    for (int i = 0; i < RPL / 4; ++i)
+        *(glint_f32x4 *)(lds + q * ROWS + RPL * lane + 4 * i) =
             glint_f32x4{tot[4 * i], tot[4 * i + 1], tot[4 * i + 2], tot[4 * i + 3]};
     __syncthreads();
-    for (int rr = threadIdx.x; rr < KM_ROWS; rr += KM_WG) {
+    for (int rr = threadIdx.x; rr < ROWS; rr += KM_WG) {
         if (r0 + rr >= N)
             break;
         float v = lds[rr];
 #pragma unroll
         for (int k = 1; k < KM_SUB; ++k)
-            v = v + lds[k * KM_ROWS + rr];
+            v = v + lds[k * ROWS + rr];
         dst[rr] = ADD ? dst[rr] + v : v;
     }
 }
@@ -150,41 +158,48 @@ __device__ __forceinline__ void km_combine_parts(float *lds, const float (&tot)[
 /* Workgroup (row block bx, channel slice by): wave q walks part q of the slice as runs of
  * channels inside one 64-block; out[by N + r] (y when there is one slice) = the slice's
  * sum for row r. N % 32 == 0; rows of lanes past N are clamped and not stored. */
-__global__ __launch_bounds__(KM_WG) void k_gemv_km_fold(const glint_u32x4 *__restrict__ hole_k,
+template <int RPL>
+__global__ __launch_bounds__(KM_WG) void k_gemv_km_fold(const uint8_t *__restrict__ hole_bytes,
                                                         const float *__restrict__ scales_k,
                                                         const uint16_t *__restrict__ x, float *__restrict__ out, int N,
                                                         int ksl) {
-    __shared__ __attribute__((aligned(16))) float lds[KM_SUB * KM_ROWS]; /* PARENT table at offset 0, then parts */
+    constexpr int ROWS = 64 * RPL, NW = RPL / 8; /* rows per workgroup, code words per lane */
+    using HV = typename std::conditional<RPL == 32, glint_u32x4,
+                                         typename std::conditional<RPL == 16, glint_u32x2, uint32_t>::type>::type;
+    static_assert(RPL == 8 || RPL == 16 || RPL == 32, "rows per lane");
+    static_assert(KM_SUB * ROWS >= 16 * 64, "PARENT table fits the part buffer");
+    const HV *__restrict__ hole_k = (const HV *)hole_bytes;
+    __shared__ __attribute__((aligned(16))) float lds[KM_SUB * ROWS]; /* PARENT table at offset 0, then parts */
     for (int i = threadIdx.x; i < 16 * 64; i += KM_WG)
         lds[i] = kParent[i >> 6];
     __syncthreads();
     const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lane4 = (uint32_t)lane * 4u;
-    const int r0 = blockIdx.x * KM_ROWS;
-    const int rc = min(r0 + 32 * lane, N - 32); /* this lane's first row, clamped */
-    const int64_t rowv = N / 32;                /* 16-B vectors per K-major row */
+    const int r0 = blockIdx.x * ROWS;
+    const int rc = min(r0 + RPL * lane, N - RPL); /* this lane's first row, clamped */
+    const int64_t rowv = N / RPL;                 /* RPL / 2-byte vectors per K-major row */
     const int sub = ksl / KM_SUB;
     const int c0 = blockIdx.y * ksl + q * sub, c1 = c0 + sub;
-    float tot[32], acc[32], sc[32];
+    float tot[RPL], acc[RPL], sc[RPL];
 #pragma unroll
-    for (int j = 0; j < 32; ++j)
+    for (int j = 0; j < RPL; ++j)
         tot[j] = 0.f;
     /* Batches of KM_U channels (a batch never crosses a 64-block: parts are multiples of
      * KM_U and blocks multiples of 64), the next batch's loads in flight while this one is
      * looked up. A run is the batches of one block: acc restarts at its first batch and is
      * folded into tot by the block scale after its last, in channel order. */
-    auto load_batch = [&](int c, glint_u32x4 (&wv)[KM_U]) {
+    auto load_batch = [&](int c, HV (&wv)[KM_U]) {
         c = min(c, c1 - KM_U); /* past the part: a clamped reload nobody uses */
 #pragma unroll
         for (int u = 0; u < KM_U; ++u)
-            wv[u] = __builtin_nontemporal_load(&hole_k[(int64_t)(c + u) * rowv + rc / 32]);
+            wv[u] = __builtin_nontemporal_load(&hole_k[(int64_t)(c + u) * rowv + rc / RPL]);
     };
-    glint_u32x4 wa[KM_U], wb[KM_U];
-    auto batch = [&](int c, const glint_u32x4 (&wv)[KM_U]) {
+    HV wa[KM_U], wb[KM_U];
+    auto batch = [&](int c, const HV (&wv)[KM_U]) {
         if (c == c0 || (c & 63) == 0) { /* a run starts: its block scales, acc from zero */
-            km_load32(scales_k + (int64_t)(c >> 6) * N + rc, sc);
+            km_load<RPL>(scales_k + (int64_t)(c >> 6) * N + rc, sc);
 #pragma unroll
-            for (int j = 0; j < 32; ++j)
+            for (int j = 0; j < RPL; ++j)
                 acc[j] = 0.f;
         }
         /* the batch's 4 x values in one wave-uniform 8-B load, waited for once before the
@@ -194,18 +209,19 @@ __global__ __launch_bounds__(KM_WG) void k_gemv_km_fold(const glint_u32x4 *__res
 #pragma unroll
         for (int u = 0; u < KM_U; ++u) {
             const float xv = (u & 1) ? glint_bf16hi(xs[u >> 1]) : glint_bf16lo(xs[u >> 1]);
-            const uint32_t W[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-            uint32_t E[4], O[4];
+            uint32_t W[NW];
+            __builtin_memcpy(W, &wv[u], sizeof(W));
+            uint32_t E[NW], O[NW];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < NW; ++q) {
                 E[q] = W[q] & 0x0F0F0F0Fu;
                 O[q] = (W[q] >> 4) & 0x0F0F0F0Fu;
             }
-            km_lookup_fma(lds, E, O, lane4, xv, acc);
+            km_lookup_fma<RPL>(lds, E, O, lane4, xv, acc);
         }
         if (c + KM_U == c1 || ((c + KM_U) & 63) == 0) { /* the run ends */
 #pragma unroll
-            for (int j = 0; j < 32; ++j)
+            for (int j = 0; j < RPL; ++j)
                 tot[j] = fmaf(acc[j], sc[j], tot[j]);
         }
     };
@@ -219,7 +235,7 @@ __global__ __launch_bounds__(KM_WG) void k_gemv_km_fold(const glint_u32x4 *__res
     }
     if (c < c1)
         batch(c, wa);
-    km_combine_parts<false>(lds, tot, r0, N, out + (int64_t)blockIdx.y * N + r0);
+    km_combine_parts<false, RPL>(lds, tot, r0, N, out + (int64_t)blockIdx.y * N + r0);
 }
 
 /* y[r] = ((part[r] + part[N + r]) + ...) + part[(ks - 1) N + r], plus y[r] first when ADD. */
@@ -348,7 +364,7 @@ __global__ __launch_bounds__(KM_WG) void k_apply_corr_km(const glint_u32x4 *__re
     int cur = -1;
     auto flush = [&]() {
         float sc[32];
-        km_load32(scales_k + (int64_t)cur * N + rc, sc);
+        km_load<32>(scales_k + (int64_t)cur * N + rc, sc);
 #pragma unroll
         for (int j = 0; j < 32; ++j) {
             tot[j] = fmaf(acc[j], sc[j], tot[j]);
@@ -371,14 +387,14 @@ __global__ __launch_bounds__(KM_WG) void k_apply_corr_km(const glint_u32x4 *__re
             E[q] = glint_codes_even(Hs[q], Ps[q]);
             O[q] = glint_codes_odd(Hs[q], Ps[q]);
         }
-        km_lookup_fma(lds, E, O, lane4, xv, acc);
+        km_lookup_fma<32>(lds, E, O, lane4, xv, acc);
     }
     if (cur >= 0)
         flush();
     if (ks > 1)
-        km_combine_parts<false>(lds, tot, r0, N, part + (int64_t)blockIdx.y * N + r0);
+        km_combine_parts<false, 32>(lds, tot, r0, N, part + (int64_t)blockIdx.y * N + r0);
     else
-        km_combine_parts<true>(lds, tot, r0, N, y + r0);
+        km_combine_parts<true, 32>(lds, tot, r0, N, y + r0);
 }
 
 /* -------------------------------------------------------------------- C ABI */
@@ -406,8 +422,8 @@ GLINT_API int glint_gemv_km_fold(const uint8_t *hole_k, const float *scales_k, c
     if (N < 32 || (N % 32) != 0 || ksg < 1 || K < 64 || (K % (64 * ksg)) != 0 || !glint_aligned(hole_k, 16) ||
         !glint_aligned(scales_k, 16) || !glint_aligned(x, 16))
         return -2;
-    const dim3 grid((N + KM_ROWS - 1) / KM_ROWS, ksg);
-    k_gemv_km_fold<<<grid, KM_WG, 0, stream>>>((const glint_u32x4 *)hole_k, scales_k, x, ksg > 1 ? part : y, N, K / ksg);
+    const dim3 grid((N + 64 * KM_FOLD_RPL - 1) / (64 * KM_FOLD_RPL), ksg);
+    k_gemv_km_fold<KM_FOLD_RPL><<<grid, KM_WG, 0, stream>>>(hole_k, scales_k, x, ksg > 1 ? part : y, N, K / ksg);
     if (ksg > 1)
         k_km_combine<false><<<(N + KM_T - 1) / KM_T, KM_T, 0, stream>>>(part, y, N, ksg);
     return km_launched();
