@@ -12,8 +12,9 @@
  *   the block scale is applied once per run of channels inside a 64-block.
  * k_select_topk — one workgroup: keys in LDS, 15 bisection steps of a block count, then
  *   a block scan that writes the kept channels in ascending order.
- * k_apply_corr_km — the fold kernel's mapping over the selected list (count read on the
- *   device), with the 256-entry delta table (CELLS - PARENT) in 64 lane copies.
+ * k_apply_corr_km — the fold kernel's mapping (KM_CORR_RPL = 8 rows per lane) over the
+ *   selected list (count read on the device), with the 256-entry delta table
+ *   (CELLS - PARENT) in 64 lane copies.
  */
 #include <algorithm>
 #include <type_traits>
@@ -87,11 +88,13 @@ __global__ __launch_bounds__(KM_T) void k_kmajor_scales(const float *__restrict_
 
 /* ------------------------------------------------------------------ fold GEMV */
 #define KM_SUB 8                /* waves per workgroup = parts of a channel slice */
-#define KM_ROWS 2048            /* output rows per workgroup: 64 lanes x 32 rows */
 #define KM_WG (64 * KM_SUB)
 #define KM_U 4                  /* channels per batch (two batches in flight per wave) */
 #ifndef KM_FOLD_RPL
-#define KM_FOLD_RPL 8 /* fold: output rows per lane (8, 16 or 32); the correction uses 32 */
+#define KM_FOLD_RPL 8 /* fold: output rows per lane (8, 16 or 32) */
+#endif
+#ifndef KM_CORR_RPL
+#define KM_CORR_RPL 8 /* correction: output rows per lane (8, 16 or 32) */
 #endif
 
 __device__ __forceinline__ float km_bf16(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
@@ -335,14 +338,20 @@ __global__ __launch_bounds__(SEL_T) void k_select_topk(const uint16_t *__restric
  * so a block's channels are adjacent). Delta = CELLS - PARENT sits in LDS as 64 lane
  * copies, addressed by the code byte (h << 4 | p). One chunk adds into y; several write
  * part[by N + r] for k_km_combine<true>. */
-__global__ __launch_bounds__(KM_WG) void k_apply_corr_km(const glint_u32x4 *__restrict__ hole_k,
-                                                         const glint_u32x4 *__restrict__ plug_k,
+template <int RPL>
+__global__ __launch_bounds__(KM_WG) void k_apply_corr_km(const uint8_t *__restrict__ hole_bytes,
+                                                         const uint8_t *__restrict__ plug_bytes,
                                                          const float *__restrict__ scales_k,
                                                          const uint16_t *__restrict__ x, const int32_t *__restrict__ idx,
                                                          const int32_t *__restrict__ cnt, float *__restrict__ y,
                                                          float *__restrict__ part, int N, int ks) {
-    __shared__ __attribute__((aligned(16))) float lds[KM_SUB * KM_ROWS]; /* delta table, then parts */
-    static_assert(KM_SUB * KM_ROWS >= GLINT_LDS_CELLS64_WORDS, "delta table fits the part buffer");
+    constexpr int ROWS = 64 * RPL, NW = RPL / 8; /* rows per workgroup, code words per lane */
+    using HV = typename std::conditional<RPL == 32, glint_u32x4,
+                                         typename std::conditional<RPL == 16, glint_u32x2, uint32_t>::type>::type;
+    static_assert(RPL == 8 || RPL == 16 || RPL == 32, "rows per lane");
+    const HV *__restrict__ hole_k = (const HV *)hole_bytes, *__restrict__ plug_k = (const HV *)plug_bytes;
+    constexpr int LDSW = KM_SUB * ROWS > GLINT_LDS_CELLS64_WORDS ? KM_SUB * ROWS : GLINT_LDS_CELLS64_WORDS;
+    __shared__ __attribute__((aligned(16))) float lds[LDSW]; /* delta table, then parts */
     for (int i = threadIdx.x; i < GLINT_LDS_CELLS64_WORDS; i += KM_WG) {
         const int hp = i >> 6;
         lds[i] = (&kCells[0][0])[hp] - kParent[hp >> 4];
@@ -350,51 +359,53 @@ __global__ __launch_bounds__(KM_WG) void k_apply_corr_km(const glint_u32x4 *__re
     __syncthreads();
     const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lane4 = (uint32_t)lane * 4u;
-    const int r0 = blockIdx.x * KM_ROWS;
-    const int rc = min(r0 + 32 * lane, N - 32);
-    const int64_t rowv = N / 32;
+    const int r0 = blockIdx.x * ROWS;
+    const int rc = min(r0 + RPL * lane, N - RPL);
+    const int64_t rowv = N / RPL;
     const int cn = cnt[0];
     const int chunk = (cn + ks - 1) / ks, sub = (chunk + KM_SUB - 1) / KM_SUB;
     const int lo = blockIdx.y * chunk, hi = min(lo + chunk, cn);
     const int i0 = min(lo + q * sub, hi), i1 = min(i0 + sub, hi);
-    float tot[32], acc[32];
+    float tot[RPL], acc[RPL];
 #pragma unroll
-    for (int j = 0; j < 32; ++j)
+    for (int j = 0; j < RPL; ++j)
         tot[j] = acc[j] = 0.f;
     int cur = -1;
     auto flush = [&]() {
-        float sc[32];
-        km_load<32>(scales_k + (int64_t)cur * N + rc, sc);
+        float sc[RPL];
+        km_load<RPL>(scales_k + (int64_t)cur * N + rc, sc);
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
+        for (int j = 0; j < RPL; ++j) {
             tot[j] = fmaf(acc[j], sc[j], tot[j]);
             acc[j] = 0.f;
         }
     };
     for (int i = i0; i < i1; ++i) {
         const int c = idx[i];
-        const glint_u32x4 hv = hole_k[(int64_t)c * rowv + rc / 32], pv = plug_k[(int64_t)c * rowv + rc / 32];
+        const HV hv = hole_k[(int64_t)c * rowv + rc / RPL], pv = plug_k[(int64_t)c * rowv + rc / RPL];
         if ((c >> 6) != cur) {
             if (cur >= 0)
                 flush();
             cur = c >> 6;
         }
         const float xv = km_bf16(x[c]);
-        const uint32_t Hs[4] = {hv.x, hv.y, hv.z, hv.w}, Ps[4] = {pv.x, pv.y, pv.z, pv.w};
-        uint32_t E[4], O[4];
+        uint32_t Hs[NW], Ps[NW];
+        __builtin_memcpy(Hs, &hv, sizeof(Hs));
+        __builtin_memcpy(Ps, &pv, sizeof(Ps));
+        uint32_t E[NW], O[NW];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < NW; ++q) {
             E[q] = glint_codes_even(Hs[q], Ps[q]);
             O[q] = glint_codes_odd(Hs[q], Ps[q]);
         }
-        km_lookup_fma<32>(lds, E, O, lane4, xv, acc);
+        km_lookup_fma<RPL>(lds, E, O, lane4, xv, acc);
     }
     if (cur >= 0)
         flush();
     if (ks > 1)
-        km_combine_parts<false, 32>(lds, tot, r0, N, part + (int64_t)blockIdx.y * N + r0);
+        km_combine_parts<false, RPL>(lds, tot, r0, N, part + (int64_t)blockIdx.y * N + r0);
     else
-        km_combine_parts<true, 32>(lds, tot, r0, N, y + r0);
+        km_combine_parts<true, RPL>(lds, tot, r0, N, y + r0);
 }
 
 /* -------------------------------------------------------------------- C ABI */
@@ -446,9 +457,8 @@ GLINT_API int glint_apply_corr_km(const uint8_t *hole_k, const uint8_t *plug_k, 
     if (N < 32 || (N % 32) != 0 || K < 64 || (K % 64) != 0 || ks < 1 || !glint_aligned(hole_k, 16) ||
         !glint_aligned(plug_k, 16) || !glint_aligned(scales_k, 16))
         return -2;
-    const dim3 grid((N + KM_ROWS - 1) / KM_ROWS, ks);
-    k_apply_corr_km<<<grid, KM_WG, 0, stream>>>((const glint_u32x4 *)hole_k, (const glint_u32x4 *)plug_k, scales_k, x,
-                                                idx, cnt, y, part, N, ks);
+    const dim3 grid((N + 64 * KM_CORR_RPL - 1) / (64 * KM_CORR_RPL), ks);
+    k_apply_corr_km<KM_CORR_RPL><<<grid, KM_WG, 0, stream>>>(hole_k, plug_k, scales_k, x, idx, cnt, y, part, N, ks);
     if (ks > 1)
         k_km_combine<true><<<(N + KM_T - 1) / KM_T, KM_T, 0, stream>>>(part, y, N, ks);
     return km_launched();
