@@ -10,8 +10,9 @@
  *   workgroup's channel slice (grid.y) and meet in LDS. Per element: one v_perm for the
  *   address, one lookup in the 64-copy PARENT table, one FMA by the wave-uniform x[c];
  *   the block scale is applied once per run of channels inside a 64-block.
- * k_select_topk — one workgroup: keys in LDS, 15 bisection steps of a block count, then
- *   a block scan that writes the kept channels in ascending order.
+ * k_select_topk — one workgroup: keys in LDS, the threshold by a two-level radix select
+ *   (LDS histograms of the top 8 and low 7 key bits), then a block scan that writes the
+ *   kept channels in ascending order.
  * k_apply_corr_km — the fold kernel's mapping (KM_CORR_RPL = 8 rows per lane) over the
  *   selected list (count read on the device), with the 256-entry delta table
  *   (CELLS - PARENT) in 64 lane copies.
@@ -268,42 +269,84 @@ __global__ __launch_bounds__(KM_T) void k_km_combine(const float *__restrict__ p
 #define SEL_T 1024
 #define SEL_MAX_K 32768
 
-__device__ __forceinline__ int sel_block_sum(int v, int *wsum) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-        v += __shfl_xor(v, o, 64);
-    if ((threadIdx.x & 63) == 0)
-        wsum[threadIdx.x >> 6] = v;
-    __syncthreads();
-    int total = 0;
-#pragma unroll
-    for (int i = 0; i < SEL_T / 64; ++i)
-        total += wsum[i];
-    __syncthreads();
-    return total;
-}
-
+/* T = the largest 15-bit key value with count(key >= T) >= nsel, found as the radix select
+ * of two histograms: 256 bins of key >> 7, then 128 bins of key & 127 inside the chosen
+ * bin. That is the same T the bit-by-bit bisection of the rule gives (the count is
+ * non-increasing in T). nsel == 0 keeps nothing; nsel above K keeps everything. Then the
+ * kept channels are written in ascending order through a block scan. */
 __global__ __launch_bounds__(SEL_T) void k_select_topk(const uint16_t *__restrict__ x, int K, int nsel,
                                                        int32_t *__restrict__ idx, int32_t *__restrict__ cnt) {
     __shared__ uint16_t keys[SEL_MAX_K];
+    __shared__ int hc[256], hf[128]; /* coarse and fine histograms */
     __shared__ int wsum[SEL_T / 64];
-    const int t = threadIdx.x;
-    for (int i = t; i < K; i += SEL_T)
-        keys[i] = x[i] & 0x7FFF;
+    __shared__ int s_bin, s_above, s_thr;
+    const int t = threadIdx.x, lane = t & 63;
+    if (t < 256)
+        hc[t] = 0;
+    if (t < 128)
+        hf[t] = 0;
+    if (t == 0) {
+        s_bin = -1;
+        s_above = 0;
+        s_thr = nsel == 0 ? 32768 : 0; /* kept when no bin qualifies: nothing, or everything */
+    }
     __syncthreads();
+    for (int i = t; i < K; i += SEL_T) {
+        const int k = x[i] & 0x7FFF;
+        keys[i] = (uint16_t)k;
+        atomicAdd(&hc[k >> 7], 1);
+    }
+    __syncthreads();
+    if (t < 64 && nsel > 0) { /* lane l: coarse bins 4 l .. 4 l + 3; suffix counts */
+        const int v0 = hc[4 * lane], v1 = hc[4 * lane + 1], v2 = hc[4 * lane + 2], v3 = hc[4 * lane + 3];
+        const int sum = v0 + v1 + v2 + v3;
+        int inc = sum; /* sum over lanes lane .. 63 */
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_down(inc, o, 64);
+            if (lane + o < 64)
+                inc += v;
+        }
+        const int c4 = inc - sum, c3 = c4 + v3, c2 = c3 + v2, c1 = c2 + v1, c0 = c1 + v0; /* c_j = count(bin >= 4 l + j) */
+        const int cs[5] = {c0, c1, c2, c3, c4};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (cs[j] >= nsel && cs[j + 1] < nsel) { /* exactly one bin, when count(all) >= nsel */
+                s_bin = 4 * lane + j;
+                s_above = cs[j + 1];
+            }
+    }
+    __syncthreads();
+    const int bin = s_bin;
+    if (bin >= 0) {
+        for (int i = t; i < K; i += SEL_T) {
+            const int k = keys[i];
+            if ((k >> 7) == bin)
+                atomicAdd(&hf[k & 127], 1);
+        }
+        __syncthreads();
+        if (t < 64) { /* lane l: fine bins 2 l, 2 l + 1 */
+            const int need = nsel - s_above;
+            const int v0 = hf[2 * lane], v1 = hf[2 * lane + 1];
+            const int sum = v0 + v1;
+            int inc = sum;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int v = __shfl_down(inc, o, 64);
+                if (lane + o < 64)
+                    inc += v;
+            }
+            const int c2 = inc - sum, c1 = c2 + v1, c0 = c1 + v0;
+            if (c0 >= need && c1 < need)
+                s_thr = (bin << 7) | (2 * lane);
+            if (c1 >= need && c2 < need)
+                s_thr = (bin << 7) | (2 * lane + 1);
+        }
+        __syncthreads();
+    }
+    const int thr = s_thr;
     const int per = (K + SEL_T - 1) / SEL_T;
     const int lo = min(t * per, K), hi = min(lo + per, K);
-    int thr = 0;
-    for (int bi = 0; bi < 15; ++bi) {
-        const int cand = thr | (1 << (14 - bi));
-        int c = 0;
-        for (int i = lo; i < hi; ++i)
-            c += keys[i] >= cand;
-        if (sel_block_sum(c, wsum) >= nsel)
-            thr = cand;
-    }
-    if (nsel == 0)
-        thr = 32768;
     int mine = 0;
     for (int i = lo; i < hi; ++i)
         mine += keys[i] >= thr;
@@ -312,10 +355,10 @@ __global__ __launch_bounds__(SEL_T) void k_select_topk(const uint16_t *__restric
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
         const int v = __shfl_up(inc, o, 64);
-        if ((t & 63) >= o)
+        if (lane >= o)
             inc += v;
     }
-    if ((t & 63) == 63)
+    if (lane == 63)
         wsum[t >> 6] = inc;
     __syncthreads();
     int base = 0, total = 0;
