@@ -395,9 +395,11 @@ __global__ __launch_bounds__(KM_WG) void k_apply_corr_km(const uint8_t *__restri
     const HV *__restrict__ hole_k = (const HV *)hole_bytes, *__restrict__ plug_k = (const HV *)plug_bytes;
     constexpr int LDSW = KM_SUB * ROWS > GLINT_LDS_CELLS64_WORDS ? KM_SUB * ROWS : GLINT_LDS_CELLS64_WORDS;
     __shared__ __attribute__((aligned(16))) float lds[LDSW]; /* delta table, then parts */
-    for (int i = threadIdx.x; i < GLINT_LDS_CELLS64_WORDS; i += KM_WG) {
-        const int hp = i >> 6;
-        lds[i] = (&kCells[0][0])[hp] - kParent[hp >> 4];
+    /* 4 adjacent copies of an entry per 16-B store: entry hp = word / 64 */
+    for (int i = threadIdx.x; i < GLINT_LDS_CELLS64_WORDS / 4; i += KM_WG) {
+        const int hp = i >> 4;
+        const float d = (&kCells[0][0])[hp] - kParent[hp >> 4];
+        *(glint_f32x4 *)(lds + 4 * i) = glint_f32x4{d, d, d, d};
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
