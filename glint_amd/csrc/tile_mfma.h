@@ -443,8 +443,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
  * s + 1 while s is multiplied); x keeps the per-step ring (RX stages) and double buffer
  * of k_tile_mfma. Block tile BM x 64 over 2 x 2 waves (BM = 64 or 128); W rows 8 w +
  * lane / 8 and 32 more (wave w), piece lane % 8. Clamping and split K as in k_tile_mfma. */
+/* BM = 64 without a producer table: at most 256 VGPRs (two waves per SIMD), so two
+ * workgroups fit a CU when the split plan asks for them */
 template <int BM, int RX, class P, class Out>
-__global__ __launch_bounds__(256) void k_tile_ss(P p, const uint16_t *__restrict__ x, typename Out::T *__restrict__ y,
+__global__ __launch_bounds__(256, (BM == 64 && P::LDS_WORDS == 0) ? 2 : 1) void k_tile_ss(P p, const uint16_t *__restrict__ x, typename Out::T *__restrict__ y,
                                                  int M, int N, int K, int kps, float *__restrict__ part,
                                                  unsigned *ctr) {
     constexpr int T = 256, BN = 64, WN = 2, TM = BM / 32, TN = 2, XV = BM * 8 / T;
@@ -831,9 +833,9 @@ static inline int glint_split_kps(int64_t tiles, int64_t slots, int nK, int min_
  * workgroup per CU measured slower: they contend for the LDS). Sets kps and ks and binds the
  * stream's workspace; without one (capture) it runs unsplit. */
 static inline void tile_split_plan(hipStream_t st, unsigned gx, unsigned gy, int nS, size_t tile_floats, int &kps,
-                                   int &ks, GlintSplitWs &ws) {
+                                   int &ks, GlintSplitWs &ws, int per_cu = 1) {
     const int64_t tiles = (int64_t)gx * gy;
-    kps = glint_split_kps(tiles, glint_cu_count(), nS, TILE_SPLIT_MIN_STEPS);
+    kps = glint_split_kps(tiles, (int64_t)per_cu * glint_cu_count(), nS, TILE_SPLIT_MIN_STEPS);
     ks = (nS + kps - 1) / kps;
     ws = GlintSplitWs{nullptr, nullptr};
     if (ks > 1 && !glint_split_ws(st, (size_t)ks * tiles * tile_floats, (size_t)tiles, ws)) {
@@ -878,11 +880,12 @@ static void tile_big_launch(const P &p, const uint16_t *x, typename Out::T *y, i
 
 /* Launch k_tile_ss over an M x N output. K % 64 == 0, M, N >= 1. */
 template <int BM, int RX, class P, class Out>
-static void tile_ss_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st) {
+static void tile_ss_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st,
+                           int per_cu = 1) {
     const unsigned gx = (unsigned)((N + 63) / 64), gy = (unsigned)((M + BM - 1) / BM);
     int kps, ks;
     GlintSplitWs ws;
-    tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * 64, kps, ks, ws);
+    tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * 64, kps, ks, ws, per_cu);
     k_tile_ss<BM, RX, P, Out><<<dim3(gx, gy, (unsigned)ks), 256, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
 }
 
