@@ -212,6 +212,9 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #ifndef GEMV_X_EL
 #define GEMV_X_EL 32 /* elements per lane per row: 32 (16-B plane loads) or 16 (8-B) */
 #endif
+#ifndef GEMV_G1_DIV
+#define GEMV_G1_DIV 2 /* one row group per workgroup (k_in > 4096): launch the resident grid / this */
+#endif
 #ifndef GEMV_X_DEPTH
 #define GEMV_X_DEPTH 2 /* rows of loads in flight per wave (3 and 4 measured 2% and 12% slower) */
 #endif
@@ -532,7 +535,8 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         /* K / 8 chunks of x over 64 S G threads: 4 / G per thread */
         auto kern = G >= 4 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 1>
                            : (G >= 2 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 2> : k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 0>);
-        const int64_t resident = glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4);
+        const int64_t resident =
+            std::max<int64_t>(glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4) / (G == 1 ? GEMV_G1_DIV : 1), 1);
         const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
         int64_t rows_per_wg = G * per_wave;
         const int64_t cap = (GEMV_X_RED_MAX / (S * 4)) / G * G;
