@@ -7,6 +7,7 @@ Outputs (git-ignored, shipped with the tree):
     glint_amd/lib/libglint_encode.so   encode / expand / H-TILE (include/glint_encode.h, glint_htile.h)
     glint_amd/lib/libp7_kernels.so     attach ABI: INT8 GEMM (include/int8_mma_gemm.h, p7_attach.h)
     oracle/liboracle.so                CPU oracle (tests only)
+    tests/native/bin/abi_caller        C++ caller of the C ABI, linked with -lglint_encode (tests only)
 """
 from __future__ import annotations
 
@@ -83,6 +84,21 @@ def build_libs() -> None:
         os.replace(tmp, out)
 
 
+NATIVE = ROOT / "tests" / "native"
+
+
+def build_native_tests() -> None:
+    """The C++ ABI caller: compiled against include/*.h only and linked with
+    -lglint_encode (rpath to glint_amd/lib), as a reference C/C++ test links the library."""
+    out = NATIVE / "bin"
+    out.mkdir(exist_ok=True)
+    exe = out / "abi_caller"
+    tmp = out / "abi_caller.tmp"
+    _run([HIPCC, "-O2", "-std=c++17", f"-I{ROOT / 'include'}", str(NATIVE / "abi_caller.cpp"),
+          f"-L{LIB}", "-lglint_encode", "-Wl,-rpath,$ORIGIN/../../../glint_amd/lib", "-o", str(tmp)])
+    os.replace(tmp, exe)
+
+
 def build_oracle() -> None:
     _run(["make", "-C", str(ROOT / "oracle"), "-j4"])
     if Path("/root/reference").is_dir():
@@ -92,6 +108,7 @@ def build_oracle() -> None:
 def build(only_libs: bool = False) -> None:
     gen_code_table()
     build_libs()
+    build_native_tests()
     if not only_libs:
         build_oracle()
 

@@ -213,7 +213,7 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #define GEMV_X_EL 32 /* elements per lane per row: 32 (16-B plane loads) or 16 (8-B) */
 #endif
 #ifndef GEMV_G1_DIV
-#define GEMV_G1_DIV 2 /* one row group per workgroup (k_in > 4096): launch the resident grid / this */
+#define GEMV_G1_DIV 2 /* one row group per workgroup (G == 1: S = K / 2048 >= 5, K >= 10240): resident grid / this */
 #endif
 #ifndef GEMV_X_DEPTH
 #define GEMV_X_DEPTH 2 /* rows of loads in flight per wave (3 and 4 measured 2% and 12% slower) */
@@ -504,9 +504,18 @@ static unsigned gemv_grid(const void *kern, int threads, size_t lds, int64_t tas
     return (unsigned)(needed < resident ? needed : resident);
 }
 
+/* f32 output at M > 1 (the reference ABI's prefill use): 3-plane k_tile_mfma, whose
+ * products are exact and whose sums are f32. 128 x 128 tiles over 8 waves (2 x 4, wave tile
+ * 64 x 32) fill the 160 KiB of LDS: x 32 KiB, three W planes 96 KiB, cell table 32 KiB;
+ * below 128 rows 64 x 128 tiles (8 waves in a row, wave tile 64 x 16). */
+#define F32_TILE_MIN_M 128
+
+/* `fixed`: the caller's split-K workspace (the no-allocation entry point); null for the
+ * stream's own. Returns 0, -1 null pointer, -2 bs <= 0 or K < 1, -3 launch error, -5 the
+ * split plan needs more than the fixed workspace holds. */
 template <bool OUT_BF16>
 static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y, int M,
-                        int N, int K, int bs, hipStream_t st) {
+                        int N, int K, int bs, hipStream_t st, const GlintSplitWs *fixed = nullptr) {
     if (!hole || !plug || !absmax || !x || !y)
         return -1;
     if (bs <= 0 || K < 1)
@@ -516,20 +525,34 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
     const bool gemv_ok = M == 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
                          glint_aligned(absmax, 4) && glint_aligned(x, 16) &&
                          K <= GEMV_MAX_K;
-    const bool mfma_ok = OUT_BF16 && M > 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) &&
-                         glint_aligned(plug, 16) && glint_aligned(absmax, 4) && glint_aligned(x, 16);
-    if (mfma_ok) {
+    const bool mfma_ok = M > 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
+                         glint_aligned(absmax, 4) && glint_aligned(x, 16);
+    if (mfma_ok && OUT_BF16) {
         const GlintTileProducer p{(const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, N, K, nullptr};
         const uint16_t *xb = (const uint16_t *)x;
         uint16_t *yb = (uint16_t *)y;
+        bool planned;
         if (M <= 64)
-            tile_ss_launch<64, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
+            planned = tile_ss_launch<64, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 1, fixed);
         else if (M < MF2_MIN_M)
-            tile_ss_launch<128, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
+            planned = tile_ss_launch<128, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 1, fixed);
         else if (TILE_BIG && tile_big_fits(M, N, K) && tile_big_pays(M, N))
-            tile_big_launch<TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
+            planned = tile_big_launch<TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, fixed);
         else
-            tile_mfma_launch<MF2_BM, MF2_BN, 4, 2, TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st);
+            planned = tile_mfma_launch<MF2_BM, MF2_BN, 4, 2, TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N,
+                                                                                                       K, st, fixed);
+        if (!planned)
+            return -5;
+    } else if (mfma_ok) {
+        const GlintTileProducer p{(const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, N, K, nullptr};
+        const uint16_t *xb = (const uint16_t *)x;
+        float *yf = (float *)y;
+        const bool planned =
+            M < F32_TILE_MIN_M
+                ? tile_mfma_launch<64, 128, 1, 8, 2, GlintTileProducer, TileOutF32, 3>(p, xb, yf, M, N, K, st, fixed)
+                : tile_mfma_launch<128, 128, 2, 4, 2, GlintTileProducer, TileOutF32, 3>(p, xb, yf, M, N, K, st, fixed);
+        if (!planned)
+            return -5;
     } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS / 64) {
         const int S = K / (64 * GEMV_X_EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
         /* K / 8 chunks of x over 64 S G threads: 4 / G per thread */
@@ -592,4 +615,19 @@ GLINT_API int launch_glint_htile_bf16_stream(const uint8_t *d_hole, const uint8_
                                              const void *d_x, uint16_t *d_y, int M, int N, int K, int bs,
                                              struct ihipStream_t *stream) {
     return htile_launch<true>(d_hole, d_plug, d_absmax, d_x, d_y, M, N, K, bs, (hipStream_t)stream);
+}
+
+GLINT_API int glint_htile_workspace_reserve(struct ihipStream_t *stream) {
+    GlintSplitWs ws;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+        return -1;
+    return glint_split_ws_stream((hipStream_t)stream, ws) ? 0 : -1;
+}
+
+/* Library-internal (not exported): the BF16-out launch with the caller's split-K
+ * workspace in place of the stream's own. Used by the no-allocation entry point. */
+int glint_htile_bf16_launch_ws(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax, const void *d_x,
+                               uint16_t *d_y, int M, int N, int K, int bs, hipStream_t st, const GlintSplitWs *ws) {
+    return htile_launch<true>(d_hole, d_plug, d_absmax, d_x, d_y, M, N, K, bs, st, ws);
 }

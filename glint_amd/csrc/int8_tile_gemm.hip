@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
 #endif
 #define I8V_RED_MAX 8192 /* floats of row partials a workgroup may park in LDS */
 #ifndef I8V_GRID_DIV
-#define I8V_GRID_DIV 2 /* m = 1, k_in > 4096: launch the resident grid / this */
+#define I8V_GRID_DIV 2 /* m = 1, one row group per workgroup (k_in >= 10240): launch the resident grid / this */
 #endif
 
 struct I8Row {
@@ -232,9 +232,11 @@ static void i8tile_launch_gemv(const uint16_t *x, const Int8PinLinear &w, float 
     /* 4 rows in flight measured 14% faster at m = 1, k_in = 4096 (14.6 against 17.0 us on
      * 14336 x 4096) and 2-5% slower at k_in = 14336 or m = 4 */
     auto kern = (MR == 1 && S <= 2) ? k_i8tile_gemv<MR, I8V_DEPTH_M1> : k_i8tile_gemv<MR, I8V_DEPTH>;
-    /* m = 1 with k_in > 4096: half the resident grid (twice the rows per wave) measured
-     * 16.5 -> 15.4 us on 4096 x 14336; at k_in = 4096 or m = 4 it was slower */
-    const int div = (MR == 1 && S > 2) ? I8V_GRID_DIV : 1;
+    /* m = 1 with one row group per workgroup (G == 1: S = k_in / 2048 >= 5, k_in >= 10240):
+     * half the resident grid (twice the rows per wave) measured 16.5 -> 15.4 us on
+     * 4096 x 14336; at k_in = 4096 or m = 4 it was slower, and k_in = 6144 / 8192 (G = 2)
+     * were not measured, so they keep the full grid */
+    const int div = (MR == 1 && G == 1) ? I8V_GRID_DIV : 1;
     const int64_t resident =
         std::max<int64_t>(glint_resident_grid((const void *)kern, threads, I8V_RED_MAX * 4) / div, 1);
     const int64_t per_wave = ((int64_t)w.n_out + G * resident - 1) / (G * resident);

@@ -126,6 +126,33 @@ struct GlintTileProducer {
         for (int i = 0; i < 8; ++i)
             packed[i] = glint_cvt_bf16x2(v[2 * i] * r.a, v[2 * i + 1] * r.a);
     }
+    /* The f32 weights w = CELLS * absmax (the reference's f32 product) as three BF16 planes
+     * with w == hi + mid + lo exactly: hi keeps w's top 16 bits, mid the top 16 bits of the
+     * exact remainder w - hi, and lo = w - hi - mid, which has at most 8 significant bits
+     * (w has 24), so it is a BF16 value as it stands. A product x * plane is then exact in
+     * the MFMA and y differs from the f32 sum of w * x only by the accumulation. An infinite
+     * w (absmax inf, or an f32 overflow of CELLS * absmax) keeps mid = lo = 0, where w - hi
+     * would be NaN; a NaN w stays NaN in hi (its quiet bit is in the top half). */
+    __device__ __forceinline__ void finish_split(const Regs &r, const float (&v)[16], uint32_t (&packed)[3][8]) const {
+        const bool big = !(__builtin_fabsf(r.a) < 0x1p126f); /* only there can w be infinite */
+        float hi[16], mid[16], lo[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float w = v[i] * r.a;
+            hi[i] = __uint_as_float(__float_as_uint(w) & 0xFFFF0000u);
+            float r1 = w - hi[i];
+            if (big)
+                r1 = __builtin_isinf(w) ? 0.0f : r1;
+            mid[i] = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
+            lo[i] = r1 - mid[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            packed[0][i] = __builtin_amdgcn_perm(__float_as_uint(hi[2 * i + 1]), __float_as_uint(hi[2 * i]), 0x07060302u);
+            packed[1][i] = __builtin_amdgcn_perm(__float_as_uint(mid[2 * i + 1]), __float_as_uint(mid[2 * i]), 0x07060302u);
+            packed[2][i] = __builtin_amdgcn_perm(__float_as_uint(lo[2 * i + 1]), __float_as_uint(lo[2 * i]), 0x07060302u);
+        }
+    }
 
     /* Super-step interface (k_tile_ss): piece c (0..7) of a row's super-step (4 K steps, 256
      * elements) is elements [32 c, +32): 16 B of each plane and one absmax. Its groups h = 0, 1
@@ -284,7 +311,10 @@ __device__ __forceinline__ bool tile_splitk_epilogue(glint_f32x4 (&acc)[NA][NB],
     return true;
 }
 
-template <int BM, int BN, int WM, int WN, int R, class P, class Out>
+/* NP = 1: W is one BF16 plane (the BF16-out GEMMs). NP = 3: the producer's finish_split
+ * makes three BF16 planes whose sum is the f32 weight exactly, and every x fragment is
+ * multiplied with all three (the f32-out H-TILE: f32 products, f32 accumulation). */
+template <int BM, int BN, int WM, int WN, int R, class P, class Out, int NP = 1>
 __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t *__restrict__ x,
                                                              typename Out::T *__restrict__ y, int M, int N, int K,
                                                              int kps, float *__restrict__ part, unsigned *ctr) {
@@ -296,9 +326,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
     static_assert(BN * 4 == T, "each thread produces a quarter of one W row");
     static_assert(XV * T == BM * 8 && TM * WM * 16 == BM && TN * WN * 16 == BN, "tile shape");
     static_assert(R >= 2 && R <= 8, "register stages");
+    static_assert(NP == 1 || NP == 3, "W planes");
     __shared__ float ptab[P::LDS_WORDS > 0 ? P::LDS_WORDS : 1];
     __shared__ __attribute__((aligned(16))) uint16_t sX[2][BM * TILE_LDW];
-    __shared__ __attribute__((aligned(16))) uint16_t sW[2][BN * TILE_LDW];
+    __shared__ __attribute__((aligned(16))) uint16_t sW[2][NP][BN * TILE_LDW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -333,10 +364,18 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
         }
     };
     auto store = [&](int buf, const Stage &sg, const float (&v)[16]) {
-        uint32_t packed[8];
-        p.finish(sg.w, v, packed);
-        *(glint_u32x4 *)(sW[buf] + tile_ofs(wr, 2 * wq)) = glint_u32x4{packed[0], packed[1], packed[2], packed[3]};
-        *(glint_u32x4 *)(sW[buf] + tile_ofs(wr, 2 * wq + 1)) = glint_u32x4{packed[4], packed[5], packed[6], packed[7]};
+        uint32_t packed[NP][8];
+        if constexpr (NP == 1)
+            p.finish(sg.w, v, packed[0]);
+        else
+            p.finish_split(sg.w, v, packed);
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) {
+            *(glint_u32x4 *)(sW[buf][pl] + tile_ofs(wr, 2 * wq)) =
+                glint_u32x4{packed[pl][0], packed[pl][1], packed[pl][2], packed[pl][3]};
+            *(glint_u32x4 *)(sW[buf][pl] + tile_ofs(wr, 2 * wq + 1)) =
+                glint_u32x4{packed[pl][4], packed[pl][5], packed[pl][6], packed[pl][7]};
+        }
 #pragma unroll
         for (int i = 0; i < XV; ++i)
             *(glint_u32x4 *)(sX[buf] + tile_ofs(xr + (T / 8) * i, xc)) = sg.x[i];
@@ -347,7 +386,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
     auto step = [&](int j, int u) {
         const int cur = u & 1;
         Stage &nx = st[(u + 1) % R];
-        glint_bf16x8 af[2][TM], bfr[2][TN];
+        glint_bf16x8 af[2][TM], bfr[2][NP][TN];
         /* rows (16-row tile base) + lane % 16, chunk 4 ks + lane / 16; the swizzle does not
          * change when a row moves by a multiple of 16 */
         auto frags = [&](int ks) {
@@ -357,16 +396,22 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
                 af[ks][a] = __builtin_bit_cast(
                     glint_bf16x8, *(const glint_u32x4 *)(sX[cur] + (wm * TM * 16 + a * 16) * TILE_LDW + fofs));
 #pragma unroll
-            for (int b = 0; b < TN; ++b)
-                bfr[ks][b] = __builtin_bit_cast(
-                    glint_bf16x8, *(const glint_u32x4 *)(sW[cur] + (wn * TN * 16 + b * 16) * TILE_LDW + fofs));
-        };
-        auto mfmas = [&](int ks) {
-#pragma unroll
-            for (int a = 0; a < TM; ++a)
+            for (int pl = 0; pl < NP; ++pl)
 #pragma unroll
                 for (int b = 0; b < TN; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][a], bfr[ks][b], acc[a][b], 0, 0, 0);
+                    bfr[ks][pl][b] = __builtin_bit_cast(
+                        glint_bf16x8, *(const glint_u32x4 *)(sW[cur][pl] + (wn * TN * 16 + b * 16) * TILE_LDW + fofs));
+        };
+        /* planes outermost: consecutive MFMAs update different accumulators */
+        auto mfmas = [&](int ks) {
+#pragma unroll
+            for (int pl = 0; pl < NP; ++pl)
+#pragma unroll
+                for (int a = 0; a < TM; ++a)
+#pragma unroll
+                    for (int b = 0; b < TN; ++b)
+                        acc[a][b] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks][a], bfr[ks][pl][b], acc[a][b], 0, 0, 0);
         };
         float v[16];
         if (TILE_INTERLEAVE) {
@@ -377,9 +422,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
             mfmas(0);
             frags(1);
 #pragma unroll
-            for (int i = 0; i < TM + TN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, (TM * TN) / (TM + TN), 0); /* MFMA */
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                     /* LDS read */
+            for (int i = 0; i < TM + NP * TN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, (NP * TM * TN) / (TM + NP * TN), 0); /* MFMA */
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                               /* LDS read */
             }
             __builtin_amdgcn_sched_barrier(0);
             mfmas(1);
@@ -769,52 +814,79 @@ __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restric
 #ifndef TILE_SPLIT_MIN_STEPS
 #define TILE_SPLIT_MIN_STEPS 8 /* fewest 64-wide K steps per split */
 #endif
+#include <thread>
 #include <unordered_map>
 
-/* Per (device, stream) split-K workspace: partial tiles plus arrival counters that are zero
- * between launches. Launches on one stream run in order, so they can share it; launches
- * on different streams get different ones. Growing it frees the old buffer (hipFree waits
- * for the device) and zeroes the new counters with a blocking hipMemset, so a stream
- * being captured into a graph cannot grow it: glint_split_ws then returns false and the
- * caller runs without splitting. */
+/* A split-K workspace: f32 partial tiles plus one arrival counter per output tile. The
+ * counters are zero between launches: the last workgroup of each tile clears its own, so
+ * a workspace stays valid as long as every launch that used it ran to completion.
+ * Capacity: a split plan has at most one partial tile per workgroup slot (tiles x splits
+ * <= 2 x CUs) and the largest split tile is 256 x 128 (32768 floats), so CUs x 32768
+ * floats and 2 x CUs counters always suffice; tile_split_plan checks the plan against the
+ * capacity and runs unsplit where it would not fit. */
 struct GlintSplitWs {
     float *part;
     unsigned *ctr;
+    size_t part_floats, nctr; /* capacities */
 };
-static inline bool glint_split_ws(hipStream_t st, size_t part_floats, size_t ntiles, GlintSplitWs &ws) {
+#define GLINT_SPLIT_TILE_FLOATS_MAX 32768
+static inline size_t glint_split_ctr_bytes(size_t nctr) { return (nctr * sizeof(unsigned) + 255) & ~(size_t)255; }
+
+/* Zero n counters on a stream (a kernel, not a memset node, so it is also safe to record
+ * into a graph). */
+static __global__ void k_glint_zero_u32(unsigned *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+/* The split-K workspace of a stream on the current device, allocated once at full
+ * capacity (hipMalloc; its counters zeroed by a kernel on `st`) and never grown or freed,
+ * so a pointer a graph captured stays valid. A launch that is being captured binds the
+ * stream's existing workspace and marks it as owned by the graph: the next eager launch on
+ * that stream allocates a fresh one, so graph replays and eager calls never share counters.
+ * A capture on a stream that has no workspace yet cannot allocate one (the launch then
+ * runs unsplit): make one eager call, or call the library's workspace reserve, first.
+ * hipStreamPerThread is keyed by host thread, since each thread's per-thread stream is a
+ * different queue behind the same handle. Returns false if no workspace can be had. */
+static inline bool glint_split_ws_stream(hipStream_t st, GlintSplitWs &ws) {
     struct Entry {
         char *base;
-        size_t part_floats, ntiles;
+        bool captured;
     };
     static std::mutex mu;
     static std::unordered_map<uint64_t, Entry> cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess)
         return false;
-    const uint64_t key = (uint64_t)(uintptr_t)st * 64u + (uint64_t)dev;
+    uint64_t key = (uint64_t)(uintptr_t)st;
+    if (st == hipStreamPerThread)
+        key = (uint64_t)std::hash<std::thread::id>{}(std::this_thread::get_id()) | 1u; /* handles are even */
+    key = key * 131u + (uint64_t)dev;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess)
+        return false;
+    const size_t cus = (size_t)glint_cu_count();
+    const size_t nctr = 2 * cus, part_floats = cus * GLINT_SPLIT_TILE_FLOATS_MAX;
+    const size_t cb = glint_split_ctr_bytes(nctr);
     std::lock_guard<std::mutex> lock(mu);
     Entry &e = cache[key];
-    if (e.base == nullptr || e.part_floats < part_floats || e.ntiles < ntiles) {
-        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+    if (cap != hipStreamCaptureStatusNone) {
+        if (e.base == nullptr)
             return false;
-        const size_t pf = std::max(part_floats, e.part_floats), nt = std::max(ntiles, e.ntiles);
-        const size_t ctr_bytes = (nt * sizeof(unsigned) + 255) & ~(size_t)255;
-        if (e.base != nullptr && (hipStreamSynchronize(st) != hipSuccess || hipFree(e.base) != hipSuccess))
-            return false;
-        e = Entry{nullptr, 0, 0};
+        e.captured = true;
+    } else if (e.base == nullptr || e.captured) {
+        /* a captured workspace stays allocated: the graph that bound it may be replayed */
         char *b = nullptr;
-        if (hipMalloc((void **)&b, ctr_bytes + pf * sizeof(float)) != hipSuccess)
+        if (hipMalloc((void **)&b, cb + part_floats * sizeof(float)) != hipSuccess)
             return false;
-        if (hipMemset(b, 0, ctr_bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
-            (void)hipFree(b);
+        k_glint_zero_u32<<<1, 256, 0, st>>>((unsigned *)b, cb / sizeof(unsigned));
+        if (hipGetLastError() != hipSuccess) {
+            (void)hipFree(b); /* nothing was enqueued on it */
             return false;
         }
-        e = Entry{b, pf, nt};
+        e = Entry{b, false};
     }
-    const size_t ctr_bytes = (e.ntiles * sizeof(unsigned) + 255) & ~(size_t)255;
-    ws.ctr = (unsigned *)e.base;
-    ws.part = (float *)(e.base + ctr_bytes);
+    ws = GlintSplitWs{(float *)(e.base + cb), (unsigned *)e.base, part_floats, nctr};
     return true;
 }
 
@@ -830,29 +902,46 @@ static inline int glint_split_kps(int64_t tiles, int64_t slots, int nK, int min_
 }
 
 /* Split plan for a gx x gy tile grid over nS K steps: fills the CUs once (a second resident
- * workgroup per CU measured slower: they contend for the LDS). Sets kps and ks and binds the
- * stream's workspace; without one (capture) it runs unsplit. */
-static inline void tile_split_plan(hipStream_t st, unsigned gx, unsigned gy, int nS, size_t tile_floats, int &kps,
-                                   int &ks, GlintSplitWs &ws, int per_cu = 1) {
+ * workgroup per CU measured slower: they contend for the LDS). Sets kps and ks and the
+ * workspace: the caller's `fixed` one if given, else the stream's. A split that does not
+ * fit the workspace, or a stream without one (capture), runs unsplit; with a `fixed`
+ * workspace that is too small the plan is refused instead (returns false), so the caller
+ * can report it. */
+static inline bool tile_split_plan(hipStream_t st, unsigned gx, unsigned gy, int nS, size_t tile_floats, int &kps,
+                                   int &ks, GlintSplitWs &ws, int per_cu = 1, const GlintSplitWs *fixed = nullptr) {
     const int64_t tiles = (int64_t)gx * gy;
     kps = glint_split_kps(tiles, (int64_t)per_cu * glint_cu_count(), nS, TILE_SPLIT_MIN_STEPS);
     ks = (nS + kps - 1) / kps;
-    ws = GlintSplitWs{nullptr, nullptr};
-    if (ks > 1 && !glint_split_ws(st, (size_t)ks * tiles * tile_floats, (size_t)tiles, ws)) {
+    ws = GlintSplitWs{nullptr, nullptr, 0, 0};
+    if (ks <= 1)
+        return true;
+    const bool got = fixed ? (ws = *fixed, true) : glint_split_ws_stream(st, ws);
+    const bool fits = got && (size_t)ks * tiles * tile_floats <= ws.part_floats && (size_t)tiles <= ws.nctr;
+    if (!fits) {
+        if (fixed)
+            return false;
         kps = nS;
         ks = 1;
+        ws = GlintSplitWs{nullptr, nullptr, 0, 0};
     }
+    return true;
 }
 
 /* Launch k_tile_mfma over an M x N output. K % 64 == 0, M, N >= 1. */
-template <int BM, int BN, int WM, int WN, int R, class P, class Out>
-static void tile_mfma_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st) {
+/* Each launcher returns false, launching nothing, only when a `fixed` workspace is too
+ * small for the split plan. */
+template <int BM, int BN, int WM, int WN, int R, class P, class Out, int NP = 1>
+static bool tile_mfma_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st,
+                             const GlintSplitWs *fixed = nullptr) {
+    static_assert(BM * BN <= GLINT_SPLIT_TILE_FLOATS_MAX, "split workspace capacity");
     const unsigned gx = (unsigned)((N + BN - 1) / BN), gy = (unsigned)((M + BM - 1) / BM);
     int kps, ks;
     GlintSplitWs ws;
-    tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * BN, kps, ks, ws);
-    k_tile_mfma<BM, BN, WM, WN, R, P, Out><<<dim3(gx, gy, (unsigned)ks), 64 * WM * WN, 0, st>>>(p, x, y, M, N, K, kps,
-                                                                                              ws.part, ws.ctr);
+    if (!tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * BN, kps, ks, ws, 1, fixed))
+        return false;
+    k_tile_mfma<BM, BN, WM, WN, R, P, Out, NP><<<dim3(gx, gy, (unsigned)ks), 64 * WM * WN, 0, st>>>(
+        p, x, y, M, N, K, kps, ws.part, ws.ctr);
+    return true;
 }
 
 /* Launch k_tile_big over an M x N output. K % 64 == 0, M, N >= 1, M * K < 2^31 and
@@ -870,23 +959,30 @@ static inline bool tile_big_pays(int M, int N) {
     return (int64_t)((M + 255) / 256) * ((N + 255) / 256) * 4 >= (int64_t)3 * glint_cu_count();
 }
 template <int R, class P, class Out>
-static void tile_big_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st) {
+static bool tile_big_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st,
+                            const GlintSplitWs *fixed = nullptr) {
     const unsigned gx = (unsigned)((N + 255) / 256), gy = (unsigned)((M + 255) / 256);
     int kps, ks;
     GlintSplitWs ws;
-    tile_split_plan(st, gx, gy, K >> 6, (size_t)256 * 256, kps, ks, ws);
+    /* 256 x 256 partials exceed the workspace's per-slot tile; tile_big_pays only picks this
+     * kernel with about a tile per CU, where the plan does not split anyway */
+    if (!tile_split_plan(st, gx, gy, K >> 6, (size_t)256 * 256, kps, ks, ws, 1, fixed))
+        return false;
     k_tile_big<R, P, Out><<<dim3(gx, gy, (unsigned)ks), 512, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
+    return true;
 }
 
 /* Launch k_tile_ss over an M x N output. K % 64 == 0, M, N >= 1. */
 template <int BM, int RX, class P, class Out>
-static void tile_ss_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st,
-                           int per_cu = 1) {
+static bool tile_ss_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st,
+                           int per_cu = 1, const GlintSplitWs *fixed = nullptr) {
     const unsigned gx = (unsigned)((N + 63) / 64), gy = (unsigned)((M + BM - 1) / BM);
     int kps, ks;
     GlintSplitWs ws;
-    tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * 64, kps, ks, ws, per_cu);
+    if (!tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * 64, kps, ks, ws, per_cu, fixed))
+        return false;
     k_tile_ss<BM, RX, P, Out><<<dim3(gx, gy, (unsigned)ks), 256, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
+    return true;
 }
 
 #endif

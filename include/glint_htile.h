@@ -13,9 +13,13 @@ extern "C" {
 #endif
 struct ihipStream_t;
 
-/* f32 output, f32 arithmetic (within 1e-5 * (1 + |ref|) of a float64 reference).
- * Enqueued on `stream`; y is overwritten. Returns 0, -1 for a null pointer,
- * -2 for blocksize <= 0 (or K < 1), -3 for a launch error.
+/* f32 output, f32 products and f32 sums (within 1e-5 * (1 + |ref|) of a float64 reference).
+ * At M > 1 with blocksize 64, K % 64 == 0 and aligned pointers the products run on BF16
+ * MFMA with each f32 weight split exactly into three BF16 planes (the sum differs from a
+ * sequential f32 sum only in order); M = 1 is the f32 GEMV, other shapes a generic
+ * kernel. Enqueued on `stream`; y is overwritten. Returns 0, -1 for a null pointer,
+ * -2 for blocksize <= 0 (or K < 1), -3 for a launch error. The MFMA route uses the
+ * stream's split-K workspace as launch_glint_htile_bf16_stream does.
  * Reference: include/glint_htile.h:11-14 (cuda/glint_htile.cu:165-180). */
 int launch_glint_htile_s3_f32_stream(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax,
                                      const void *d_x_bf16, float *d_y,
@@ -29,12 +33,22 @@ int launch_glint_htile_s3_f32(const uint8_t *d_hole, const uint8_t *d_plug, cons
  * prefill GEMM (larger M: BF16 MFMA on LDS-dequantized weight tiles). Contract: within
  * 1e-2 relative Frobenius error of an f32 GEMM on the expanded weights; results are
  * deterministic (split K adds its partial tiles in a fixed order).
- * At M > 1 the first call on a stream at a given size may allocate the stream's split-K
- * workspace (hipMalloc, at most 32 MiB, kept until exit); during graph capture it is not
- * grown and the GEMM runs unsplit. Same return codes. */
+ * Split-K workspace (M > 1 on the MFMA routes, both outputs): one per (device, stream),
+ * allocated at full size (CUs x 128 KiB of partials plus counters, 32 MiB on MI355X) by
+ * the first call that splits, its counters zeroed by a kernel on the stream, never grown
+ * or freed. hipStreamPerThread gets one per host thread. A launch captured into a graph
+ * keeps the workspace it bound for the graph; the next eager call on that stream gets a
+ * fresh one, so replays and eager calls never share counters. Replays of graphs captured
+ * on one stream share that workspace and must not overlap one another. A capture on a
+ * stream with no workspace yet runs unsplit. Same return codes. */
 int launch_glint_htile_bf16_stream(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax,
                                    const void *d_x_bf16, uint16_t *d_y_bf16,
                                    int M, int N, int K, int blocksize, struct ihipStream_t *stream);
+/* Allocate `stream`'s split-K workspace now (no-op if it has one), so that a later graph
+ * capture on the stream can split K and no later call allocates. Not during capture.
+ * Returns 0, or -1 if it cannot (allocation failed, or the stream is capturing). */
+int glint_htile_workspace_reserve(struct ihipStream_t *stream);
+
 #ifdef __cplusplus
 }
 #endif

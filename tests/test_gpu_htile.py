@@ -190,3 +190,116 @@ def test_bf16_split_k_workspace_growth(oracle):
         res.append(H.htile_bf16(hole, plug, am, x, N, K, 64))
     torch.cuda.synchronize()
     assert torch.equal(res[0].view(torch.int16), res[2].view(torch.int16))
+
+
+F32_SHAPES = [(2, 64, 64), (3, 300, 1088), (64, 1024, 4096), (127, 520, 2368), (128, 4096, 576), (300, 1100, 1024),
+              (513, 2048, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", F32_SHAPES)
+def test_f32_prefill_mfma_vs_float64(oracle, M, N, K):
+    """The f32-out ABI at M > 1, bs 64 (launch_glint_htile_s3_f32_stream on BF16 MFMA with the
+    weights in three exact BF16 planes): against float64, every output within the f32
+    summation bound (K + 2) 2^-23 sum|t| and within the reference's 1e-5 (1 + |ref|);
+    ragged M and N (64 x 128 tiles below M = 128, 128 x 128 above), split K, odd K steps."""
+    torch = torch_cuda()
+    print(f"f32 prefill M={M} N={N} K={K}", flush=True)
+    hole, plug, am = _encoded_weight(oracle, N, K, 3200 + M)
+    g = torch.Generator(device="cuda").manual_seed(3201 + N)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    y = host(H.htile_f32(hole, plug, am, x, N, K, 64)).reshape(M, N).astype(np.float64)
+    rows = np.unique(np.linspace(0, M - 1, min(M, 24)).astype(np.int64))
+    xs = host(x, np.uint16).reshape(M, K)[rows]
+    ref, asum = oracle.htile_f64(host(hole), host(plug), host(am), xs, rows.size, N, K, 64)
+    err = np.abs(y[rows] - ref)
+    assert (err <= (K + 2) * 2.0 ** -23 * asum).all(), float((err / ((K + 2) * 2.0 ** -23 * asum)).max())
+    assert (err <= 1e-5 * (1 + np.abs(ref))).all(), float(err.max())
+    again = H.htile_f32(hole, plug, am, x, N, K, 64)
+    assert np.array_equal(host(again).reshape(M, N), y.astype(np.float32))
+
+
+def test_f32_prefill_mfma_full_size_gate(oracle):
+    """BASELINE configs[2] shape on the f32 ABI: M = 2048 x 14336 x 4096; 16 rows against
+    float64 within both bounds, all rows finite."""
+    torch = torch_cuda()
+    M, N, K = 2048, 14336, 4096
+    print(f"f32 prefill full M={M} N={N} K={K}", flush=True)
+    hole, plug, am = _encoded_weight(oracle, N, K, 3002)
+    g = torch.Generator(device="cuda").manual_seed(3001)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    yd = H.htile_f32(hole, plug, am, x, N, K, 64)
+    assert bool(torch.isfinite(yd).all())
+    rows = np.linspace(0, M - 1, 16).astype(np.int64)
+    y = host(yd).reshape(M, N)[rows].astype(np.float64)
+    ref, asum = oracle.htile_f64(host(hole), host(plug), host(am), host(x, np.uint16).reshape(M, K)[rows], 16, N, K, 64)
+    err = np.abs(y - ref)
+    assert (err <= (K + 2) * 2.0 ** -23 * asum).all()
+    assert (err <= 1e-5 * (1 + np.abs(ref))).all()
+
+
+def test_f32_prefill_mfma_special_absmax(oracle):
+    """Blocks with an infinite or NaN absmax, and one whose CELLS * absmax overflows f32:
+    the MFMA path gives NaN and +-inf exactly where the f32 restatement does, and the
+    finite outputs agree within the bounds."""
+    torch = torch_cuda()
+    M, N, K = 8, 64, 256
+    rng = np.random.default_rng(77)
+    i = np.arange(N * K // 2)
+    hole = ((i * 7 + 1) % 256).astype(np.uint8)
+    plug = ((i * 13 + 5) % 256).astype(np.uint8)
+    am = rng.uniform(0.5, 1.5, N * K // 64).astype(np.float32)
+    am[4 * 3 + 1] = np.inf          # row 3, block 1
+    am[4 * 10 + 0] = np.nan         # row 10, block 0
+    am[4 * 20 + 2] = np.finfo(np.float32).max  # row 20: CELLS * absmax overflows where |cells| > 1
+    am[4 * 30 + 3] = np.float32(2.0 ** 126)
+    # small x keeps every product of a finite weight finite, so overflow cannot depend on order
+    x = bf16_bits(rng.normal(0, 1e-3, M * K).astype(np.float32))
+    x[5] = 0  # a zero x against the infinite block
+    y = host(H.htile_f32(dev(hole), dev(plug), dev(am), dev(x), N, K, 64)).reshape(M, N)
+    ref32 = oracle.htile_f32(hole, plug, am, x, M, N, K, 64)
+    assert np.array_equal(np.isnan(y), np.isnan(ref32))
+    assert np.array_equal(np.isinf(y), np.isinf(ref32)) and np.array_equal(y[np.isinf(y)], ref32[np.isinf(ref32)])
+    fin = np.isfinite(ref32)
+    ref, asum = oracle.htile_f64(hole, plug, am, x, M, N, K, 64)
+    err = np.abs(y[fin].astype(np.float64) - ref[fin])
+    assert (err <= (K + 2) * 2.0 ** -23 * asum[fin] + 1e-30).all()
+
+
+def test_split_workspace_under_graph_capture(oracle):
+    """A split-K launch captured into a graph keeps the workspace it bound: after the
+    capture, eager calls on the capture stream get a fresh workspace (they never share
+    counters with the graph), and every replay, with eager split launches and
+    synchronisations between them, equals the eager result bit for bit."""
+    torch = torch_cuda()
+    M, N, K = 64, 4096, 14336
+    print(f"graph capture split-K M={M} N={N} K={K}", flush=True)
+    hole, plug, am = _encoded_weight(oracle, N, K, 3301)
+    g = torch.Generator(device="cuda").manual_seed(3302)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    x2 = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        want = H.htile_bf16(hole, plug, am, x, N, K, 64, stream=s)  # reserves the stream's workspace
+        want2 = H.htile_bf16(hole, plug, am, x2, N, K, 64, stream=s)
+    s.synchronize()
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        H.htile_bf16(hole, plug, am, x, N, K, 64, out=out, stream=s)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.zero_()
+        graph.replay()
+        with torch.cuda.stream(s):
+            e = H.htile_bf16(hole, plug, am, x2, N, K, 64, stream=s)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), rep
+        assert torch.equal(e.view(torch.int16), want2.view(torch.int16)), rep
+
+
+def test_workspace_reserve_entry():
+    torch = torch_cuda()
+    s = torch.cuda.Stream()
+    assert H.encode_lib().glint_htile_workspace_reserve(H._stream(s)) == 0
+    assert H.encode_lib().glint_htile_workspace_reserve(H._stream(s)) == 0

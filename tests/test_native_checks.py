@@ -5,7 +5,9 @@
 * the committed glint_code_table.inc is what the generator produces;
 * the reciprocal-plus-correction divide matches the IEEE divide bit for bit where it
   matters and code for code everywhere, over every bf16 (w, absmax) pair the fast path
-  sees (tests/native/check_markstein.c).
+  sees (tests/native/check_markstein.c);
+* the three-plane BF16 split of the f32-out H-TILE on MFMA is exact for every f32 weight
+  (tests/native/check_split3.c).
 """
 import subprocess
 from pathlib import Path
@@ -38,3 +40,10 @@ def test_fast_divide_exhaustive_over_bf16_pairs(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=900)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "0 differ with w >= 2^-100 and w/s normal" in r.stdout and "0 code mismatches" in r.stdout
+
+
+def test_three_plane_split_exhaustive(tmp_path):
+    exe = _build(tmp_path, ROOT / "tests" / "native" / "check_split3.c", "split3")
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "0 sums differ, 0 lo not BF16, 0 special mismatches" in r.stdout
