@@ -293,17 +293,28 @@ def bench_prefill(torch, H, steps: int, copies: int = 6):
         del w
         pins[name] = ([pin] + [tuple(t.clone() for t in pin) for _ in range(copies - 1)], N, K)
     gx = torch.Generator(device="cuda").manual_seed(3001)
+    lib, st = H.encode_lib(), stream_handle(torch)
     for M in (64, 512, 2048):
         for name, (cps, N, K) in pins.items():
             x = torch.randn(M, K, device="cuda", generator=gx).to(torch.bfloat16)
             y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-            calls = [lambda pin=pin: H.htile_bf16(pin[0], pin[1], pin[2], x, N, K, 64, out=y) for pin in cps]
+            calls = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, y, M, N, K, 64, st) for p in cps]
             settle(torch, calls, 0.05)
             ms = timed(torch, calls, steps * (3 if M <= 64 else 1), copies)
             fl = 2.0 * M * N * K
             byt = N * K * (1 + 4 / 64) + 2 * M * K + 2 * M * N
+            # the reference ABI's f32 output (three exact BF16 weight planes on MFMA)
+            yf = torch.empty(M, N, dtype=torch.float32, device="cuda")
+            calls32 = [bound(lib.launch_glint_htile_s3_f32_stream, p[0], p[1], p[2], x, yf, M, N, K, 64, st) for p in cps]
+            settle(torch, calls32, 0.05)
+            ms32 = timed(torch, calls32, steps * (3 if M <= 64 else 1), copies)
+            byt32 = byt + 2 * M * N
             out[f"M{M}_{name}"] = {"ms": ms, "tflops": fl / ms / 1e9, "mfma_frac": fl / ms / 1e9 / BF16_PEAK_TFLOPS,
-                                   "eff_gbs": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS}
+                                   "eff_gbs": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS,
+                                   "f32_out": {"ms": ms32, "tflops": fl / ms32 / 1e9, "over_bf16": ms32 / ms,
+                                               "eff_gbs": byt32 / ms32 / 1e6,
+                                               "mfma_frac_3planes": 3 * fl / ms32 / 1e9 / BF16_PEAK_TFLOPS}}
+            del yf
     del pins
     return out
 
@@ -321,6 +332,31 @@ def bench_int8(torch, H, steps: int):
     ms = timed(torch, [call], steps, 2)
     ops = 2.0 * M * N * K
     return {"ms": ms, "tops": ops / ms / 1e9, "mfma_frac": ops / ms / 1e9 / I8_PEAK_TOPS, "shape": [M, N, K]}
+
+
+def bench_int8_abi(torch, H, steps: int):
+    """The attach ABI's int8_mma_gemm (bf16 x quantized per 64-block on the device, per-64
+    weight scales, f32 out) at the reference's published shape (M 70, N 4096, K 3072:
+    0.1524 ms on an RTX 3060) and at the INT8 config's 2048 x 8192 x 8192. OP = 2 M N K."""
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(5004)
+    lib = H.p7_lib()
+    st = stream_handle(torch)
+    for M, N, K in ((70, 4096, 3072), (2048, 8192, 8192)):
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        q = torch.randint(-127, 128, (N * K,), device="cuda", generator=g, dtype=torch.int8)
+        sc = torch.rand(N * K // 64, device="cuda", generator=g) * 0.02 + 1e-3
+        y = torch.empty(M, N, dtype=torch.float32, device="cuda")
+        xq = torch.empty(M * K, dtype=torch.int8, device="cuda")
+        sx = torch.empty(M * K // 64, dtype=torch.float32, device="cuda")
+        lin = H.Int8MmaLinear(q.data_ptr(), sc.data_ptr(), N, K)
+        call = bound(lib.int8_mma_gemm, x, lin, y, M, xq, sx, st)
+        settle(torch, [call], 0.05)
+        ms = timed(torch, [call], steps * (10 if M < 256 else 1), 2)
+        ops = 2.0 * M * N * K
+        out[f"M{M}_{N}x{K}"] = {"ms": ms, "tops": ops / ms / 1e9, "mfma_frac": ops / ms / 1e9 / I8_PEAK_TOPS}
+        del x, q, sc, y, xq, sx
+    return out
 
 
 def bench_w8a16(torch, H, steps: int, copies: int = 6):
@@ -561,6 +597,9 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 10 plain 256 MiB device copies (the reference kernel for scaling PMC byte counters)")
     ap.add_argument("--headline-only", action="store_true", help="only the bf16-out 14336x4096 GEMV loop")
+    ap.add_argument("--parts", default="all",
+                    help="comma list of extra measurements to run (copy,encode4096,model,prefill,int8,int8abi,w8a16,"
+                         "kmajor,hostabi,pintools) or 'all'")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
                     help="write the traffic figures from two rocprofv3 --pmc databases (no GPU needed)")
     ap.add_argument("--summarize-trace", nargs="+", metavar="DB",
@@ -596,25 +635,42 @@ def main() -> int:
     del pins
     torch.cuda.empty_cache()
     extra = {}
+    parts = set(args.parts.split(",")) if args.parts != "all" else {
+        "copy", "encode4096", "model", "prefill", "int8", "int8abi", "w8a16", "kmajor", "hostabi", "pintools"}
     if not args.quick:
-        extra["hbm_copy_1gib"] = bench_copy_ceiling(torch)
-        log(f"device copy 1 GiB {extra['hbm_copy_1gib']['gbs']:.0f} GB/s (read + write)")
-        extra["encode_4096x4096"] = bench_encode_4096(torch, H)
-        log(f"encode 4096^2 {extra['encode_4096x4096']['encode_bf16_in_gbs']:.0f} GB/s bf16-in")
-        extra["model_encode"] = bench_model_encode(torch, H, passes=3)
-        log(f"model encode {extra['model_encode']['encode_bf16_in_gbs']:.0f} GB/s bf16-in")
-        extra["prefill"] = bench_prefill(torch, H, steps=12)
-        log("prefill done")
-        extra["int8_gemm"] = bench_int8(torch, H, steps=10)
-        log(f"int8 {extra['int8_gemm']['tops']:.0f} TOPS")
-        extra["w8a16"] = bench_w8a16(torch, H, steps=10)
-        log("w8a16 done")
-        extra["kmajor_decode"] = bench_kmajor(torch, H)
-        log(f"k-major fold {extra['kmajor_decode']['fold_ms'] * 1e3:.1f} us")
-        extra["host_abi_pcie"] = bench_host_abi(H)
-        extra["pin_tools"] = bench_pin_tools()
-        log(f"pin tools convert {extra['pin_tools']['convert_bf16_in_gbs']:.2f} GB/s bf16-in (files and PCIe inclusive)")
-        log(f"host ABI encode {extra['host_abi_pcie']['encode_bf16_in_gbs']:.1f} GB/s bf16-in (PCIe inclusive)")
+        if "copy" in parts:
+            extra["hbm_copy_1gib"] = bench_copy_ceiling(torch)
+            log(f"device copy 1 GiB {extra['hbm_copy_1gib']['gbs']:.0f} GB/s (read + write)")
+        if "encode4096" in parts:
+            extra["encode_4096x4096"] = bench_encode_4096(torch, H)
+            log(f"encode 4096^2 {extra['encode_4096x4096']['encode_bf16_in_gbs']:.0f} GB/s bf16-in")
+        if "model" in parts:
+            extra["model_encode"] = bench_model_encode(torch, H, passes=3)
+            log(f"model encode {extra['model_encode']['encode_bf16_in_gbs']:.0f} GB/s bf16-in")
+        if "prefill" in parts:
+            extra["prefill"] = bench_prefill(torch, H, steps=12)
+            log("prefill " + ", ".join(f"{k} {v['ms'] * 1e3:.1f} us (f32 out {v['f32_out']['ms'] * 1e3:.1f})"
+                                       for k, v in extra["prefill"].items()))
+        if "int8" in parts:
+            extra["int8_gemm"] = bench_int8(torch, H, steps=10)
+            log(f"int8 {extra['int8_gemm']['tops']:.0f} TOPS")
+        if "int8abi" in parts:
+            extra["int8_mma_gemm_abi"] = bench_int8_abi(torch, H, steps=10)
+            log("int8_mma_gemm abi " + ", ".join(f"{k} {v['ms'] * 1e3:.1f} us"
+                                                 for k, v in extra["int8_mma_gemm_abi"].items()))
+        if "w8a16" in parts:
+            extra["w8a16"] = bench_w8a16(torch, H, steps=10)
+            log("w8a16 done")
+        if "kmajor" in parts:
+            extra["kmajor_decode"] = bench_kmajor(torch, H)
+            log(f"k-major fold {extra['kmajor_decode']['fold_ms'] * 1e3:.1f} us")
+        if "hostabi" in parts:
+            extra["host_abi_pcie"] = bench_host_abi(H)
+            log(f"host ABI encode {extra['host_abi_pcie']['encode_bf16_in_gbs']:.1f} GB/s bf16-in (PCIe inclusive)")
+        if "pintools" in parts:
+            extra["pin_tools"] = bench_pin_tools()
+            log(f"pin tools convert {extra['pin_tools']['convert_bf16_in_gbs']:.2f} GB/s bf16-in "
+                "(files and PCIe inclusive)")
     cpu = None if args.no_cpu else cpu_baseline()
     achieved = gemv["gbs"]
     line = {
