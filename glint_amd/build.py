@@ -36,7 +36,7 @@ HIP_FLAGS = [
 ]
 
 LIBS = {
-    "libglint_encode.so": ["glint_encode.hip", "glint_htile.hip", "glint_select.hip"],
+    "libglint_encode.so": ["glint_encode.hip", "glint_htile.hip", "glint_select.hip", "glint_noalloc.hip"],
     "libp7_kernels.so": ["int8_mma_gemm.hip", "int8_tile_gemm.hip", "p7_abi.cpp", "glint_plug_streamer.cpp", "p7_selftest.cpp"],
 }
 

@@ -58,6 +58,7 @@ _ENCODE_SIGS = {
     "launch_glint_htile_s3_f32": ([VP, VP, VP, VP, VP, I32, I32, I32, I32], I32),
     "launch_glint_htile_bf16_stream": ([VP, VP, VP, VP, VP, I32, I32, I32, I32, VP], I32),
     "glint_htile_workspace_reserve": ([VP], I32),
+    "launch_glint_htile_bf16_stream_noalloc": ([VP, VP, VP, VP, VP, I32, I32, I32, I32, VP], I32),
     "glint_kmajor_pack": ([VP, VP, VP, I32, I32, VP, VP, VP, VP], I32),
     "glint_gemv_km_fold": ([VP, VP, VP, VP, I32, I32, I32, VP, VP], I32),
     "glint_select_topk": ([VP, I32, I32, VP, VP, VP], I32),

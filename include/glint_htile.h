@@ -49,6 +49,16 @@ int launch_glint_htile_bf16_stream(const uint8_t *d_hole, const uint8_t *d_plug,
  * Returns 0, or -1 if it cannot (allocation failed, or the stream is capturing). */
 int glint_htile_workspace_reserve(struct ihipStream_t *stream);
 
+/* No reference counterpart. For callers that cannot allocate (code under graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): launch_glint_htile_bf16_stream
+ * with the split-K partials and counters in a static per-GPU scratch array of the library
+ * (32 MiB plus 4 KiB, held until the process ends) instead of a per-stream workspace. Same
+ * kernels, split plan and results; allocates nothing. Calls that overlap on one GPU share
+ * the array and race. Returns the codes above, or -5 when the split plan would need more
+ * than the array holds (possible only on a part with more than 256 CUs). */
+int launch_glint_htile_bf16_stream_noalloc(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax,
+                                           const void *d_x_bf16, uint16_t *d_y_bf16,
+                                           int M, int N, int K, int blocksize, struct ihipStream_t *stream);
 #ifdef __cplusplus
 }
 #endif
