@@ -221,6 +221,9 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #ifndef GEMV_X_PRE
 #define GEMV_X_PRE GEMV_X_DEPTH /* of those, rows issued before the table fill's barrier */
 #endif
+#ifndef GEMV_X_NO_RELOAD
+#define GEMV_X_NO_RELOAD 1 /* the ring loads no row past the wave's last */
+#endif
 #ifndef GEMV_X_BATCH
 #define GEMV_X_BATCH 4 /* groups of 8 cell lookups a wave may have in flight */
 #endif
@@ -385,8 +388,31 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
     };
 
     /* rows i .. i + DEPTH - 1 are in flight at the top of each round; full rounds keep
-     * every compute unconditional, so the wait counter can count the loads in flight */
+     * every compute unconditional, so the wait counter can count the loads in flight.
+     * Rounds run while every load is of a real row (GEMV_X_NO_RELOAD), then the at most
+     * 2 DEPTH - 1 rows left load only what exists: a clamped re-load of the last row would be
+     * a request for nothing. */
     int i = 0;
+#if GEMV_X_NO_RELOAD
+    for (; i + 2 * GEMV_X_DEPTH <= my; i += GEMV_X_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < GEMV_X_DEPTH; ++d) {
+            compute_row(i + d, buf[d]);
+            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + GEMV_X_DEPTH), nch, j, buf[d]);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < GEMV_X_DEPTH; ++d)
+        if (i + d < my) {
+            compute_row(i + d, buf[d]);
+            if (i + d + GEMV_X_DEPTH < my)
+                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + GEMV_X_DEPTH), nch, j, buf[d]);
+        }
+#pragma unroll
+    for (int d = 0; d < GEMV_X_DEPTH; ++d)
+        if (i + GEMV_X_DEPTH + d < my)
+            compute_row(i + GEMV_X_DEPTH + d, buf[d]);
+#else
     for (; i + GEMV_X_DEPTH <= my; i += GEMV_X_DEPTH) {
 #pragma unroll
         for (int d = 0; d < GEMV_X_DEPTH; ++d) {
@@ -398,6 +424,7 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
     for (int d = 0; d < GEMV_X_DEPTH - 1; ++d)
         if (i + d < my)
             compute_row(i + d, buf[d]);
+#endif
     __syncthreads();
 
     for (int t = threadIdx.x; t < nrows; t += blockDim.x) {
@@ -504,6 +531,31 @@ static unsigned gemv_grid(const void *kern, int threads, size_t lds, int64_t tas
     return (unsigned)(needed < resident ? needed : resident);
 }
 
+/* k_htile_gemv_xreg over an M = 1 GEMV (bs 64, K % 2048 == 0, K / 2048 <= 8, aligned). */
+template <bool OUT_BF16>
+static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x,
+                                  void *y, int N, int K, hipStream_t st) {
+    const int S = K / (64 * GEMV_X_EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
+    /* K / 8 chunks of x over 64 S G threads: 4 / G per thread */
+    auto kern = G >= 4 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 1>
+                       : (G >= 2 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 2> : k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 0>);
+    const int64_t resident =
+        std::max<int64_t>(glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4) / (G == 1 ? GEMV_G1_DIV : 1), 1);
+    const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
+    int64_t rows_per_wg = G * per_wave;
+    const int64_t cap = (GEMV_X_RED_MAX / (S * 4)) / G * G;
+    if (rows_per_wg > cap)
+        rows_per_wg = cap;
+    const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
+    size_t lds = (size_t)rows_per_wg * S * 4 * sizeof(float);
+    if (G >= 2 && lds < (size_t)K * 2)
+        lds = (size_t)K * 2; /* x staging; K <= 8192 here, within GEMV_X_RED_MAX floats */
+    if (glint_set_lds_limit((const void *)kern, GEMV_X_RED_MAX * 4) != 0)
+        return -3;
+    kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const glint_u32x4 *)x, y, N, K, G, (int)rows_per_wg);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 /* f32 output at M > 1 (the reference ABI's prefill use): 3-plane k_tile_mfma, whose
  * products are exact and whose sums are f32. 128 x 128 tiles over 8 waves (2 x 4, wave tile
  * 64 x 32) fill the 160 KiB of LDS: x 32 KiB, three W planes 96 KiB, cell table 32 KiB;
@@ -554,24 +606,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         if (!planned)
             return -5;
     } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS / 64) {
-        const int S = K / (64 * GEMV_X_EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
-        /* K / 8 chunks of x over 64 S G threads: 4 / G per thread */
-        auto kern = G >= 4 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 1>
-                           : (G >= 2 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 2> : k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 0>);
-        const int64_t resident =
-            std::max<int64_t>(glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4) / (G == 1 ? GEMV_G1_DIV : 1), 1);
-        const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
-        int64_t rows_per_wg = G * per_wave;
-        const int64_t cap = (GEMV_X_RED_MAX / (S * 4)) / G * G;
-        if (rows_per_wg > cap)
-            rows_per_wg = cap;
-        const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
-        size_t lds = (size_t)rows_per_wg * S * 4 * sizeof(float);
-        if (G >= 2 && lds < (size_t)K * 2)
-            lds = (size_t)K * 2; /* x staging; K <= 8192 here, within GEMV_X_RED_MAX floats */
-        if (glint_set_lds_limit((const void *)kern, GEMV_X_RED_MAX * 4) != 0)
-            return -3;
-        kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const glint_u32x4 *)x, y, N, K, G, (int)rows_per_wg);
+        return htile_launch_gemv_xreg<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);
     } else if (gemv_ok) {
         constexpr int R = GEMV_R, D = GEMV_D;
         const size_t lds = GEMV_LDS_BYTES(K);

@@ -79,10 +79,12 @@ __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict_
                                                        const int8_t *__restrict__ wq, const float *__restrict__ sw,
                                                        float *__restrict__ y, int m, int n, int k_in,
                                                        const uint8_t *__restrict__ pq4, const float *__restrict__ psc) {
-    __shared__ __attribute__((aligned(16))) int8_t sA[Q_BM * Q_LDS_ROW];
-    __shared__ __attribute__((aligned(16))) int8_t sB[Q_BN * Q_LDS_ROW];
-    __shared__ __attribute__((aligned(16))) int8_t sP[PLUG ? Q_BN * Q_LDS_ROW : 16];
-    __shared__ float sSx[Q_BM], sSw[Q_BN], sSp[PLUG ? Q_BN : 1];
+    /* two LDS buffers per operand: slice kb runs from buffer kb & 1 while slice kb + 1, loaded
+     * into registers during slice kb's MFMAs, is written to the other; one barrier per slice */
+    __shared__ __attribute__((aligned(16))) int8_t sA[2][Q_BM * Q_LDS_ROW];
+    __shared__ __attribute__((aligned(16))) int8_t sB[2][Q_BN * Q_LDS_ROW];
+    __shared__ __attribute__((aligned(16))) int8_t sP[2][PLUG ? Q_BN * Q_LDS_ROW : 16];
+    __shared__ float sSx[2][Q_BM], sSw[2][Q_BN], sSp[2][PLUG ? Q_BN : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * Q_BM, n0 = blockIdx.x * Q_BN;
@@ -96,31 +98,53 @@ __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict_
             for (int i = 0; i < 4; ++i)
                 acc[a][b][i] = 0.0f;
     /* staging: thread t copies 16 B of A row (t >> 2) and of B row (t >> 2), K bytes (t & 3) * 16;
-     * the plug slice is 8 B of nibbles per thread, widened to the same 16 B */
+     * the plug slice is 8 B of nibbles per thread, widened to the same 16 B; threads 0-63 load
+     * the slice's sx, 64-127 its sw, 128-191 its plug scales */
     const int sr = tid >> 2, sc = (tid & 3) * 16;
-    for (int kb = 0; kb < nkb; ++kb) {
-        glint_u32x4 va = glint_u32x4{0u, 0u, 0u, 0u}, vb = va;
+    struct Stage {
+        glint_u32x4 a, b;
+        uint32_t nib[2];
+        float s;
+    };
+    auto gload = [&](int kb, Stage &g) {
+        g.a = glint_u32x4{0u, 0u, 0u, 0u};
+        g.b = g.a;
         if (m0 + sr < m)
-            va = *(const glint_u32x4 *)(xq + (int64_t)(m0 + sr) * k_in + (int64_t)kb * 64 + sc);
+            g.a = *(const glint_u32x4 *)(xq + (int64_t)(m0 + sr) * k_in + (int64_t)kb * 64 + sc);
         if (n0 + sr < n)
-            vb = *(const glint_u32x4 *)(wq + (int64_t)(n0 + sr) * k_in + (int64_t)kb * 64 + sc);
-        *(glint_u32x4 *)(sA + sr * Q_LDS_ROW + sc) = va;
-        *(glint_u32x4 *)(sB + sr * Q_LDS_ROW + sc) = vb;
+            g.b = *(const glint_u32x4 *)(wq + (int64_t)(n0 + sr) * k_in + (int64_t)kb * 64 + sc);
         if (PLUG) {
             /* rows past n read as nibble 8 (value 0); k_in is even, so a row's nibbles start on a byte */
-            uint32_t nib[2] = {0x88888888u, 0x88888888u};
+            g.nib[0] = g.nib[1] = 0x88888888u;
             if (n0 + sr < n) {
                 const uint8_t *src = pq4 + (((int64_t)(n0 + sr) * k_in + (int64_t)kb * 64 + sc) >> 1);
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
-                    nib[h] = (uint32_t)src[4 * h] | (uint32_t)src[4 * h + 1] << 8 | (uint32_t)src[4 * h + 2] << 16 |
-                             (uint32_t)src[4 * h + 3] << 24;
+                    g.nib[h] = (uint32_t)src[4 * h] | (uint32_t)src[4 * h + 1] << 8 | (uint32_t)src[4 * h + 2] << 16 |
+                               (uint32_t)src[4 * h + 3] << 24;
             }
+        }
+        g.s = 0.0f;
+        if (tid < Q_BM) {
+            if (m0 + tid < m)
+                g.s = sx[(int64_t)(m0 + tid) * nkb + kb];
+        } else if (tid < Q_BM + Q_BN) {
+            if (n0 + tid - Q_BM < n)
+                g.s = sw[(int64_t)(n0 + tid - Q_BM) * nkb + kb];
+        } else if (PLUG && tid < Q_BM + 2 * Q_BN) {
+            if (n0 + tid - Q_BM - Q_BN < n)
+                g.s = psc[(int64_t)(n0 + tid - Q_BM - Q_BN) * nkb + kb];
+        }
+    };
+    auto lstore = [&](int buf, const Stage &g) {
+        *(glint_u32x4 *)(sA[buf] + sr * Q_LDS_ROW + sc) = g.a;
+        *(glint_u32x4 *)(sB[buf] + sr * Q_LDS_ROW + sc) = g.b;
+        if (PLUG) {
             uint32_t out[4];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 /* bytes 4h..4h+3 hold elements 8h..8h+7: low nibble first; value = nibble - 8 */
-                const uint32_t lo = nib[h] & 0x0F0F0F0Fu, hi = (nib[h] >> 4) & 0x0F0F0F0Fu;
+                const uint32_t lo = g.nib[h] & 0x0F0F0F0Fu, hi = (g.nib[h] >> 4) & 0x0F0F0F0Fu;
                 const uint32_t e0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u); /* elements 0..3 */
                 const uint32_t e1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u); /* elements 4..7 */
                 /* per byte: nibble - 8 mod 256; setting bit 7 of every byte first keeps the
@@ -128,24 +152,32 @@ __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict_
                 out[2 * h] = ((e0 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
                 out[2 * h + 1] = ((e1 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
             }
-            *(glint_u32x4 *)(sP + sr * Q_LDS_ROW + sc) = glint_u32x4{out[0], out[1], out[2], out[3]};
+            *(glint_u32x4 *)(sP[buf] + sr * Q_LDS_ROW + sc) = glint_u32x4{out[0], out[1], out[2], out[3]};
         }
         if (tid < Q_BM)
-            sSx[tid] = (m0 + tid < m) ? sx[(int64_t)(m0 + tid) * nkb + kb] : 0.0f;
+            sSx[buf][tid] = g.s;
         else if (tid < Q_BM + Q_BN)
-            sSw[tid - Q_BM] = (n0 + tid - Q_BM < n) ? sw[(int64_t)(n0 + tid - Q_BM) * nkb + kb] : 0.0f;
+            sSw[buf][tid - Q_BM] = g.s;
         else if (PLUG && tid < Q_BM + 2 * Q_BN)
-            sSp[tid - Q_BM - Q_BN] = (n0 + tid - Q_BM - Q_BN < n) ? psc[(int64_t)(n0 + tid - Q_BM - Q_BN) * nkb + kb] : 0.0f;
-        __syncthreads();
+            sSp[buf][tid - Q_BM - Q_BN] = g.s;
+    };
+    Stage st;
+    gload(0, st);
+    lstore(0, st);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int cur = kb & 1;
+        if (kb + 1 < nkb)
+            gload(kb + 1, st);
         glint_i32x4 af[2], bf[2], pf[2];
 #pragma unroll
         for (int a = 0; a < 2; ++a)
-            af[a] = *(const glint_i32x4 *)(sA + (wm * 32 + a * 16 + (lane & 15)) * Q_LDS_ROW + (lane >> 4) * 16);
+            af[a] = *(const glint_i32x4 *)(sA[cur] + (wm * 32 + a * 16 + (lane & 15)) * Q_LDS_ROW + (lane >> 4) * 16);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            bf[b] = *(const glint_i32x4 *)(sB + (wn * 32 + b * 16 + (lane & 15)) * Q_LDS_ROW + (lane >> 4) * 16);
+            bf[b] = *(const glint_i32x4 *)(sB[cur] + (wn * 32 + b * 16 + (lane & 15)) * Q_LDS_ROW + (lane >> 4) * 16);
             if (PLUG)
-                pf[b] = *(const glint_i32x4 *)(sP + (wn * 32 + b * 16 + (lane & 15)) * Q_LDS_ROW + (lane >> 4) * 16);
+                pf[b] = *(const glint_i32x4 *)(sP[cur] + (wn * 32 + b * 16 + (lane & 15)) * Q_LDS_ROW + (lane >> 4) * 16);
         }
 #pragma unroll
         for (int a = 0; a < 2; ++a)
@@ -156,16 +188,18 @@ __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict_
                 if (PLUG)
                     ip = glint_mfma_i8(af[a], pf[b], glint_i32x4{0, 0, 0, 0});
                 const int col = wn * 32 + b * 16 + (lane & 15);
-                const float swv = sSw[col];
-                const float spv = PLUG ? sSp[col] : 0.0f;
+                const float swv = sSw[cur][col];
+                const float spv = PLUG ? sSp[cur][col] : 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float sxv = sSx[wm * 32 + a * 16 + (lane >> 4) * 4 + i];
+                    const float sxv = sSx[cur][wm * 32 + a * 16 + (lane >> 4) * 4 + i];
                     acc[a][b][i] = acc[a][b][i] + ((float)ic[i] * sxv) * swv;
                     if (PLUG)
                         acc[a][b][i] = acc[a][b][i] + ((float)ip[i] * sxv) * spv;
                 }
             }
+        if (kb + 1 < nkb)
+            lstore(cur ^ 1, st);
         __syncthreads();
     }
 #pragma unroll
@@ -537,6 +571,268 @@ __global__ __launch_bounds__(G3_THREADS) void k_int8_gemm_dma(const int8_t *__re
             }
 }
 
+/* The attach ABI's W8A8 GEMM on the same 256 x 256 DMA ring (int8_mma_gemm at the shapes
+ * with at least 3/4 as many 256 x 256 tiles as CUs). Per 64-slice kb the wave's 32 MFMAs
+ * run with zero C (ic = the slice's exact int32 dot products), and each A tile's 4 results
+ * go straight into the f32 accumulators as acc = acc + ((float)ic * sx[m, kb]) * sw[n, kb]
+ * (separate multiplies and add, kb ascending: bit-identical to the 64 x 64 kernel and to
+ * the CPU emulation). A third ring carries the slice's scales: 256 sx (rows of the tile)
+ * and 256 sw (columns), one 4-byte DMA per wave per step (waves 0-3 rows, 4-7 columns).
+ * That epilogue is 4 VALU ops per output per slice against one MFMA per 16 x 16 x 64, so
+ * the kernel is VALU-bound: at 2048 x 8192 x 8192 about 218 us of VALU issue on 256 CUs.
+ * ACCUM stores y + acc (the second pass of the two-pass forms). Offsets are 32-bit:
+ * M K, N K, M K / 16 and N K / 16 < 2^31 (the host checks). */
+template <bool ACCUM>
+__global__ __launch_bounds__(512) void k_int8_mma_dma(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
+                                                      const float *__restrict__ sx, const float *__restrict__ sw,
+                                                      float *__restrict__ y, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) int8_t sA0[G2_BM * G2_LDS_ROW], sA1[G2_BM * G2_LDS_ROW],
+        sA2[G2_BM * G2_LDS_ROW], sA3[G2_BM * G2_LDS_ROW];
+    __shared__ __attribute__((aligned(16))) int8_t sB0[G2_BN * G2_LDS_ROW], sB1[G2_BN * G2_LDS_ROW],
+        sB2[G2_BN * G2_LDS_ROW], sB3[G2_BN * G2_LDS_ROW];
+    /* scales of a slice: [0, 256) sx of the tile's rows, [256, 512) sw of its columns */
+    __shared__ __attribute__((aligned(16))) float sS0[512], sS1[512], sS2[512], sS3[512];
+    auto bufA = [&](int i) { return i == 0 ? sA0 : (i == 1 ? sA1 : (i == 2 ? sA2 : sA3)); };
+    auto bufB = [&](int i) { return i == 0 ? sB0 : (i == 1 ? sB1 : (i == 2 ? sB2 : sB3)); };
+    auto bufS = [&](int i) { return i == 0 ? sS0 : (i == 1 ? sS1 : (i == 2 ? sS2 : sS3)); };
+    constexpr int NW = 8, WNW = 4, TM = 8, TN = 4, RPW = 32, QN = 2;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WNW, wn = wave % WNW;
+    const int m0 = blockIdx.y * G2_BM, n0 = blockIdx.x * G2_BN;
+    const int nkb = K / 64;
+    float acc[TM][TN][4];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[a][b][i] = 0.0f;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)A, (short)0, (int)((uint32_t)M * (uint32_t)K), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)B, (short)0, (int)((uint32_t)N * (uint32_t)K), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rs = wave < 4
+        ? __builtin_amdgcn_make_buffer_rsrc((void *)sx, (short)0, (int)((uint32_t)M * (uint32_t)nkb * 4u), GLINT_BUF_DWORD3)
+        : __builtin_amdgcn_make_buffer_rsrc((void *)sw, (short)0, (int)((uint32_t)N * (uint32_t)nkb * 4u), GLINT_BUF_DWORD3);
+    uint32_t avo[QN], bvo[QN];
+#pragma unroll
+    for (int q = 0; q < QN; ++q) {
+        const int r = RPW * wave + 16 * q + (lane >> 2);
+        const int c = (lane & 3) ^ (((r >> 1) ^ ((r >> 3) & 1)) & 3);
+        avo[q] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)c * 16u;
+        bvo[q] = (uint32_t)min(n0 + r, N - 1) * (uint32_t)K + (uint32_t)c * 16u;
+    }
+    /* scale lane: wave w < 4 row m0 + 64 w + l, else column n0 + 64 (w - 4) + l (clamped) */
+    const uint32_t svo = (wave < 4 ? (uint32_t)min(m0 + 64 * wave + lane, M - 1)
+                                   : (uint32_t)min(n0 + 64 * (wave - 4) + lane, N - 1)) *
+                         (uint32_t)nkb * 4u;
+    auto dma = [&](int kb, int buf) {
+        const uint32_t kc = (uint32_t)min(kb, nkb - 1);
+#pragma unroll
+        for (int q = 0; q < QN; ++q) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void *)(bufA(buf) + (RPW * wave + 16 * q) * G2_LDS_ROW), 16,
+                avo[q], kc * 64u, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void *)(bufB(buf) + (RPW * wave + 16 * q) * G2_LDS_ROW), 16,
+                bvo[q], kc * 64u, 0, 0);
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(bufS(buf) + 64 * wave),
+                                                 4, svo, kc * 4u, 0, 0);
+    };
+    const int fr_ofs = g2_lds_ofs(lane & 15, lane >> 4);
+    auto step = [&](int kb, int u) {
+        /* own loads of step kb landed (later steps' 2 QN + 1 each remain), own reads of step
+         * kb - 1 done; then the barrier with global-only fences (see k_int8_gemm_dma) */
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0((2 * QN + 1) * (G3_NBUF - 2)));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
+        dma(kb + G3_NBUF - 1, (u + G3_NBUF - 1) % G3_NBUF);
+        __builtin_amdgcn_sched_barrier(0);
+        const int8_t *ta = bufA(u), *tb = bufB(u);
+        const float *ts = bufS(u);
+        glint_i32x4 bf[TN];
+        float swv[TN];
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            bf[b] = *(const glint_i32x4 *)(tb + (wn * TN * 16 + b * 16) * G2_LDS_ROW + fr_ofs);
+            swv[b] = ts[256 + wn * TN * 16 + b * 16 + (lane & 15)];
+        }
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+            const glint_i32x4 af = *(const glint_i32x4 *)(ta + (wm * 128 + a * 16) * G2_LDS_ROW + fr_ofs);
+            const glint_f32x4 sxv = *(const glint_f32x4 *)(ts + wm * 128 + a * 16 + (lane >> 4) * 4);
+#pragma unroll
+            for (int b = 0; b < TN; ++b) {
+                const glint_i32x4 ic = glint_mfma_i8(af, bf[b], glint_i32x4{0, 0, 0, 0});
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[a][b][i] = acc[a][b][i] + ((float)ic[i] * sxv[i]) * swv[b];
+            }
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < G3_NBUF - 1; ++i)
+        dma(i, i);
+    int kb = 0;
+    for (; kb + G3_NBUF <= nkb; kb += G3_NBUF) {
+#pragma unroll
+        for (int u = 0; u < G3_NBUF; ++u)
+            step(kb + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < G3_NBUF; ++u)
+        if (kb + u < nkb)
+            step(kb + u, u);
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0); /* the ring's last (clamped) loads land first */
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = m0 + wm * 128 + a * 16 + (lane >> 4) * 4 + i;
+                const int c = n0 + wn * TN * 16 + b * 16 + (lane & 15);
+                if (r < M && c < N) {
+                    float *dst = y + (int64_t)r * N + c;
+                    *dst = ACCUM ? *dst + acc[a][b][i] : acc[a][b][i];
+                }
+            }
+}
+
+/* The attach ABI's W8A8 GEMM for the shapes with few 256 x 256 tiles (small m: a decode or
+ * short prefill): 64 x 64 tiles, 4 waves in 2 x 2 (32 x 32 each), operands and scales
+ * through a ring of Q_NBUF slice buffers filled by LDS DMA, loads Q_NBUF - 1 slices ahead.
+ * The slices of an output must be added in order, so a tile walks all of K; with few
+ * tiles per CU the time per slice is the load latency, and the deep ring spreads it over
+ * Q_NBUF - 1 slices. Each wave issues 3 loads per slice (16 rows of A, 16 of B, 64 scales:
+ * wave 0 the tile's sx, wave 1 its sw, waves 2-3 copies of both into spare slots, so every
+ * wave's wait count is the same). Epilogue as k_int8_mma_dma. */
+#ifndef Q_NBUF
+#define Q_NBUF 8
+#endif
+template <bool ACCUM>
+__global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
+                                                       const float *__restrict__ sx, const float *__restrict__ sw,
+                                                       float *__restrict__ y, int M, int N, int K) {
+    /* one array per ring slot: the compiler then sees that a DMA into one slot does not
+     * alias fragment reads of another (with one array it waits for every DMA in flight,
+     * vmcnt(0), before each step's reads, which empties the ring) */
+    static_assert(Q_NBUF == 8, "ring slots are declared one by one");
+#define Q_SLOT(i) __shared__ __attribute__((aligned(16))) int8_t sA##i[Q_BM * G2_LDS_ROW], sB##i[Q_BN * G2_LDS_ROW]; \
+    __shared__ __attribute__((aligned(16))) float sS##i[256]; /* [0, 64) sx, [64, 128) sw */
+    Q_SLOT(0) Q_SLOT(1) Q_SLOT(2) Q_SLOT(3) Q_SLOT(4) Q_SLOT(5) Q_SLOT(6) Q_SLOT(7)
+#undef Q_SLOT
+    auto slotA = [&](int i) -> int8_t * {
+        switch (i) { case 0: return sA0; case 1: return sA1; case 2: return sA2; case 3: return sA3;
+                     case 4: return sA4; case 5: return sA5; case 6: return sA6; default: return sA7; }
+    };
+    auto slotB = [&](int i) -> int8_t * {
+        switch (i) { case 0: return sB0; case 1: return sB1; case 2: return sB2; case 3: return sB3;
+                     case 4: return sB4; case 5: return sB5; case 6: return sB6; default: return sB7; }
+    };
+    auto slotS = [&](int i) -> float * {
+        switch (i) { case 0: return sS0; case 1: return sS1; case 2: return sS2; case 3: return sS3;
+                     case 4: return sS4; case 5: return sS5; case 6: return sS6; default: return sS7; }
+    };
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * Q_BM, n0 = blockIdx.x * Q_BN;
+    const int nkb = K / 64;
+    float acc[2][2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[a][b][i] = 0.0f;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)A, (short)0, (int)((uint32_t)M * (uint32_t)K), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)B, (short)0, (int)((uint32_t)N * (uint32_t)K), GLINT_BUF_DWORD3);
+    const bool rows = (wave & 1) == 0; /* waves 0, 2: sx; 1, 3: sw */
+    const __amdgpu_buffer_rsrc_t rs = rows
+        ? __builtin_amdgcn_make_buffer_rsrc((void *)sx, (short)0, (int)((uint32_t)M * (uint32_t)nkb * 4u), GLINT_BUF_DWORD3)
+        : __builtin_amdgcn_make_buffer_rsrc((void *)sw, (short)0, (int)((uint32_t)N * (uint32_t)nkb * 4u), GLINT_BUF_DWORD3);
+    /* wave w: rows 16 w .. +15 of both tiles; lane l takes row 16 w + l / 4, LDS slot l % 4 */
+    const int r = 16 * wave + (lane >> 2);
+    const int c = (lane & 3) ^ (((r >> 1) ^ ((r >> 3) & 1)) & 3);
+    const uint32_t avo = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)c * 16u;
+    const uint32_t bvo = (uint32_t)min(n0 + r, N - 1) * (uint32_t)K + (uint32_t)c * 16u;
+    const uint32_t svo = (rows ? (uint32_t)min(m0 + lane, M - 1) : (uint32_t)min(n0 + lane, N - 1)) * (uint32_t)nkb * 4u;
+    auto dma = [&](int kb, int buf) {
+        const uint32_t kc = (uint32_t)min(kb, nkb - 1);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ra, (__attribute__((address_space(3))) void *)(slotA(buf) + 16 * wave * G2_LDS_ROW), 16, avo, kc * 64u, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb, (__attribute__((address_space(3))) void *)(slotB(buf) + 16 * wave * G2_LDS_ROW), 16, bvo, kc * 64u, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(slotS(buf) + 64 * wave),
+                                                 4, svo, kc * 4u, 0, 0);
+    };
+    const int fr_ofs = g2_lds_ofs(lane & 15, lane >> 4);
+    auto step = [&](int kb, int u) {
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(3 * (Q_NBUF - 2)));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
+        dma(kb + Q_NBUF - 1, (u + Q_NBUF - 1) % Q_NBUF);
+        __builtin_amdgcn_sched_barrier(0);
+        const int8_t *ta = slotA(u), *tb = slotB(u);
+        const float *ts = slotS(u);
+        glint_i32x4 af[2], bf[2];
+        float swv[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+            af[a] = *(const glint_i32x4 *)(ta + (wm * 32 + a * 16) * G2_LDS_ROW + fr_ofs);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            bf[b] = *(const glint_i32x4 *)(tb + (wn * 32 + b * 16) * G2_LDS_ROW + fr_ofs);
+            swv[b] = ts[64 + wn * 32 + b * 16 + (lane & 15)];
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            const glint_f32x4 sxv = *(const glint_f32x4 *)(ts + wm * 32 + a * 16 + (lane >> 4) * 4);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const glint_i32x4 ic = glint_mfma_i8(af[a], bf[b], glint_i32x4{0, 0, 0, 0});
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[a][b][i] = acc[a][b][i] + ((float)ic[i] * sxv[i]) * swv[b];
+            }
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < Q_NBUF - 1; ++i)
+        dma(i, i);
+    int kb = 0;
+    for (; kb + Q_NBUF <= nkb; kb += Q_NBUF) {
+#pragma unroll
+        for (int u = 0; u < Q_NBUF; ++u)
+            step(kb + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < Q_NBUF; ++u)
+        if (kb + u < nkb)
+            step(kb + u, u);
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0); /* the ring's last (clamped) loads land first */
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rr = m0 + wm * 32 + a * 16 + (lane >> 4) * 4 + i;
+                const int cc = n0 + wn * 32 + b * 16 + (lane & 15);
+                if (rr < M && cc < N) {
+                    float *dst = y + (int64_t)rr * N + cc;
+                    *dst = ACCUM ? *dst + acc[a][b][i] : acc[a][b][i];
+                }
+            }
+}
+
 #ifndef G3_DMA
 #define G3_DMA 1
 #endif
@@ -570,9 +866,22 @@ static void q_launch_quant(const void *x, int m, int k_in, int8_t *xq, float *sx
     k_quant_act<<<(unsigned)grid, 256, 0, st>>>((const glint_u32x4 *)x, nchunk8, (glint_u32x2 *)xq, sx);
 }
 
+/* The W8A8 product: the 256 x 256 DMA-ring kernel where there are enough tiles, else the
+ * 64 x 64 DMA-ring kernel (both need their 32-bit offsets to fit); the fused plug (and an
+ * operand past 2 GiB) takes the 64 x 64 register-staged kernel. */
 template <bool PLUG, bool ACCUM>
 static void q_launch_gemm(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw, float *y, int m,
                           int n, int k_in, const uint8_t *pq4, const float *psc, hipStream_t st) {
+    if (!PLUG && g2_pays(m, n) && g3_fits(m, n, k_in)) {
+        k_int8_mma_dma<ACCUM><<<dim3((n + G2_BN - 1) / G2_BN, (m + G2_BM - 1) / G2_BM), 512, 0, st>>>(
+            xq, wq, sx, sw, y, m, n, k_in);
+        return;
+    }
+    if (!PLUG && g3_fits(m, n, k_in)) {
+        k_int8_mma_ring<ACCUM><<<dim3((n + Q_BN - 1) / Q_BN, (m + Q_BM - 1) / Q_BM), 256, 0, st>>>(xq, wq, sx, sw, y, m,
+                                                                                                 n, k_in);
+        return;
+    }
     dim3 g((n + Q_BN - 1) / Q_BN, (m + Q_BM - 1) / Q_BM);
     k_int8_mma_gemm<PLUG, ACCUM><<<g, 256, 0, st>>>(xq, sx, wq, sw, y, m, n, k_in, pq4, psc);
 }

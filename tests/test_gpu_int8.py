@@ -120,3 +120,70 @@ def test_int8_gemm_extremes(oracle, M, N):
     B[1::2] = -127
     C = host(H.int8_gemm_i32(dev(A).reshape(M, K), dev(B).reshape(N, K)))
     assert (C[:, 0::2] == -K * 127 * 127).all() and (C[:, 1::2] == K * 127 * 127).all()
+
+
+def _bands(m, h):
+    return sorted({(0, min(h, m)), (max(m // 2 - h // 2, 0), min(m // 2 + h // 2, m)), (max(m - h, 0), m)})
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 24576, 640), (4096, 3100, 1088), (3000, 4100, 64)])
+def test_int8_mma_gemm_dma_tiles_match_emulation(oracle, m, n, k):
+    """int8_mma_gemm where it takes the 256 x 256 DMA-ring kernel (at least 3/4 as many
+    256 x 256 tiles as CUs on a 256-CU part): ragged N, a ragged slice count (17), a single
+    slice. Activation bytes exact on the whole input; y bit-exact against the oracle's
+    emulation on three 64-row bands (first, middle, last)."""
+    print(f"int8_mma_gemm dma m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(m + n + k)
+    x = bf16_bits(rng.normal(0, 1, m * k).astype(np.float32))
+    wq = rng.integers(-127, 128, n * k, dtype=np.int8)
+    sw = rng.uniform(1e-3, 2e-2, n * (k // 64)).astype(np.float32)
+    y, xq, sx = H.int8_mma_gemm(dev(x), dev(wq), dev(sw), n, k)
+    oxq, osx = oracle.quant_act(x, m, k)
+    assert host(xq).tobytes() == oxq.tobytes() and host(sx).tobytes() == osx.tobytes()
+    got = host(y).reshape(m, n)
+    nkb = k // 64
+    for r0, r1 in _bands(m, 64):
+        ref = oracle.int8_mma_emu(oxq[r0 * k:r1 * k], osx[r0 * nkb:r1 * nkb], wq, sw, r1 - r0, n, k)
+        assert got[r0:r1].tobytes() == ref.tobytes(), (r0, first_diff(got[r0:r1].view(np.uint32), ref.view(np.uint32)))
+
+
+def test_int8_mma_gemm_plug_two_pass_on_dma_tiles(oracle):
+    """The two-pass late plug where both passes take the DMA-ring kernel (the second one
+    accumulating into y): bit-exact against base + plug on 64-row bands."""
+    m, n, k = 512, 24576, 128
+    print(f"int8_mma_gemm_plug dma m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(99)
+    x = bf16_bits(rng.normal(0, 1, m * k).astype(np.float32))
+    wq = rng.integers(-127, 128, n * k, dtype=np.int8)
+    sw = rng.uniform(1e-3, 2e-2, n * (k // 64)).astype(np.float32)
+    q4 = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
+    sp = rng.uniform(1e-4, 2e-3, n * (k // 64)).astype(np.float32)
+    got = host(H.int8_mma_gemm_plug(dev(x), dev(wq), dev(sw), dev(q4), dev(sp), n, k, fused=False)).reshape(m, n)
+    xq, sx = oracle.quant_act(x, m, k)
+    pq = oracle.unpack_res4(q4, n * k)
+    nkb = k // 64
+    for r0, r1 in _bands(m, 64):
+        xs, ss = xq[r0 * k:r1 * k], sx[r0 * nkb:r1 * nkb]
+        want = oracle.int8_mma_emu(xs, ss, wq, sw, r1 - r0, n, k) + oracle.int8_mma_emu(xs, ss, pq, sp, r1 - r0, n, k)
+        assert got[r0:r1].tobytes() == want.tobytes(), (r0, first_diff(got[r0:r1].view(np.uint32), want.view(np.uint32)))
+
+
+def test_int8_mma_gemm_config4_full_size(oracle):
+    """BASELINE configs[4]'s shape on the attach ABI (bf16 x quantized per 64-block, per-64
+    weight scales): 2048 x 8192 x 8192, bit-exact on two 32-row bands."""
+    m, n, k = 2048, 8192, 8192
+    print(f"int8_mma_gemm configs[4] m={m} n={n} k={k}", flush=True)
+    torch = torch_cuda()
+    g = torch.Generator(device="cuda").manual_seed(5004)
+    xd = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+    qd = torch.randint(-127, 128, (n * k,), device="cuda", generator=g, dtype=torch.int8)
+    sd = torch.rand(n * k // 64, device="cuda", generator=g) * 0.02 + 1e-3
+    y, xq, sx = H.int8_mma_gemm(xd, qd, sd, n, k)
+    x = host(xd, np.uint16).reshape(-1)
+    oxq, osx = oracle.quant_act(x, m, k)
+    assert host(xq).tobytes() == oxq.tobytes() and host(sx).tobytes() == osx.tobytes()
+    got, wq, sw = host(y).reshape(m, n), host(qd), host(sd)
+    nkb = k // 64
+    for r0, r1 in ((0, 32), (m - 32, m)):
+        ref = oracle.int8_mma_emu(oxq[r0 * k:r1 * k], osx[r0 * nkb:r1 * nkb], wq, sw, r1 - r0, n, k)
+        assert got[r0:r1].tobytes() == ref.tobytes(), (r0, first_diff(got[r0:r1].view(np.uint32), ref.view(np.uint32)))
