@@ -432,7 +432,7 @@ def bench_pin_tools(tensors: int = 16):
     import time
     import numpy as np
     from glint_amd import pin_tools as P
-    from glint_amd.safetensors_io import write_safetensors
+    from glint_amd.tensorfile import save
     rng = np.random.default_rng(4000)
     with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as td:
         src = Path(td) / "src"
@@ -445,7 +445,7 @@ def bench_pin_tools(tensors: int = 16):
                 w = (rng.standard_normal((4096, 4096), dtype=np.float32) * 0.02).view(np.uint32)
                 raw = ((w + (0x7FFF + ((w >> 16) & 1))) >> 16).astype("<u2").tobytes()
                 ts.append((f"layers.{s * tensors // 2 + l}.mlp.weight", "BF16", (4096, 4096), raw))
-            write_safetensors(src / shard, ts)
+            save(src / shard, ts)
             wmap.update({t[0]: shard for t in ts})
         (src / P.INDEX_NAME).write_text(json.dumps({"metadata": {}, "weight_map": wmap}))
         P.convert(src, Path(td) / "warm", dry_run=True)

@@ -1,27 +1,24 @@
-"""GLINT pin tools on the MI355X device path: convert, verify and unpin.
+"""GLINT pin tools on the MI355X device path: convert, verify, unpin.
 
     python -m glint_amd.pin_tools convert --src MODEL --out PIN [--blocksize 64] [--dry-run]
     python -m glint_amd.pin_tools verify  --pin PIN [--src MODEL] [--parity] [--cuda] [--out F] [--quiet]
     python -m glint_amd.pin_tools unpin   --pin PIN --out DIR [--dtype BF16|F16|F32]
 
-The pin format, the file set (shards, index, sidecar files, pin.json,
-CONVERT_REPORT.json) and the verify evidence follow the reference's tools
-(glint_pin.py:23-193, glint_verify.py:29-144, glint_unpin.py:24-85,
-glint_pinfile.py:8-61), so a pin made here reads in the reference's tools and back.
+Interface kept from the reference's tools, so pins move between the two: the pin layout
+(per linear "<stem>.weight" U8 [ceil(n/2), 1] hole plane, ".weight.glint_plug" U8 plug
+plane, ".weight.absmax" F32 [ceil(n/bs)], ".weight.glint_state" JSON bytes; one
+"_glint_cells" F32 [16, 16] in the first shard), the file set (shards named as the
+source's, "model.safetensors.index.json" when sharded, "pin.json", "CONVERT_REPORT.json",
+the copied sidecar files) and the JSON keys of every report (glint_pin.py:87-193,
+glint_verify.py:48-144, glint_unpin.py:45-85).
 
-What runs where:
-- convert reads each shard through a memory map. For every dense 2-D ".weight" it
-  stages the bytes in pinned host memory, copies them on a copy stream and encodes on a
-  compute stream: BF16 straight from its bits, F16 widened to f32 on the device, F32
-  as is. It then expands the pin on the device for the module's RMSE and copies the
-  planes back. Staging of tensor i + 1 on the host overlaps the device work of tensor i.
-- unpin expands on the device (BF16 with the reference's rounding and NaN rule, F32, or
-  F16 from the f32 expand), with the same overlap.
-- verify checks layout on the host. Its gates compare against the host codec
-  (glint_amd.host_codec): --cuda is the device expand vs the host expand at
-  max_abs < 1e-5; --parity is the pin's bytes vs a host re-encode of the source.
-There is no host encode or expand path: without the HIP library and a GPU, convert and
-unpin raise RuntimeError (dry runs and the layout checks still work).
+Device path: each tensor to encode is copied from the shard's memory map into pinned
+host memory, moved on a copy stream and encoded on a compute stream (BF16 from its bits,
+F16 widened on the device, F32 as is); its RMSE comes from a device expand, and the planes
+return through pinned memory. Work is queued one tensor ahead, so reading and staging the
+next tensor overlaps the device work of the current one. unpin expands on the device the
+same way. Without the HIP library or a GPU, convert and unpin raise RuntimeError; dry runs
+and verify's layout checks need neither.
 """
 from __future__ import annotations
 
@@ -29,76 +26,119 @@ import argparse
 import json
 import shutil
 import sys
+from collections import deque
+from dataclasses import dataclass, field
 from pathlib import Path
-from typing import Dict, Iterator, List, Optional, Tuple
+from typing import Callable, Dict, Iterable, Iterator, List, Optional, Tuple
 
 import numpy as np
 
 from . import codebook
-from . import host_codec as HC
-from .safetensors_io import SafeTensorsFile, write_safetensors
+from . import host_codec as hc
+from .tensorfile import TensorFile, save
 
-PARENT_KEEP = ("norm", "bias", "rotary", "cos_cached", "sin_cached")
+# ---------------------------------------------------------------- format names
+PIN_SCHEMA = "glint_pin_v1"
+VERIFY_SCHEMA = "glint_verify_v1"
 INDEX_NAME = "model.safetensors.index.json"
+SINGLE_SHARD = "model.safetensors"
+CELLS_TENSOR = "_glint_cells"
 STATE_SUFFIX = ".weight.glint_state"
+DENSE_DTYPES = ("BF16", "F16", "F32")
+# files that make a pin (or an unpinned model) loadable, copied when present
 SIDECAR = ("config.json", "generation_config.json", "tokenizer.json", "tokenizer_config.json",
            "special_tokens_map.json", "tokenizer.model", "vocab.json", "merges.txt", "added_tokens.json",
            "chat_template.jinja")
-CUDA_EXPAND_TOL = 1e-5  # glint_verify.py:29
-DENSE = ("BF16", "F16", "F32")
+# substrings of tensor names that stay dense (normalisation, biases, rotary tables)
+DENSE_KEEP = ("norm", "bias", "rotary", "cos_cached", "sin_cached")
+EXPAND_GATE = 1e-5  # verify --cuda: largest |device - host| expand difference allowed (glint_verify.py:29)
 
 
-def numel_of(shape) -> int:
-    n = 1
-    for d in shape:
-        n *= int(d)
-    return n
+def module_names(stem: str) -> Dict[str, str]:
+    """The four tensors a converted linear becomes."""
+    w = stem + ".weight"
+    return {"hole": w, "plug": w + ".glint_plug", "absmax": w + ".absmax", "state": stem + STATE_SUFFIX}
 
 
-def _is_keep(name: str) -> bool:
+def is_linear(name: str, dtype: str, shape) -> bool:
+    """A tensor the pin encodes: a dense 2-D ".weight" that is not a norm, bias or rotary table."""
     low = name.lower()
-    return any(k in low for k in PARENT_KEEP) or name.endswith(".bias")
+    kept = name.endswith(".bias") or any(k in low for k in DENSE_KEEP)
+    return dtype in DENSE_DTYPES and len(shape) == 2 and name.endswith(".weight") and not kept
+
+
+def element_count(shape) -> int:
+    return int(np.prod([int(d) for d in shape], dtype=np.int64)) if len(shape) else 1
+
+
+def table_values() -> List[float]:
+    return np.frombuffer(codebook.cells_f32_bytes(), dtype="<f4").tolist()
+
+
+# ------------------------------------------------------------------- the source
+class ModelSource:
+    """Where a model's tensors live: a .safetensors file, or a directory holding
+    model.safetensors, an index naming its shards, or a single .safetensors file."""
+
+    def __init__(self, path: Path):
+        root = Path(path).expanduser().resolve()
+        self.sharded = False
+        if not root.is_dir():
+            self.dir, self.files = root.parent, [root]
+            return
+        self.dir = root
+        if (root / SINGLE_SHARD).is_file():
+            self.files = [root / SINGLE_SHARD]
+        elif (root / INDEX_NAME).is_file():
+            wanted = sorted(set(json.loads((root / INDEX_NAME).read_text())["weight_map"].values()))
+            absent = [s for s in wanted if not (root / s).is_file()]
+            if absent:
+                raise FileNotFoundError(f"{root / INDEX_NAME} lists shards that are not there: {', '.join(absent)}")
+            self.files = [root / s for s in wanted]
+        else:
+            found = sorted(root.glob("*.safetensors"))
+            if len(found) != 1:
+                raise FileNotFoundError(f"{root}: expected {SINGLE_SHARD}, {INDEX_NAME} or a single .safetensors "
+                                        f"file, found {len(found)} .safetensors files")
+            self.files = found
+        self.sharded = len(self.files) > 1
+
+    def lookup(self) -> Dict[str, TensorFile]:
+        """Every tensor name -> its open file (the caller closes them: close_all)."""
+        table: Dict[str, TensorFile] = {}
+        for f in self.files:
+            tf = TensorFile(f)
+            table.update(dict.fromkeys(tf.entries, tf))
+        return table
 
 
 def resolve_shards(src: Path) -> List[Path]:
-    """A file, or a dir with model.safetensors, an index, or exactly one .safetensors
-    (glint_pin.py:41-60)."""
-    src = Path(src).expanduser().resolve()
-    if not src.is_dir():
-        return [src]
-    if (src / "model.safetensors").is_file():
-        return [src / "model.safetensors"]
-    index = src / INDEX_NAME
-    if index.is_file():
-        names = sorted(set(json.loads(index.read_text())["weight_map"].values()))
-        missing = [n for n in names if not (src / n).is_file()]
-        if missing:
-            raise FileNotFoundError(f"{INDEX_NAME} names missing shards: {missing}")
-        return [src / n for n in names]
-    shards = sorted(src.glob("*.safetensors"))
-    if len(shards) != 1:
-        raise FileNotFoundError(f"need model.safetensors, {INDEX_NAME}, or exactly one .safetensors in {src}")
-    return shards
+    """The source's shard files in order (see ModelSource)."""
+    return ModelSource(src).files
 
 
+def close_all(files: Iterable[TensorFile]) -> None:
+    for tf in {id(f): f for f in files}.values():
+        tf.close()
+
+
+# ---------------------------------------------------------------------- the pin
 class Pin:
-    """A pin dir, every shard open, tensors looked up by name (glint_pinfile.py:10-61)."""
+    """An open pin directory: pin.json, every shard mapped, tensors found by name."""
 
     def __init__(self, root: Path):
         self.root = Path(root).expanduser().resolve()
-        pj = self.root / "pin.json"
-        if not pj.is_file():
-            raise FileNotFoundError(f"no pin.json in {self.root}")
-        self.meta = json.loads(pj.read_text())
-        index = self.root / INDEX_NAME
-        names = (sorted(set(json.loads(index.read_text())["weight_map"].values())) if index.is_file()
-                 else ["model.safetensors"])
-        self.shards: Dict[str, SafeTensorsFile] = {n: SafeTensorsFile(self.root / n) for n in names}
-        self.where: Dict[str, str] = {t: s for s, st in self.shards.items() for t in st.tensors}
+        meta = self.root / "pin.json"
+        if not meta.is_file():
+            raise FileNotFoundError(f"{self.root} is not a pin: pin.json is missing")
+        self.meta = json.loads(meta.read_text())
+        idx = self.root / INDEX_NAME
+        names = sorted(set(json.loads(idx.read_text())["weight_map"].values())) if idx.is_file() else [SINGLE_SHARD]
+        self.shards: Dict[str, TensorFile] = {s: TensorFile(self.root / s) for s in names}
+        self.where: Dict[str, str] = {t: s for s, tf in self.shards.items() for t in tf.entries}
 
     def close(self) -> None:
-        for st in self.shards.values():
-            st.close()
+        close_all(self.shards.values())
 
     def __enter__(self) -> "Pin":
         return self
@@ -106,409 +146,440 @@ class Pin:
     def __exit__(self, *exc) -> None:
         self.close()
 
-    def info(self, name: str):
-        return self.shards[self.where[name]].tensors[name]
+    def entry(self, name: str):
+        return self.shards[self.where[name]].entries[name]
 
-    def read(self, name: str) -> bytes:
-        return self.shards[self.where[name]].read_bytes(name)
+    def blob(self, name: str) -> bytes:
+        return self.shards[self.where[name]].blob(name)
 
     def stems(self) -> List[str]:
-        return [n[: -len(STATE_SUFFIX)] for n in self.where if n.endswith(STATE_SUFFIX)]
+        return [t[:-len(STATE_SUFFIX)] for t in self.where if t.endswith(STATE_SUFFIX)]
 
-    def state(self, stem: str) -> dict:
-        return json.loads(self.read(stem + STATE_SUFFIX).decode())
-
-    def cells(self) -> Optional[List[float]]:
-        if "_glint_cells" not in self.where:
-            return None
-        return np.frombuffer(self.read("_glint_cells"), dtype="<f4").tolist()
+    def table(self) -> Optional[List[float]]:
+        return np.frombuffer(self.blob(CELLS_TENSOR), dtype="<f4").tolist() if CELLS_TENSOR in self.where else None
 
     def module(self, stem: str) -> Tuple[dict, bytes, bytes, bytes]:
-        w = stem + ".weight"
-        return self.state(stem), self.read(w), self.read(w + ".glint_plug"), self.read(w + ".absmax")
+        """(state, hole bytes, plug bytes, absmax bytes); KeyError names a missing tensor."""
+        t = module_names(stem)
+        state = json.loads(self.blob(t["state"]).decode())
+        return state, self.blob(t["hole"]), self.blob(t["plug"]), self.blob(t["absmax"])
 
-    @staticmethod
-    def module_names(stem: str) -> Tuple[str, ...]:
-        w = stem + ".weight"
-        return (w, w + ".glint_plug", w + ".absmax", w + ".glint_state")
+    def dense_names(self) -> List[str]:
+        """Tensors carried over unchanged (not part of a module, not the cell table)."""
+        owned = {CELLS_TENSOR}
+        for stem in self.stems():
+            owned.update(module_names(stem).values())
+        return [t for t in self.where if t not in owned]
 
 
-# ------------------------------------------------------------------ device pipeline
-class _Device:
-    """Copy stream + compute stream; a job's outputs land in pinned host buffers and are
-    read once its completion event has fired."""
+# ------------------------------------------------------------ device execution
+class Ticket:
+    """Device work in flight: pinned host outputs, readable after `done` fires."""
+
+    def __init__(self, outputs: Dict[str, object], done):
+        self.outputs, self.done = outputs, done
+
+    def result(self) -> Dict[str, bytes]:
+        self.done.synchronize()
+        return {k: v.numpy().tobytes() for k, v in self.outputs.items()}
+
+
+class DeviceCodec:
+    """Encode and expand jobs on the GPU through the C ABI: host bytes are staged in pinned
+    memory and moved on a copy stream, the kernels run on a compute stream that waits for
+    the copy, and the outputs come back to pinned memory on the compute stream."""
 
     def __init__(self):
         try:
             import torch
-        except ImportError as e:  # pragma: no cover - torch is part of the image
-            raise RuntimeError("the pin tools need torch for device memory and streams") from e
+        except ImportError as exc:  # pragma: no cover - torch is part of the image
+            raise RuntimeError("the pin tools use torch for device memory and streams") from exc
         if not torch.cuda.is_available():
-            raise RuntimeError("GLINT encode/expand run on the GPU: no GPU is visible (this build has no host path)")
+            raise RuntimeError("the pin tools encode and expand on the GPU, and no GPU is visible")
         from . import glint_hip
-        glint_hip.encode_lib()  # raises if libglint_encode.so is missing
-        self.torch, self.H = torch, glint_hip
-        self.copy_s = torch.cuda.Stream()
-        self.comp_s = torch.cuda.Stream()
+        glint_hip.encode_lib()  # RuntimeError if libglint_encode.so is missing
+        self.torch, self.kern = torch, glint_hip
+        self.copy_stream, self.work_stream = torch.cuda.Stream(), torch.cuda.Stream()
 
-    def _to_device(self, raw) -> "object":
-        """Host bytes -> pinned staging -> device (uint8), ordered before the compute stream."""
+    def _upload(self, data):
         torch = self.torch
-        src = np.frombuffer(raw, dtype=np.uint8)
-        pinned = torch.empty(src.size, dtype=torch.uint8, pin_memory=True)
-        pinned.numpy()[:] = src  # host copy (pages the memory map in)
-        with torch.cuda.stream(self.copy_s):
-            dev = pinned.to("cuda", non_blocking=True)
-        self.comp_s.wait_stream(self.copy_s)
-        dev.record_stream(self.comp_s)
-        return dev
+        host = np.frombuffer(data, dtype=np.uint8)
+        staging = torch.empty(host.size, dtype=torch.uint8, pin_memory=True)
+        staging.numpy()[:] = host
+        with torch.cuda.stream(self.copy_stream):
+            on_device = staging.to("cuda", non_blocking=True)
+        self.work_stream.wait_stream(self.copy_stream)
+        on_device.record_stream(self.work_stream)
+        return on_device
 
-    def _to_host(self, t):
+    def _download(self, t):
         host = self.torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
         host.copy_(t, non_blocking=True)
         return host
 
-    def encode_job(self, dtype: str, raw, n: int, bs: int) -> dict:
-        torch, H = self.torch, self.H
-        dev = self._to_device(raw)
-        with torch.cuda.stream(self.comp_s):
+    def _finish(self, outs) -> Ticket:
+        staged = {k: self._download(v) for k, v in outs.items()}
+        done = self.torch.cuda.Event()
+        done.record(self.work_stream)
+        return Ticket(staged, done)
+
+    def encode(self, dtype: str, data, n: int, blocksize: int) -> Ticket:
+        """Outputs: hole, plug, absmax (f32) and rmse (f64, of the device expand against the source)."""
+        torch, k = self.torch, self.kern
+        raw = self._upload(data)
+        with torch.cuda.stream(self.work_stream):
             if dtype == "BF16":
-                src16 = dev.view(torch.int16)[:n]
-                hole, plug, am = H.encode_bf16(src16, bs, stream=self.comp_s)
-                w32 = src16.view(torch.bfloat16).float()
+                bits = raw.view(torch.int16)[:n]
+                hole, plug, am = k.encode_bf16(bits, blocksize, stream=self.work_stream)
+                src = bits.view(torch.bfloat16).float()
             else:
-                w32 = (dev.view(torch.float16)[:n].float() if dtype == "F16" else dev.view(torch.float32)[:n])
-                hole, plug, am = H.encode_f32(w32, bs, stream=self.comp_s)
+                src = raw.view(torch.float16)[:n].float() if dtype == "F16" else raw.view(torch.float32)[:n]
+                hole, plug, am = k.encode_f32(src, blocksize, stream=self.work_stream)
             if n:
-                rec = H.expand_f32(hole, plug, am, n, bs, stream=self.comp_s)
-                d = w32.double() - rec.double()
-                err = torch.sqrt(torch.mean(d * d)).reshape(1)
+                back = k.expand_f32(hole, plug, am, n, blocksize, stream=self.work_stream)
+                err = (src.double() - back.double()).square().mean().sqrt().reshape(1)
             else:
                 err = torch.zeros(1, dtype=torch.float64, device="cuda")
-            job = {"hole": self._to_host(hole), "plug": self._to_host(plug), "am": self._to_host(am),
-                   "rmse": self._to_host(err), "event": torch.cuda.Event()}
-            job["event"].record(self.comp_s)
-        return job
+            return self._finish({"hole": hole, "plug": plug, "absmax": am, "rmse": err})
 
-    def expand_job(self, hole: bytes, plug: bytes, am: bytes, n: int, bs: int, dtype: str) -> dict:
-        torch, H = self.torch, self.H
-        dh, dp, da = self._to_device(hole), self._to_device(plug), self._to_device(am)
-        with torch.cuda.stream(self.comp_s):
-            amf = da.view(torch.float32)
+    def expand(self, hole: bytes, plug: bytes, absmax: bytes, n: int, blocksize: int, dtype: str) -> Ticket:
+        """Output: out, the n weights as dtype (BF16 bits with the reference's rounding)."""
+        torch, k = self.torch, self.kern
+        dh, dp, da = self._upload(hole), self._upload(plug), self._upload(absmax)
+        with torch.cuda.stream(self.work_stream):
+            am = da.view(torch.float32)
             if dtype == "BF16":
-                out = H.expand_bf16(dh, dp, amf, n, bs, stream=self.comp_s).view(torch.int16)
+                out = k.expand_bf16(dh, dp, am, n, blocksize, stream=self.work_stream).view(torch.int16)
             else:
-                out = H.expand_f32(dh, dp, amf, n, bs, stream=self.comp_s)
-                if dtype == "F16":
-                    out = out.half()
-            job = {"out": self._to_host(out), "event": torch.cuda.Event()}
-            job["event"].record(self.comp_s)
-        return job
-
-    @staticmethod
-    def finish(job: dict) -> dict:
-        job["event"].synchronize()
-        return {k: (v.numpy().tobytes() if k != "event" else None) for k, v in job.items()}
+                out = k.expand_f32(dh, dp, am, n, blocksize, stream=self.work_stream)
+                out = out.half() if dtype == "F16" else out
+            return self._finish({"out": out})
 
 
-def _pipelined(dev_jobs: Iterator[Tuple[object, Optional[callable]]]):
-    """Run (key, make_job) pairs one deep: job i + 1 is staged and enqueued before job i is
-    waited on. make_job None passes the key through untouched, in order."""
-    pending = []
-    for key, make in dev_jobs:
-        pending.append((key, make() if make is not None else None))
-        while len(pending) > 1:
-            k, j = pending.pop(0)
-            yield k, (_Device.finish(j) if j is not None else None)
-    for k, j in pending:
-        yield k, (_Device.finish(j) if j is not None else None)
+def lookahead(work: Iterable[Tuple[object, Optional[Callable[[], Ticket]]]], depth: int = 1):
+    """Yield (key, result) in input order, starting up to `depth` jobs before waiting on
+    the oldest; a None job passes its key through with a None result."""
+    queue: deque = deque()
+    for key, start in work:
+        queue.append((key, start() if start else None))
+        if len(queue) > depth:
+            k, t = queue.popleft()
+            yield k, t.result() if t else None
+    while queue:
+        k, t = queue.popleft()
+        yield k, t.result() if t else None
 
 
-def _device_or_none():
-    try:
-        return _Device(), None
-    except RuntimeError as e:
-        return None, str(e)
+# -------------------------------------------------------------------- convert
+@dataclass
+class ShardPlan:
+    source: Path
+    out_name: str
+    tensors: List[str] = field(default_factory=list)
 
 
-# ------------------------------------------------------------------------ convert
-def _state_bytes(bs: int, shape, dtype: str) -> bytes:
-    return json.dumps({"quant_type": "glint", "blocksize": bs, "shape": list(shape), "src_dtype": dtype},
-                      separators=(",", ":")).encode()
+def _state_json(blocksize: int, shape, dtype: str) -> bytes:
+    return json.dumps({"quant_type": "glint", "blocksize": blocksize, "shape": [int(d) for d in shape],
+                       "src_dtype": dtype}, separators=(",", ":")).encode()
+
+
+def _copy_sidecars(src_dir: Path, out: Path, names: Iterable[str]) -> List[str]:
+    copied = []
+    for fname in names:
+        f = src_dir / fname
+        if f.is_file() and f.resolve() != (out / fname).resolve():
+            shutil.copyfile(f, out / fname)
+            copied.append(fname)
+    return copied
+
+
+def _stats(values: List[float]) -> Tuple[Optional[float], Optional[float]]:
+    return (sum(values) / len(values), max(values)) if values else (None, None)
 
 
 def convert(src: Path, out: Path, blocksize: int = 64, dry_run: bool = False, allow_cpu: bool = False,
             force_python: bool = False) -> dict:
-    """BF16/F16/F32 dense linears -> GLINT pin (glint_pin.py:87-193), encoded on the GPU.
-    allow_cpu and force_python exist for call compatibility: this build has no host
-    encoder, so force_python raises and allow_cpu changes nothing."""
-    if blocksize <= 0:
-        raise ValueError("blocksize must be positive")
+    """Dense BF16/F16/F32 linears of a model -> a GLINT pin, encoded on the GPU.
+    allow_cpu and force_python keep the reference's signature: there is no host encoder
+    here, so allow_cpu has no effect and force_python raises NotImplementedError."""
+    if blocksize < 1:
+        raise ValueError(f"blocksize {blocksize} is not positive")
     if force_python:
-        raise NotImplementedError("this build encodes on the GPU only (no pure-Python encoder)")
-    shards = resolve_shards(src)
+        raise NotImplementedError("no pure-Python encoder in this build: GLINT pins are encoded on the GPU")
+    source = ModelSource(src)
     out = Path(out).expanduser().resolve()
-    sharded = len(shards) > 1
+    plans: List[ShardPlan] = []
     linears: List[str] = []
-    keep: List[str] = []
-    for wf in shards:
-        with SafeTensorsFile(wf) as st:
-            for name, info in st.tensors.items():
-                dense = info.dtype in DENSE and len(info.shape) == 2
-                (linears if dense and name.endswith(".weight") and not _is_keep(name) else keep).append(name)
-    dev, why = _device_or_none()
+    n_dense = 0
+    for f in source.files:
+        plan = ShardPlan(f, f.name if source.sharded else SINGLE_SHARD)
+        with TensorFile(f) as tf:
+            for name, e in tf.entries.items():
+                plan.tensors.append(name)
+                if is_linear(name, e.dtype, e.shape):
+                    linears.append(name)
+                else:
+                    n_dense += 1
+        plans.append(plan)
+    try:
+        codec, why = DeviceCodec(), None
+    except RuntimeError as exc:
+        codec, why = None, str(exc)
     if dry_run:
-        return {"schema": "glint_pin_v1", "n_linears": len(linears), "n_keep": len(keep), "blocksize": blocksize,
-                "shards": [s.name for s in shards], "linears": linears, "hip": dev is not None, "numpy": True}
-    if dev is None:
-        raise RuntimeError(f"GLINT encode runs on the GPU (libglint_encode.so): {why}")
+        return {"schema": PIN_SCHEMA, "n_linears": len(linears), "n_keep": n_dense, "blocksize": blocksize,
+                "shards": [f.name for f in source.files], "linears": linears, "cuda": codec is not None,
+                "device": "hip", "numpy": True}
+    if codec is None:
+        raise RuntimeError(f"convert encodes on the GPU (libglint_encode.so): {why}")
+    to_encode = set(linears)
     out.mkdir(parents=True, exist_ok=True)
-    linear_set = set(linears)
-    reports, weight_map, total = [], {}, 0
-    for si, wf in enumerate(shards):
-        out_name = wf.name if sharded else "model.safetensors"
-        tensors = []
-        with SafeTensorsFile(wf) as st:
-            def jobs():
-                for name, info in st.tensors.items():
-                    if name not in linear_set:
-                        yield (name, info), None
+    modules, weight_map, total = [], {}, 0
+    for shard_no, plan in enumerate(plans):
+        items = []
+        with TensorFile(plan.source) as tf:
+            def work():
+                for name in plan.tensors:
+                    e = tf.entries[name]
+                    if name in to_encode:
+                        yield name, (lambda e=e, name=name: codec.encode(e.dtype, tf.buffer(name), e.count, blocksize))
                     else:
-                        n = numel_of(info.shape)
-                        yield (name, info), (lambda i=info, nm=name, nn=n: dev.encode_job(i.dtype, st.view(nm), nn,
-                                                                                         blocksize))
-            for (name, info), res in _pipelined(jobs()):
+                        yield name, None
+            for name, res in lookahead(work()):
+                e = tf.entries[name]
                 if res is None:
-                    tensors.append((name, info.dtype, info.shape, st.read_bytes(name)))
+                    items.append((name, e.dtype, e.shape, tf.blob(name)))
                     continue
-                stem = name[: -len(".weight")]
-                hole, plug, am = res["hole"], res["plug"], res["am"]
-                state = _state_bytes(blocksize, info.shape, info.dtype)
-                tensors += [(stem + ".weight", "U8", (len(hole), 1), hole),
-                            (stem + ".weight.glint_plug", "U8", (len(plug), 1), plug),
-                            (stem + ".weight.absmax", "F32", (len(am) // 4,), am),
-                            (stem + STATE_SUFFIX, "U8", (len(state),), state)]
-                backend = "hip_bf16" if info.dtype == "BF16" else "hip_f32"
-                err = float(np.frombuffer(res["rmse"], dtype=np.float64)[0])
-                reports.append({"src": stem, "rmse": err, "shape": list(info.shape), "backend": backend,
-                                "shard": out_name})
-        if si == 0:
-            tensors.append(("_glint_cells", "F32", (16, 16), codebook.cells_f32_bytes()))
-        for t in tensors:
-            weight_map[t[0]] = out_name
-            total += len(t[3])
-        write_safetensors(out / out_name, tensors, metadata={"format": "pt", "quantization": "glint"})
-        del tensors
-    if sharded:
-        index = {"metadata": {"total_size": total, "quantization": "glint"}, "weight_map": weight_map}
-        (out / INDEX_NAME).write_text(json.dumps(index, indent=2) + "\n")
-    src_dir = shards[0].parent
-    copied = []
-    for side in SIDECAR:
-        p = src_dir / side
-        if p.is_file() and p.resolve() != (out / side).resolve():
-            shutil.copyfile(p, out / side)
-            copied.append(side)
-    rated = [r["rmse"] for r in reports if r["rmse"] is not None]
-    backends = sorted({r["backend"] for r in reports})
-    pin = {"schema": "glint_pin_v1", "src": str(shards[0] if not sharded else src_dir), "dest": "glint",
-           "n_converted": len(reports), "blocksize": blocksize,
-           "rmse_mean": (sum(rated) / len(rated)) if rated else None, "rmse_max": max(rated) if rated else None,
-           "backend": backends[0] if len(backends) == 1 else ("mixed" if backends else None), "backends": backends,
-           "shards": [s.name for s in shards] if sharded else ["model.safetensors"], "sidecar": copied,
+                stem = name[:-len(".weight")]
+                t = module_names(stem)
+                state = _state_json(blocksize, e.shape, e.dtype)
+                items += [(t["hole"], "U8", (len(res["hole"]), 1), res["hole"]),
+                          (t["plug"], "U8", (len(res["plug"]), 1), res["plug"]),
+                          (t["absmax"], "F32", (len(res["absmax"]) // 4,), res["absmax"]),
+                          (t["state"], "U8", (len(state),), state)]
+                modules.append({"src": stem, "rmse": float(np.frombuffer(res["rmse"], np.float64)[0]),
+                                "shape": [int(d) for d in e.shape],
+                                "backend": "hip_bf16" if e.dtype == "BF16" else "hip_f32", "shard": plan.out_name})
+        if shard_no == 0:
+            items.append((CELLS_TENSOR, "F32", (16, 16), codebook.cells_f32_bytes()))
+        total += save(out / plan.out_name, items, meta={"format": "pt", "quantization": "glint"})
+        weight_map.update(dict.fromkeys((it[0] for it in items), plan.out_name))
+        del items
+    if source.sharded:
+        (out / INDEX_NAME).write_text(json.dumps({"metadata": {"total_size": total, "quantization": "glint"},
+                                                  "weight_map": weight_map}, indent=2) + "\n")
+    sidecars = _copy_sidecars(source.dir, out, SIDECAR)
+    mean, worst = _stats([m["rmse"] for m in modules if m["rmse"] is not None])
+    kinds = sorted({m["backend"] for m in modules})
+    pin = {"schema": PIN_SCHEMA, "src": str(source.dir if source.sharded else source.files[0]), "dest": "glint",
+           "n_converted": len(modules), "blocksize": blocksize, "rmse_mean": mean, "rmse_max": worst,
+           "backend": kinds[0] if len(kinds) == 1 else ("mixed" if kinds else None), "backends": kinds,
+           "shards": [f.name for f in source.files] if source.sharded else [SINGLE_SHARD], "sidecar": sidecars,
            "note": "hole = parent (NF4) cell, plug = child index; weight = GLINT_CELLS[hole][plug] * absmax"}
     (out / "pin.json").write_text(json.dumps(pin, indent=2) + "\n")
-    (out / "CONVERT_REPORT.json").write_text(json.dumps({"pin": pin, "modules": reports}, indent=2) + "\n")
-    return {"pin": pin, "modules": reports}
+    (out / "CONVERT_REPORT.json").write_text(json.dumps({"pin": pin, "modules": modules}, indent=2) + "\n")
+    return {"pin": pin, "modules": modules}
 
 
-# ------------------------------------------------------------------------- verify
-def _first_diff(a: bytes, b: bytes) -> Optional[int]:
-    if len(a) != len(b):
-        return min(len(a), len(b))
+# --------------------------------------------------------------------- verify
+def _first_mismatch(a: bytes, b: bytes) -> Optional[int]:
+    """Offset of the first differing byte (the shorter length if only lengths differ)."""
     if a == b:
         return None
-    return int(np.flatnonzero(np.frombuffer(a, np.uint8) != np.frombuffer(b, np.uint8))[0])
+    if len(a) != len(b):
+        return min(len(a), len(b))
+    return int(np.argmax(np.frombuffer(a, np.uint8) != np.frombuffer(b, np.uint8)))
+
+
+def _pin_level_failures(pin: Pin, cells: Optional[List[float]], n_modules: int) -> List[str]:
+    found = []
+    if pin.meta.get("schema") != PIN_SCHEMA:
+        found.append(f"schema={pin.meta.get('schema')!r}")
+    if cells is None:
+        found.append(f"{CELLS_TENSOR} missing")
+    elif cells != table_values():
+        found.append(f"{CELLS_TENSOR} is not the GLINT cell table")
+    declared = pin.meta.get("n_converted")
+    if declared is not None and declared != n_modules:
+        found.append(f"pin.json n_converted={declared}, the pin holds {n_modules} modules")
+    return found
+
+
+def _layout_problems(n: int, bs: int, hole: bytes, plug: bytes, absmax: bytes) -> List[str]:
+    planes, scales = (n + 1) // 2, -(-n // bs)
+    found = []
+    if (len(hole), len(plug)) != (planes, planes):
+        found.append(f"planes hold {len(hole)}/{len(plug)} bytes, {planes} expected")
+    if len(absmax) != 4 * scales:
+        found.append(f"{len(absmax) // 4} absmax values, {scales} expected")
+    if n % 2 and planes and (hole[-1] >> 4 or plug[-1] >> 4):
+        found.append("the pad nibble of an odd-length module is not zero")
+    return found
+
+
+def _parity(w: np.ndarray, bs: int, hole: bytes, plug: bytes, absmax: bytes) -> dict:
+    h2, p2, am2 = hc.encode_f32(w, bs)
+    out = {"hole_first_diff": _first_mismatch(hole, h2), "plug_first_diff": _first_mismatch(plug, p2),
+           "absmax_first_diff": _first_mismatch(absmax, am2.astype("<f4").tobytes())}
+    for key, mine, host in (("hole_bytes_differ", hole, h2), ("plug_bytes_differ", plug, p2)):
+        a, b = np.frombuffer(mine, np.uint8), np.frombuffer(host, np.uint8)
+        common = min(a.size, b.size)  # bytes past the shorter plane count as differing
+        out[key] = int(np.count_nonzero(a[:common] != b[:common])) + abs(a.size - b.size)
+    return out
 
 
 def verify(pin_dir: Path, src: Optional[Path] = None, parity: bool = False, cuda: bool = False) -> dict:
-    """Layout of every module, optional RMSE against the source, and the two gates
-    (glint_verify.py:48-144). Exit status of the CLI: 1 on any failure."""
+    """Check a pin: its schema and cell table, each module's layout; with src, each
+    module's RMSE against the source weights; the --cuda gate (device expand against the
+    host expand, max |diff| < 1e-5) and the --parity gate (the pin's bytes against a host
+    re-encode of the source). The report's "ok" is False on any failure."""
     if parity and src is None:
-        raise ValueError("--parity needs --src")
-    dev = _Device() if cuda else None
-    fails, modules = [], []
+        raise ValueError("the parity gate re-encodes the source: pass src")
+    codec = DeviceCodec() if cuda else None
+    rows: List[dict] = []
     with Pin(pin_dir) as pin:
-        if pin.meta.get("schema") != "glint_pin_v1":
-            fails.append(f"schema={pin.meta.get('schema')!r}")
-        cells = pin.cells()
-        if cells is None:
-            fails.append("_glint_cells missing")
-        elif cells != np.frombuffer(codebook.cells_f32_bytes(), dtype="<f4").tolist():
-            fails.append("_glint_cells differs from the GLINT table")
-        src_ix: Dict[str, SafeTensorsFile] = {}
-        if src is not None:
-            for wf in resolve_shards(src):
-                st = SafeTensorsFile(wf)
-                for name in st.tensors:
-                    src_ix[name] = st
+        cells = pin.table()
         stems = pin.stems()
-        if pin.meta.get("n_converted") not in (None, len(stems)):
-            fails.append(f"pin.json n_converted={pin.meta.get('n_converted')} but {len(stems)} modules")
-        for stem in stems:
-            row = {"module": stem, "ok": True, "problems": []}
-            try:
-                state, hole, plug, am = pin.module(stem)
-            except KeyError as e:
-                row["problems"].append(f"missing tensor {e}")
-                row["ok"] = False
-                modules.append(row)
-                continue
-            n = numel_of(tuple(state["shape"]))
-            bs = int(state["blocksize"])
-            npk, nam = (n + 1) // 2, (n + bs - 1) // bs
-            if len(hole) != npk or len(plug) != npk:
-                row["problems"].append(f"hole/plug bytes {len(hole)}/{len(plug)} != {npk}")
-            if len(am) != 4 * nam:
-                row["problems"].append(f"absmax {len(am) // 4} floats != {nam}")
-            if n & 1 and npk and ((hole[-1] >> 4) or (plug[-1] >> 4)):
-                row["problems"].append("odd n but pad nibble is not zero")
-            amf = np.frombuffer(am, dtype="<f4") if len(am) == 4 * nam else None
-            if not row["problems"] and cuda:
-                host = HC.expand(hole, plug, amf, n, bs, cells)
-                got = np.frombuffer(_Device.finish(dev.expand_job(hole, plug, am, n, bs, "F32"))["out"], dtype="<f4")
-                row["cuda_expand_max_abs"] = float(np.max(np.abs(got - host))) if n else 0.0
-                if not row["cuda_expand_max_abs"] < CUDA_EXPAND_TOL:
-                    row["problems"].append(f"cuda expand max_abs {row['cuda_expand_max_abs']:.3g} >= {CUDA_EXPAND_TOL}")
-            if not row["problems"] and src is not None:
-                name = stem + ".weight"
-                st = src_ix.get(name)
-                if st is None:
-                    row["problems"].append("not in --src")
-                else:
-                    info = st.tensors[name]
-                    if list(info.shape) != list(state["shape"]):
-                        row["problems"].append(f"shape {state['shape']} != src {list(info.shape)}")
-                    else:
-                        w = HC.dense_to_f32(info.dtype, st.view(name), n)
-                        rec = HC.expand(hole, plug, amf, n, bs, cells)
-                        row["rmse"] = HC.rmse(w, rec)
-                        ref = float(np.sqrt(np.mean(w.astype(np.float64) ** 2))) if n else 0.0
-                        row["rel_rmse"] = row["rmse"] / ref if ref else 0.0
-                        if not np.all(np.isfinite(rec[np.isfinite(w)])):
-                            row["problems"].append("non-finite reconstruction of finite weights")
-                        if parity:
-                            h2, p2, am2 = HC.encode_f32(w, bs)
-                            par = {"hole_first_diff": _first_diff(hole, h2), "plug_first_diff": _first_diff(plug, p2),
-                                   "absmax_first_diff": _first_diff(am, am2.astype("<f4").tobytes())}
-                            hb, pb = np.frombuffer(hole, np.uint8), np.frombuffer(plug, np.uint8)
-                            par["hole_bytes_differ"] = int(np.count_nonzero(hb != np.frombuffer(h2, np.uint8)))
-                            par["plug_bytes_differ"] = int(np.count_nonzero(pb != np.frombuffer(p2, np.uint8)))
-                            row["parity"] = par
-                            if any(v is not None for k, v in par.items() if k.endswith("first_diff")):
-                                row["problems"].append("host re-encode bytes differ")
-            row["ok"] = not row["problems"]
-            if not row["problems"]:
-                del row["problems"]
-            modules.append(row)
-        for st in {id(s): s for s in src_ix.values()}.values():
-            st.close()
+        failures = _pin_level_failures(pin, cells, len(stems))
+        source = ModelSource(src).lookup() if src is not None else {}
+        try:
+            for stem in stems:
+                rows.append(_check_module(pin, stem, cells, source, codec, parity))
+        finally:
+            close_all(source.values())
         backend = pin.meta.get("backend")
-    rated = [m["rmse"] for m in modules if "rmse" in m]
-    bad = [m["module"] for m in modules if not m["ok"]]
-    return {"schema": "glint_verify_v1", "pin": str(Path(pin_dir).expanduser().resolve()), "backend": backend,
-            "n_modules": len(modules), "n_failed": len(bad), "rmse_mean": sum(rated) / len(rated) if rated else None,
-            "rmse_max": max(rated) if rated else None, "parity_checked": parity, "cuda_expand_checked": cuda,
-            "ok": not fails and not bad, "failures": fails + [f"module {b}" for b in bad], "modules": modules}
+    rated = [r["rmse"] for r in rows if "rmse" in r]
+    mean, worst = _stats(rated)
+    bad = [r["module"] for r in rows if not r["ok"]]
+    return {"schema": VERIFY_SCHEMA, "pin": str(Path(pin_dir).expanduser().resolve()), "backend": backend,
+            "n_modules": len(rows), "n_failed": len(bad), "rmse_mean": mean, "rmse_max": worst,
+            "parity_checked": parity, "cuda_expand_checked": cuda, "ok": not failures and not bad,
+            "failures": failures + [f"module {m}" for m in bad], "modules": rows}
 
 
-# -------------------------------------------------------------------------- unpin
+def _check_module(pin: Pin, stem: str, cells, source: Dict[str, TensorFile], codec: Optional[DeviceCodec],
+                  parity: bool) -> dict:
+    row: dict = {"module": stem}
+    problems: List[str] = []
+    try:
+        state, hole, plug, absmax = pin.module(stem)
+    except KeyError as exc:
+        return {"module": stem, "ok": False, "problems": [f"tensor {exc} is missing"]}
+    n, bs = element_count(state["shape"]), int(state["blocksize"])
+    problems += _layout_problems(n, bs, hole, plug, absmax)
+    scales = np.frombuffer(absmax, dtype="<f4")
+    if not problems and codec is not None:
+        host = hc.expand(hole, plug, scales, n, bs, cells)
+        device = np.frombuffer(codec.expand(hole, plug, absmax, n, bs, "F32").result()["out"], dtype="<f4")
+        gap = float(np.abs(device - host).max()) if n else 0.0
+        row["cuda_expand_max_abs"] = gap
+        if not gap < EXPAND_GATE:
+            problems.append(f"device expand differs from the host expand by {gap:.3g} (gate {EXPAND_GATE})")
+    if not problems and source:
+        name = module_names(stem)["hole"]
+        tf = source.get(name)
+        if tf is None:
+            problems.append("the source has no such tensor")
+        elif list(tf.entries[name].shape) != list(state["shape"]):
+            problems.append(f"source shape {list(tf.entries[name].shape)}, pin shape {state['shape']}")
+        else:
+            w = hc.to_f32(tf.entries[name].dtype, tf.buffer(name), n)
+            rec = hc.expand(hole, plug, scales, n, bs, cells)
+            row["rmse"] = hc.rms_error(w, rec)
+            scale = hc.rms_error(w, np.zeros_like(w))
+            row["rel_rmse"] = row["rmse"] / scale if scale else 0.0
+            if not np.isfinite(rec[np.isfinite(w)]).all():
+                problems.append("finite source weights reconstruct to non-finite values")
+            if parity:
+                row["parity"] = _parity(w, bs, hole, plug, absmax)
+                if any(v is not None for k, v in row["parity"].items() if k.endswith("_first_diff")):
+                    problems.append("the pin's bytes differ from a host re-encode of the source")
+    row["ok"] = not problems
+    if problems:
+        row["problems"] = problems
+    return row
+
+
+# ---------------------------------------------------------------------- unpin
 def unpin(pin_dir: Path, out: Path, dtype: str = "BF16") -> dict:
-    """Pin -> dense safetensors with the original names and shapes (glint_unpin.py:45-85),
-    expanded on the GPU with the pin's own table."""
-    if dtype not in DENSE:
-        raise ValueError(f"dtype must be one of {DENSE}")
+    """A pin -> dense safetensors under the original tensor names and shapes (the GLINT
+    reconstruction, expanded on the GPU), plus the pin's sidecar files."""
+    if dtype not in DENSE_DTYPES:
+        raise ValueError(f"unpin writes one of {', '.join(DENSE_DTYPES)}, not {dtype}")
     out = Path(out).expanduser().resolve()
     with Pin(pin_dir) as pin:
-        if pin.meta.get("schema") != "glint_pin_v1":
-            raise ValueError(f"not a glint_pin_v1 pin: {pin.meta.get('schema')}")
-        cells = pin.cells()
-        if cells is not None and cells != np.frombuffer(codebook.cells_f32_bytes(), dtype="<f4").tolist():
-            raise ValueError("the pin's _glint_cells differ from the table the device kernels use")
-        dev = _Device()
+        if pin.meta.get("schema") != PIN_SCHEMA:
+            raise ValueError(f"{pin.root} holds schema {pin.meta.get('schema')!r}, not {PIN_SCHEMA}")
+        cells = pin.table()
+        if cells is not None and cells != table_values():
+            raise ValueError(f"{pin.root}: its {CELLS_TENSOR} is not the table the device kernels expand with")
+        codec = DeviceCodec()
         out.mkdir(parents=True, exist_ok=True)
-        per_shard: Dict[str, list] = {s: [] for s in pin.shards}
-        stem_of = {stem + ".weight": stem for stem in pin.stems()}
-        owned = set()
-        for stem in pin.stems():
-            owned.update(pin.module_names(stem))
+        hole_of = {module_names(s)["hole"]: s for s in pin.stems()}
+        carried = set(pin.dense_names())
 
-        def jobs():
-            for name, shard in pin.where.items():
-                if name in stem_of:
-                    state, hole, plug, am = pin.module(stem_of[name])
-                    n, bs = numel_of(tuple(state["shape"])), int(state["blocksize"])
-                    yield (name, shard, state), (lambda h=hole, p=plug, a=am, nn=n, b=bs:
-                                                 dev.expand_job(h, p, a, nn, b, dtype))
-                elif name not in owned and name != "_glint_cells":
-                    yield (name, shard, None), None
+        def work():
+            for name in pin.where:
+                if name in hole_of:
+                    state, hole, plug, absmax = pin.module(hole_of[name])
+                    n, bs = element_count(state["shape"]), int(state["blocksize"])
+                    yield (name, state), (lambda h=hole, p=plug, a=absmax, n=n, bs=bs: codec.expand(h, p, a, n, bs,
+                                                                                                     dtype))
+                elif name in carried:
+                    yield (name, None), None
 
-        n_expanded = 0
-        for (name, shard, state), res in _pipelined(jobs()):
-            if res is not None:
-                per_shard[shard].append((name, dtype, tuple(state["shape"]), res["out"]))
-                n_expanded += 1
+        shards: Dict[str, list] = {s: [] for s in pin.shards}
+        expanded = 0
+        for (name, state), res in lookahead(work()):
+            if res is None:
+                e = pin.entry(name)
+                shards[pin.where[name]].append((name, e.dtype, e.shape, pin.blob(name)))
             else:
-                info = pin.info(name)
-                per_shard[shard].append((name, info.dtype, info.shape, pin.read(name)))
+                shards[pin.where[name]].append((name, dtype, tuple(state["shape"]), res["out"]))
+                expanded += 1
         weight_map, total = {}, 0
-        for shard, tensors in per_shard.items():
-            write_safetensors(out / shard, tensors, metadata={"format": "pt", "unpinned_from": "glint"})
-            for t in tensors:
-                weight_map[t[0]] = shard
-                total += len(t[3])
-        if len(per_shard) > 1:
+        for shard, items in shards.items():
+            total += save(out / shard, items, meta={"format": "pt", "unpinned_from": "glint"})
+            weight_map.update(dict.fromkeys((it[0] for it in items), shard))
+        if len(shards) > 1:
             (out / INDEX_NAME).write_text(json.dumps({"metadata": {"total_size": total}, "weight_map": weight_map},
                                                      indent=2) + "\n")
-        for side in pin.meta.get("sidecar", []):
-            p = pin.root / side
-            if p.is_file():
-                shutil.copyfile(p, out / side)
-    return {"out": str(out), "dtype": dtype, "n_expanded": n_expanded, "shards": list(per_shard)}
+        _copy_sidecars(pin.root, out, pin.meta.get("sidecar", []))
+    return {"out": str(out), "dtype": dtype, "n_expanded": expanded, "shards": list(shards)}
 
 
-# ---------------------------------------------------------------------------- CLI
+# ------------------------------------------------------------------------ CLI
 def main(argv=None) -> int:
-    ap = argparse.ArgumentParser(description="GLINT pin tools (MI355X device path)")
+    ap = argparse.ArgumentParser(description="GLINT pin tools on the GPU")
     sub = ap.add_subparsers(dest="cmd", required=True)
-    c = sub.add_parser("convert", help="BF16/F16/F32 -> hole+plug pin")
-    c.add_argument("--src", required=True)
+    c = sub.add_parser("convert", help="dense BF16/F16/F32 linears -> hole + plug pin")
+    c.add_argument("--src", required=True, help=".safetensors file, model dir or sharded model dir")
     c.add_argument("--out", required=True)
     c.add_argument("--blocksize", type=int, default=64)
     c.add_argument("--dry-run", action="store_true")
-    v = sub.add_parser("verify", help="check a pin; exit 1 on any failure")
+    c.add_argument("--allow-cpu", action="store_true", help="accepted; this build has no host encoder")
+    v = sub.add_parser("verify", help="check a pin; exit status 1 if any check fails")
     v.add_argument("--pin", required=True)
-    v.add_argument("--src")
-    v.add_argument("--parity", action="store_true", help="pin bytes vs a host re-encode of --src")
-    v.add_argument("--cuda", action="store_true", help="device expand vs host expand, max_abs < 1e-5")
-    v.add_argument("--out")
-    v.add_argument("--quiet", action="store_true")
+    v.add_argument("--src", help="source model, for per-module RMSE")
+    v.add_argument("--parity", action="store_true", help="compare the pin's bytes with a host re-encode of --src")
+    v.add_argument("--cuda", action="store_true", help="compare the device expand with the host expand (< 1e-5)")
+    v.add_argument("--out", help="write the full report here")
+    v.add_argument("--quiet", action="store_true", help="leave the per-module rows out of stdout")
     u = sub.add_parser("unpin", help="pin -> dense safetensors")
     u.add_argument("--pin", required=True)
     u.add_argument("--out", required=True)
-    u.add_argument("--dtype", default="BF16", choices=DENSE)
+    u.add_argument("--dtype", default="BF16", choices=DENSE_DTYPES)
     a = ap.parse_args(argv)
     if a.cmd == "convert":
-        got = convert(Path(a.src), Path(a.out), a.blocksize, a.dry_run)
-        print(json.dumps(got if a.dry_run else got["pin"], indent=2))
+        res = convert(Path(a.src), Path(a.out), a.blocksize, a.dry_run, a.allow_cpu)
+        print(json.dumps(res if a.dry_run else res["pin"], indent=2))
         return 0
     if a.cmd == "verify":
-        got = verify(Path(a.pin), Path(a.src) if a.src else None, a.parity, a.cuda)
-        text = json.dumps(got, indent=2) + "\n"
+        rep = verify(Path(a.pin), Path(a.src) if a.src else None, a.parity, a.cuda)
         if a.out:
-            Path(a.out).write_text(text)
-        print(json.dumps({k: v for k, v in got.items() if k != "modules"} if a.quiet else got, indent=2))
-        return 0 if got["ok"] else 1
+            Path(a.out).write_text(json.dumps(rep, indent=2) + "\n")
+        shown = {k: v for k, v in rep.items() if k != "modules"} if a.quiet else rep
+        print(json.dumps(shown, indent=2))
+        return 0 if rep["ok"] else 1
     print(json.dumps(unpin(Path(a.pin), Path(a.out), a.dtype), indent=2))
     return 0
 

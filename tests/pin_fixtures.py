@@ -9,7 +9,7 @@ from pathlib import Path
 
 import numpy as np
 
-from glint_amd.safetensors_io import write_safetensors
+from glint_amd.tensorfile import save
 
 
 def gauss(n, seed, scale=0.02):
@@ -48,7 +48,7 @@ def write_model(root: Path, shards: dict, index: bool = True) -> None:
     root.mkdir(parents=True, exist_ok=True)
     weight_map = {}
     for shard, tensors in shards.items():
-        write_safetensors(str(root / shard), tensors)
+        save(root / shard, tensors)
         for t in tensors:
             weight_map[t[0]] = shard
     if index:

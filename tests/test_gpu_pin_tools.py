@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 from glint_amd import pin_tools as P
-from glint_amd.safetensors_io import SafeTensorsFile, write_safetensors
+from glint_amd.tensorfile import TensorFile, save
 from tests.gpu_util import torch_cuda
 from tests.pin_fixtures import bf16_bytes, dense_f32, toy_shards, write_model
 
@@ -63,9 +63,9 @@ def test_convert_writes_the_oracle_pin(oracle):
                 row = next(m for m in report["modules"] if m["src"] == stem)
                 assert row["rmse"] == pytest.approx(want, rel=1e-9, abs=1e-12), stem
                 assert row["shard"] == shard
-        with P.Pin(pin_dir) as p, SafeTensorsFile(src / "model-00001-of-00002.safetensors") as s:
-            assert p.read("layers.0.norm.weight") == s.read_bytes("layers.0.norm.weight")
-            assert p.info("layers.0.q.weight").shape == (512, 1)
+        with P.Pin(pin_dir) as p, TensorFile(src / "model-00001-of-00002.safetensors") as s:
+            assert p.blob("layers.0.norm.weight") == s.blob("layers.0.norm.weight")
+            assert p.entry("layers.0.q.weight").shape == (512, 1)
 
 
 def test_verify_gates_and_unpin(oracle):
@@ -91,20 +91,20 @@ def test_verify_gates_and_unpin(oracle):
                     hh, pp = np.frombuffer(hole, np.uint8), np.frombuffer(plug, np.uint8)
                     aa = np.frombuffer(am, np.float32)
                     shard = pin.where[stem + ".weight"]
-                    with SafeTensorsFile(back / shard) as st:
-                        info = st.tensors[stem + ".weight"]
+                    with TensorFile(back / shard) as st:
+                        info = st.entries[stem + ".weight"]
                         assert info.dtype == dt and list(info.shape) == state["shape"]
-                        got = st.read_bytes(stem + ".weight")
-                        assert "_glint_cells" not in st.tensors
+                        got = st.blob(stem + ".weight")
+                        assert "_glint_cells" not in st.entries
                     if dt == "BF16":
                         want = oracle.expand_bf16(hh, pp, aa, n, 64).tobytes()
                     else:
                         f = oracle.expand_f32(hh, pp, aa, n, 64)
                         want = (f if dt == "F32" else f.astype("<f2")).tobytes()
                     assert got == want, (dt, stem)
-        with SafeTensorsFile(Path(td) / "back_BF16" / "model-00002-of-00002.safetensors") as st, \
-                SafeTensorsFile(src / "model-00002-of-00002.safetensors") as s:
-            assert st.read_bytes("layers.1.up.bias") == s.read_bytes("layers.1.up.bias")
+        with TensorFile(Path(td) / "back_BF16" / "model-00002-of-00002.safetensors") as st, \
+                TensorFile(src / "model-00002-of-00002.safetensors") as s:
+            assert st.blob("layers.1.up.bias") == s.blob("layers.1.up.bias")
 
 
 def test_files_load_in_the_official_reader():
@@ -161,9 +161,9 @@ def test_pipeline_on_a_larger_model(oracle):
         t0 = time.perf_counter()
         P.unpin(pin_dir, Path(td) / "back")
         print(f"pin tools: unpin {mb:.0f} MB BF16 in {time.perf_counter() - t0:.2f} s", flush=True)
-        with SafeTensorsFile(Path(td) / "back" / "model-00002-of-00002.safetensors") as st:
+        with TensorFile(Path(td) / "back" / "model-00002-of-00002.safetensors") as st:
             state, hole, plug, am = _module_bytes(pin_dir, "layers.5.mlp")
             n = 4096 * 4096
             want = oracle.expand_bf16(np.frombuffer(hole, np.uint8), np.frombuffer(plug, np.uint8),
                                       np.frombuffer(am, np.float32), n, 64)
-            assert st.read_bytes("layers.5.mlp.weight") == want.tobytes()
+            assert st.blob("layers.5.mlp.weight") == want.tobytes()

@@ -1,10 +1,10 @@
-"""CPU checks of the pin tools (glint_amd.pin_tools, safetensors_io, host_codec).
+"""CPU checks of the pin tools (glint_amd.pin_tools, glint_amd.tensorfile, glint_amd.host_codec).
 
-The file format is checked against the safetensors spec and the official reader. The
-host codec that verify's gates use is pinned against the oracle. Dry-run plans, layout
-checks and the parity gate run on a pin assembled here from oracle bytes. Encoding and
-expanding need the GPU: without one, convert and unpin must refuse (tested here); with
-one they are tested in test_gpu_pin_tools.py.
+The container format is checked against the safetensors specification and the official
+reader. The host codec that verify's gates use is pinned against the oracle. Dry-run
+plans, layout checks and the parity gate run on a pin assembled here from oracle bytes.
+Encoding and expanding need the GPU: without one, convert and unpin must refuse (tested
+here); with one they are tested in test_gpu_pin_tools.py.
 """
 import json
 import struct
@@ -15,29 +15,31 @@ import numpy as np
 import pytest
 
 from glint_amd import codebook, host_codec, pin_tools as P
-from glint_amd.safetensors_io import SafeTensorsFile, write_safetensors
+from glint_amd.tensorfile import TensorFile, save
 from tests.pin_fixtures import bf16_bytes, dense_f32, gauss, toy_shards, write_model
 
 
-def test_safetensors_offsets_are_contiguous_and_header_aligned():
-    """Spec: the byte buffer is fully indexed with no holes (test_glint_tools.py:229-238);
-    the data section starts 8-byte aligned."""
+def test_container_offsets_are_contiguous_and_header_aligned():
+    """Specification: the data section is fully indexed with no holes
+    (test_glint_tools.py:229-238) and starts on an 8-byte boundary."""
     with tempfile.TemporaryDirectory() as td:
         f = Path(td) / "m.safetensors"
-        write_safetensors(f, [("a", "U8", (3,), b"abc"), ("b", "F32", (1,), b"\0" * 4), ("c", "U8", (1,), b"z")],
-                          metadata={"format": "pt"})
+        n = save(f, [("a", "U8", (3,), b"abc"), ("b", "F32", (1,), b"\0" * 4), ("c", "U8", (1,), b"z")],
+                 meta={"format": "pt"})
+        assert n == 8
         raw = f.read_bytes()
         (hlen,) = struct.unpack("<Q", raw[:8])
         assert (8 + hlen) % 8 == 0
         header = json.loads(raw[8:8 + hlen])
         assert list(header)[0] == "__metadata__" and header["__metadata__"] == {"format": "pt"}
-        with SafeTensorsFile(f) as st:
-            spans = sorted(i.data_offsets for i in st.tensors.values())
-            assert spans[0][0] == 0
-            assert all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
-            assert st.data_start + spans[-1][1] == f.stat().st_size
-            assert st.read_bytes("c") == b"z" and st.read_bytes("a") == b"abc"
-            assert st.metadata == {"format": "pt"}
+        spans = sorted(tuple(v["data_offsets"]) for k, v in header.items() if k != "__metadata__")
+        assert spans[0][0] == 0 and all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
+        assert 8 + hlen + spans[-1][1] == len(raw)
+        with TensorFile(f) as tf:
+            assert tf.blob("c") == b"z" and tf.blob("a") == b"abc" and tf.meta == {"format": "pt"}
+            assert tf.entries["b"].count == 1 and tf.array("a", np.uint8).tolist() == [97, 98, 99]
+            assert list(tf) == ["a", "b", "c"]
+        assert [p.name for p in Path(td).iterdir()] == ["m.safetensors"]  # no temporary file left
 
 
 def test_official_reader_accepts_our_files():
@@ -45,20 +47,35 @@ def test_official_reader_accepts_our_files():
     with tempfile.TemporaryDirectory() as td:
         f = Path(td) / "m.safetensors"
         vals = np.arange(12, dtype=np.float32)
-        write_safetensors(f, [("w", "F32", (3, 4), vals.tobytes()), ("u", "U8", (5, 1), bytes(range(5)))])
+        save(f, [("w", "F32", (3, 4), vals.tobytes()), ("u", "U8", (5, 1), bytes(range(5)))])
         with safetensors.safe_open(str(f), "np") as h:
             assert np.array_equal(h.get_tensor("w"), vals.reshape(3, 4))
             assert h.get_tensor("u").reshape(-1).tolist() == [0, 1, 2, 3, 4]
 
 
-def test_reader_rejects_out_of_file_offsets():
+def _raw_file(f: Path, header: dict, data: bytes) -> None:
+    hb = json.dumps(header).encode()
+    hb += b" " * ((-(len(hb) + 8)) % 8)
+    f.write_bytes(struct.pack("<Q", len(hb)) + hb + data)
+
+
+def test_reader_rejects_bad_ranges_and_writer_bad_sizes():
     with tempfile.TemporaryDirectory() as td:
         f = Path(td) / "bad.safetensors"
-        hb = json.dumps({"x": {"dtype": "U8", "shape": [10], "data_offsets": [0, 10]}}).encode()
-        hb += b" " * ((-(len(hb) + 8)) % 8)
-        f.write_bytes(struct.pack("<Q", len(hb)) + hb + b"abc")
-        with pytest.raises(ValueError):
-            SafeTensorsFile(f)
+        _raw_file(f, {"x": {"dtype": "U8", "shape": [10], "data_offsets": [0, 10]}}, b"abc")
+        with pytest.raises(ValueError, match="spans"):
+            TensorFile(f)
+        _raw_file(f, {"x": {"dtype": "F32", "shape": [2], "data_offsets": [0, 4]}}, b"abcd")
+        with pytest.raises(ValueError, match="holds"):
+            TensorFile(f)
+        f.write_bytes(struct.pack("<Q", 1 << 40) + b"{}")
+        with pytest.raises(ValueError, match="does not fit"):
+            TensorFile(f)
+        with pytest.raises(ValueError, match="bytes for shape"):
+            save(Path(td) / "w.safetensors", [("y", "F32", (3,), b"\0" * 8)])
+        with pytest.raises(ValueError, match="not a safetensors dtype"):
+            save(Path(td) / "w.safetensors", [("y", "Q4", (3,), b"\0" * 3)])
+        assert not (Path(td) / "w.safetensors").exists()
 
 
 def test_resolve_shards_rules():
@@ -69,9 +86,9 @@ def test_resolve_shards_rules():
         assert [p.name for p in got] == sorted(toy_shards())
         one = root / "one"
         one.mkdir()
-        write_safetensors(one / "weights.safetensors", [("a.weight", "BF16", (2, 64), bf16_bytes(gauss(128, 7)))])
+        save(one / "weights.safetensors", [("a.weight", "BF16", (2, 64), bf16_bytes(gauss(128, 7)))])
         assert [p.name for p in P.resolve_shards(one)] == ["weights.safetensors"]
-        write_safetensors(one / "other.safetensors", [("b", "U8", (1,), b"x")])
+        save(one / "other.safetensors", [("b", "U8", (1,), b"x")])
         with pytest.raises(FileNotFoundError):
             P.resolve_shards(one)
         (root / "sharded" / "model-00002-of-00002.safetensors").unlink()
@@ -118,8 +135,12 @@ def test_host_codec_matches_the_oracle(oracle):
     assert h == oh.tobytes() and p == op.tobytes() and am.tobytes() == oam.tobytes()
     rec = host_codec.expand(h, p, am, w.size, 64)
     assert rec.tobytes() == oracle.expand_f32(oh, op, oam, w.size, 64).tobytes()
+    every = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)  # every bf16 pattern, specials included
+    h, p, am = host_codec.encode_f32(every, 64)
+    oh, op, oam = oracle.encode_f32(every, 64)
+    assert h == oh.tobytes() and p == op.tobytes() and am.tobytes() == oam.tobytes()
     for bs in (23, 128):
-        h, p, am = host_codec.encode_f32(w, bs, chunk_blocks=3)
+        h, p, am = host_codec.encode_f32(w, bs, block_chunk=3)
         oh, op, oam = oracle.encode_f32(w, bs)
         assert h == oh.tobytes() and p == op.tobytes() and am.tobytes() == oam.tobytes()
 
@@ -131,31 +152,31 @@ def test_host_codec_tables_are_the_pinned_ones():
 
 # ------------------------------------------- verify on a pin assembled from oracle bytes
 def _assemble_pin(oracle, src: Path, pin: Path, bs: int = 64):
-    """A pin written the way convert writes it, with the oracle's encode."""
+    """A pin laid out as convert lays it out, with the oracle's encode."""
     shards = P.resolve_shards(src)
     pin.mkdir(parents=True)
     weight_map, n_conv = {}, 0
     for si, wf in enumerate(shards):
-        tensors = []
-        with SafeTensorsFile(wf) as st:
-            for name, info in st.tensors.items():
-                raw = st.read_bytes(name)
-                if info.dtype in P.DENSE and len(info.shape) == 2 and name.endswith(".weight") and not P._is_keep(name):
-                    h, p, am = oracle.encode_f32(dense_f32(info.dtype, raw), bs)
-                    stem = name[:-7]
-                    state = P._state_bytes(bs, info.shape, info.dtype)
-                    tensors += [(stem + ".weight", "U8", (h.size, 1), h.tobytes()),
-                                (stem + ".weight.glint_plug", "U8", (p.size, 1), p.tobytes()),
-                                (stem + ".weight.absmax", "F32", (am.size,), am.tobytes()),
-                                (stem + ".weight.glint_state", "U8", (len(state),), state)]
+        items = []
+        with TensorFile(wf) as tf:
+            for name, e in tf.entries.items():
+                raw = tf.blob(name)
+                if P.is_linear(name, e.dtype, e.shape):
+                    h, p, am = oracle.encode_f32(dense_f32(e.dtype, raw), bs)
+                    t = P.module_names(name[:-7])
+                    state = json.dumps({"quant_type": "glint", "blocksize": bs, "shape": list(e.shape),
+                                        "src_dtype": e.dtype}, separators=(",", ":")).encode()
+                    items += [(t["hole"], "U8", (h.size, 1), h.tobytes()),
+                              (t["plug"], "U8", (p.size, 1), p.tobytes()),
+                              (t["absmax"], "F32", (am.size,), am.tobytes()),
+                              (t["state"], "U8", (len(state),), state)]
                     n_conv += 1
                 else:
-                    tensors.append((name, info.dtype, info.shape, raw))
+                    items.append((name, e.dtype, e.shape, raw))
         if si == 0:
-            tensors.append(("_glint_cells", "F32", (16, 16), codebook.cells_f32_bytes()))
-        for t in tensors:
-            weight_map[t[0]] = wf.name
-        write_safetensors(pin / wf.name, tensors, metadata={"format": "pt", "quantization": "glint"})
+            items.append(("_glint_cells", "F32", (16, 16), codebook.cells_f32_bytes()))
+        weight_map.update(dict.fromkeys((it[0] for it in items), wf.name))
+        save(pin / wf.name, items, meta={"format": "pt", "quantization": "glint"})
     (pin / P.INDEX_NAME).write_text(json.dumps({"metadata": {}, "weight_map": weight_map}))
     (pin / "pin.json").write_text(json.dumps({"schema": "glint_pin_v1", "n_converted": n_conv, "backend": "test"}))
 
@@ -183,9 +204,9 @@ def test_verify_catches_corrupt_plug_and_pad(oracle):
         _assemble_pin(oracle, src, pin)
         (pin / P.INDEX_NAME).unlink()
         f = pin / "model.safetensors"
-        with SafeTensorsFile(f) as st:
-            off_plug = st.data_start + st.tensors["lin.weight.glint_plug"].data_offsets[0] + 3
-            off_pad = st.data_start + st.tensors["odd.weight"].data_offsets[1] - 1
+        with TensorFile(f) as tf:
+            off_plug = tf.entries["lin.weight.glint_plug"].begin + 3
+            off_pad = tf.entries["odd.weight"].end - 1
         raw = bytearray(f.read_bytes())
         raw[off_plug] ^= 0x11
         raw[off_pad] |= 0x50
@@ -195,7 +216,7 @@ def test_verify_catches_corrupt_plug_and_pad(oracle):
         lin = next(m for m in ev["modules"] if m["module"] == "lin")
         assert lin["parity"]["plug_first_diff"] == 3 and lin["parity"]["plug_bytes_differ"] == 1
         odd = next(m for m in ev["modules"] if m["module"] == "odd")
-        assert "odd n but pad nibble is not zero" in odd["problems"]
+        assert any("pad nibble" in q for q in odd["problems"])
 
 
 def test_verify_flags_missing_cells_and_count(oracle):
