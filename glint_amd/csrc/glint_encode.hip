@@ -7,11 +7,14 @@
  *
  * Fast encode (bs = 64, BF16, aligned): one pass, one 16-byte load per lane per
  * 512-element wave chunk. Lane l of the chunk owns elements [8l, 8l+8), so a 64-block is
- * 8 lanes: absmax is a packed-i16 max over BF16 magnitudes plus a 3-step DPP max. The
- * divide is a per-block correctly rounded reciprocal and Markstein's one-fma correction
- * (exact for every bf16 pair with 2^-90 <= absmax < 2^90; tests/native/check_markstein.c),
- * other blocks take the IEEE divide. The nearest-code search is one LDS bucket lookup and
- * one compare (glint_codebook.h, verified against the scan for every float in [-1, 1]).
+ * 8 lanes: absmax is a packed-u16 max over BF16 magnitudes plus a 3-step DPP max. For a
+ * block with 2^-90 <= absmax < 2^90 and no NaN the code is looked up from
+ * q = RN(w * RN(1/s)), one multiply: for every bf16 pair in that range q gives the code of
+ * the correctly rounded w / s and |q| <= 1 (tests/native/check_encode_quotient.c walks all
+ * 374,549,760 of them), and RN(1/s) of a bf16 s is a 128-entry LDS table plus an integer
+ * subtract. Other blocks (zero, tiny, huge, inf or NaN present) take the NaN-skipping
+ * absmax and the IEEE divide. The nearest-code search is one LDS bucket lookup and one
+ * compare (glint_codebook.h, verified against the scan for every float in [-1, 1]).
  * Everything else (any bs, F32 input, tails, unaligned pointers) runs the generic pair.
  */
 #include "glint_common.h"
@@ -50,11 +53,12 @@ __device__ __forceinline__ glint_i16x2 glint_mag_key(uint32_t d) {
     return __builtin_bit_cast(glint_i16x2, m);
 }
 
-/* LDS form of the bucket table: entry b = {threshold bits, S(base), S(base + 1), 0} with
+/* LDS form of the bucket table: entry b = {threshold bits, S(base), S(base + 1), R(b)} with
  * the "spread" code S(c) = hole | plug << 16 = (c >> 4) | (c & 15) << 16, so a lane folds
  * its 4 codes into hole nibbles (bits 0..15) and plug nibbles (bits 16..31) with one
- * shift-or each. ENC_COPIES copies, entry b of copy j at byte (b * ENC_COPIES + j) * 16,
- * lane l reading copy l % ENC_COPIES, to spread the random lookups over the banks. */
+ * shift-or each, and the reciprocal word R (glint_recip_word). ENC_COPIES copies, entry b
+ * of copy j at byte (b * ENC_COPIES + j) * 16, lane l reading copy l % ENC_COPIES, to
+ * spread the random lookups over the banks. */
 #ifndef ENC_COPIES
 #define ENC_COPIES 8
 #endif
@@ -70,12 +74,17 @@ __device__ __forceinline__ glint_i16x2 glint_mag_key(uint32_t d) {
 
 __device__ __forceinline__ uint32_t glint_spread_code(uint32_t c) { return (c >> 4) | ((c & 15u) << 16); }
 
-__device__ __forceinline__ void glint_fill_code_lds(glint_u32x4 *tab) {
-    for (int i = threadIdx.x; i < GLINT_CODE_BUCKETS * ENC_COPIES; i += blockDim.x) {
-        const GlintCodeEntry e = kCodeTable[i / ENC_COPIES];
-        tab[i] = glint_u32x4{e.thr, glint_spread_code(e.base), glint_spread_code(e.base + 1), 0u};
-    }
-    __syncthreads();
+/* R(b) for b < 128: bits(RN(1/(1 + b/128))) + 0x3F800000 + (b << 16). A normal bf16
+ * s = 2^(E-127) (1 + b/128) has RN(1/s) = RN(1/(1 + b/128)) 2^(127-E) (exact scaling while
+ * the result is normal), whose bits are R(b) - bits(s) since bits(s) = E << 23 | b << 16.
+ * The divide is IEEE (correctly rounded); tests/native/check_encode_quotient.c checks the
+ * identity for every s the fast path takes. */
+__device__ __forceinline__ uint32_t glint_recip_word(int b) {
+    return b < 128 ? __float_as_uint(1.0f / (1.0f + (float)b * 0.0078125f)) + 0x3F800000u + ((uint32_t)b << 16) : 0u;
+}
+
+__device__ __forceinline__ glint_u32x4 glint_code_lds_entry(GlintCodeEntry e, int b) {
+    return glint_u32x4{e.thr, glint_spread_code(e.base), glint_spread_code(e.base + 1), glint_recip_word(b)};
 }
 
 /* Spread code of v (|v| <= 1 or a quiet NaN; see glint_code_of). `lane_k` is this lane's
@@ -87,25 +96,53 @@ __device__ __forceinline__ uint32_t glint_spread_of(float v, const glint_u32x4 *
     return v > __uint_as_float(e.x) ? e.z : e.y;
 }
 
+/* Spread code of q with |q| <= 1 (no clamp: the fast path's quotients never leave
+ * [-1, 1], so the bucket is in [0, 512]). */
+__device__ __forceinline__ uint32_t glint_spread_fast(float q, const glint_u32x4 *tab, uint32_t lane_k) {
+    const uint32_t addr = (__float_as_uint(fmaf(q, 256.0f, GLINT_CODE_MAGIC)) * (ENC_COPIES * 16u)) + lane_k;
+    const glint_u32x4 e = *(const glint_u32x4 *)((const char *)tab + addr);
+    return q > __uint_as_float(e.x) ? e.z : e.y;
+}
+
 template <int CTRL>
 __device__ __forceinline__ int glint_max_dpp(int v) {
     /* bound_ctrl with full masks lets the DPP move fold into v_max_i32_dpp */
     return max(v, __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true));
 }
 
-__device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const glint_u32x4 *tab, uint32_t lane_k,
-                                                   int64_t chunk, int lane, uint32_t *__restrict__ hole,
-                                                   uint32_t *__restrict__ plug, float *__restrict__ absmax) {
-    /* absmax of this lane's 8 values, then of the 8 lanes that share the block; the
-     * floor at key 0x7F (magnitude 0) makes an all-NaN lane contribute 0 */
+/* Largest BF16 magnitude bits of a lane's 8 values (NaN not skipped: a NaN, 0x7F81 and up,
+ * wins and sends its block to the exact path). */
+__device__ __forceinline__ uint32_t glint_mag_max(const glint_u32x4 d) {
+    const glint_u16x2 a = __builtin_bit_cast(glint_u16x2, d.x & 0x7FFF7FFFu);
+    const glint_u16x2 b = __builtin_bit_cast(glint_u16x2, d.y & 0x7FFF7FFFu);
+    const glint_u16x2 c = __builtin_bit_cast(glint_u16x2, d.z & 0x7FFF7FFFu);
+    const glint_u16x2 e = __builtin_bit_cast(glint_u16x2, d.w & 0x7FFF7FFFu);
+    const glint_u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(a, b), __builtin_elementwise_max(c, e));
+    return max((uint32_t)m.x, (uint32_t)m.y);
+}
+
+/* Block absmax bits with NaN skipped (glint_mag_key), reduced over the 8 lanes. */
+__device__ __forceinline__ uint32_t glint_absmax_skip_nan(const glint_u32x4 d) {
     glint_i16x2 k = __builtin_elementwise_max(glint_mag_key(d.x), glint_mag_key(d.y));
     k = __builtin_elementwise_max(k, __builtin_elementwise_max(glint_mag_key(d.z), glint_mag_key(d.w)));
     int m16 = max(max((int)k.x, (int)k.y), 0x7F) - 0x7F;
     m16 = glint_max_dpp<GLINT_DPP_QUAD_1032>(m16);
     m16 = glint_max_dpp<GLINT_DPP_QUAD_2301>(m16);
     m16 = glint_max_dpp<GLINT_DPP_ROW_HALF_MIRROR>(m16);
-    const uint32_t sbits = (uint32_t)m16 << 16;
-    const float s = __uint_as_float(sbits);
+    return (uint32_t)m16 << 16;
+}
+
+__device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const glint_u32x4 *tab, uint32_t lane_k,
+                                                   uint32_t lane_r, int64_t chunk, int lane,
+                                                   uint32_t *__restrict__ hole, uint32_t *__restrict__ plug,
+                                                   float *__restrict__ absmax) {
+    /* magnitude max of this lane's 8 values, then of the 8 lanes that share the block (the
+     * DPP moves stay inside each aligned group of 8 lanes) */
+    int m16 = (int)glint_mag_max(d);
+    m16 = glint_max_dpp<GLINT_DPP_QUAD_1032>(m16);
+    m16 = glint_max_dpp<GLINT_DPP_QUAD_2301>(m16);
+    m16 = glint_max_dpp<GLINT_DPP_ROW_HALF_MIRROR>(m16);
+    uint32_t sbits = (uint32_t)m16 << 16;
 
     const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
     float w[8];
@@ -114,34 +151,35 @@ __device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const gl
         w[2 * j] = glint_bf16lo(dw[j]);
         w[2 * j + 1] = glint_bf16hi(dw[j]);
     }
-    float v[8];
-    if (sbits - 0x12800000u < 0x6C800000u - 0x12800000u) { /* 2^-90 <= s < 2^90 */
-        const float y = 1.0f / s;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float q = w[j] * y;
-            const float r = fmaf(-q, s, w[j]);
-            v[j] = fmaf(r, y, q);
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            v[j] = (s == 0.0f) ? 0.0f : w[j] / s;
-    }
     /* element 4h + i contributes its hole nibble at bit 4i and plug nibble at 16 + 4i */
     uint32_t acc[2];
+    if (sbits - 0x12800000u < 0x6C800000u - 0x12800000u) { /* 2^-90 <= s < 2^90, so no NaN or inf */
+        const uint32_t rw = *(const uint32_t *)((const char *)tab + ((sbits >> 9) & (127u << 7)) + lane_r);
+        const float y = __uint_as_float(rw - sbits); /* RN(1/s) */
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        uint32_t a = glint_spread_of(v[4 * h], tab, lane_k);
+        for (int h = 0; h < 2; ++h) {
+            uint32_t a = glint_spread_fast(w[4 * h] * y, tab, lane_k);
 #pragma unroll
-        for (int i = 1; i < 4; ++i)
-            a |= glint_spread_of(v[4 * h + i], tab, lane_k) << (4 * i);
-        acc[h] = a;
+            for (int i = 1; i < 4; ++i)
+                a |= glint_spread_fast(w[4 * h + i] * y, tab, lane_k) << (4 * i);
+            acc[h] = a;
+        }
+    } else {
+        sbits = glint_absmax_skip_nan(d);
+        const float s = __uint_as_float(sbits);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t a = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                a |= glint_spread_of((s == 0.0f) ? 0.0f : w[4 * h + i] / s, tab, lane_k) << (4 * i);
+            acc[h] = a;
+        }
     }
     hole[chunk * 64 + lane] = __builtin_amdgcn_perm(acc[1], acc[0], 0x05040100u);
     plug[chunk * 64 + lane] = __builtin_amdgcn_perm(acc[1], acc[0], 0x07060302u);
     if ((lane & 7) == 0)
-        absmax[chunk * 8 + (lane >> 3)] = s;
+        absmax[chunk * 8 + (lane >> 3)] = __uint_as_float(sbits);
 }
 
 /* One wave handles groups of ENC_UNROLL consecutive chunks: groups wave, wave + nwaves, ...
@@ -160,6 +198,7 @@ __global__ __launch_bounds__(ENC_THREADS, ENC_WPE) void k_encode_bf16_b64(const 
      * entry stride (mod 2^32) */
     const uint32_t lane_k =
         (uint32_t)(lane % ENC_COPIES) * 16u - GLINT_CODE_MAGIC_BITS * (uint32_t)(ENC_COPIES * 16);
+    const uint32_t lane_r = (uint32_t)(lane % ENC_COPIES) * 16u + 12u; /* word 3 of this lane's copy */
     /* wave-uniform, so group arithmetic stays in scalar registers */
     const int wave = (int)blockIdx.x * (ENC_THREADS / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nwaves = (int)gridDim.x * (ENC_THREADS / 64);
@@ -191,11 +230,9 @@ __global__ __launch_bounds__(ENC_THREADS, ENC_WPE) void k_encode_bf16_b64(const 
     }
 #pragma unroll
     for (int k = 0; k < kFill; ++k) /* clamped indices rewrite the last entry with its own value */
-        tab[fi[k]] = glint_u32x4{fe[k].thr, glint_spread_code(fe[k].base), glint_spread_code(fe[k].base + 1), 0u};
-    for (int e = threadIdx.x + kFill * blockDim.x; e < kEntries; e += blockDim.x) { /* blockDim < 1024 only */
-        const GlintCodeEntry ce = kCodeTable[e / ENC_COPIES];
-        tab[e] = glint_u32x4{ce.thr, glint_spread_code(ce.base), glint_spread_code(ce.base + 1), 0u};
-    }
+        tab[fi[k]] = glint_code_lds_entry(fe[k], fi[k] / ENC_COPIES);
+    for (int e = threadIdx.x + kFill * blockDim.x; e < kEntries; e += blockDim.x) /* blockDim < 1024 only */
+        tab[e] = glint_code_lds_entry(kCodeTable[e / ENC_COPIES], e / ENC_COPIES);
     __syncthreads();
 
     int i = 0;
@@ -203,7 +240,7 @@ __global__ __launch_bounds__(ENC_THREADS, ENC_WPE) void k_encode_bf16_b64(const 
         const int64_t c0 = (int64_t)(wave + i * nwaves) * ENC_UNROLL;
 #pragma unroll
         for (int u = 0; u < ENC_UNROLL; ++u)
-            glint_encode_chunk(da[u], tab, lane_k, c0 + u, lane, hole, plug, absmax);
+            glint_encode_chunk(da[u], tab, lane_k, lane_r, c0 + u, lane, hole, plug, absmax);
         const int64_t ga = (int64_t)min(wave + (i + 2) * nwaves, last) * ENC_UNROLL;
 #pragma unroll
         for (int u = 0; u < ENC_UNROLL; ++u)
@@ -211,7 +248,7 @@ __global__ __launch_bounds__(ENC_THREADS, ENC_WPE) void k_encode_bf16_b64(const 
         const int64_t c1 = (int64_t)(wave + (i + 1) * nwaves) * ENC_UNROLL;
 #pragma unroll
         for (int u = 0; u < ENC_UNROLL; ++u)
-            glint_encode_chunk(db[u], tab, lane_k, c1 + u, lane, hole, plug, absmax);
+            glint_encode_chunk(db[u], tab, lane_k, lane_r, c1 + u, lane, hole, plug, absmax);
         const int64_t gb = (int64_t)min(wave + (i + 3) * nwaves, last) * ENC_UNROLL;
 #pragma unroll
         for (int u = 0; u < ENC_UNROLL; ++u)
@@ -221,11 +258,11 @@ __global__ __launch_bounds__(ENC_THREADS, ENC_WPE) void k_encode_bf16_b64(const 
         const int64_t c0 = (int64_t)(wave + i * nwaves) * ENC_UNROLL;
 #pragma unroll
         for (int u = 0; u < ENC_UNROLL; ++u)
-            glint_encode_chunk(da[u], tab, lane_k, c0 + u, lane, hole, plug, absmax);
+            glint_encode_chunk(da[u], tab, lane_k, lane_r, c0 + u, lane, hole, plug, absmax);
     }
     const int64_t c = (int64_t)ngroups * ENC_UNROLL + wave; /* at most ENC_UNROLL - 1 leftover chunks */
     if (c < nchunks)
-        glint_encode_chunk(w[c * 64 + lane], tab, lane_k, c, lane, hole, plug, absmax);
+        glint_encode_chunk(w[c * 64 + lane], tab, lane_k, lane_r, c, lane, hole, plug, absmax);
 }
 
 /* ---------------------------------------------------------------- generic encode */

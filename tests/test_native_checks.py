@@ -3,9 +3,10 @@
 * the bucket table reproduces the reference's first-minimum scan for every float in
   [-1, 1] and for NaN (glint_amd/csrc/gen_code_table.c --verify);
 * the committed glint_code_table.inc is what the generator produces;
-* the reciprocal-plus-correction divide matches the IEEE divide bit for bit where it
-  matters and code for code everywhere, over every bf16 (w, absmax) pair the fast path
-  sees (tests/native/check_markstein.c);
+* the fast path's one-multiply quotient q = RN(w * RN(1/s)), with RN(1/s) from the
+  128-entry reciprocal table, stays in [-1, 1] and gives the code of the IEEE quotient
+  w / s for every bf16 (w, absmax) pair the fast path sees, both signs, also with a
+  flush-to-zero multiply (tests/native/check_encode_quotient.c);
 * the three-plane BF16 split of the f32-out H-TILE on MFMA is exact for every f32 weight
   (tests/native/check_split3.c).
 """
@@ -35,11 +36,13 @@ def test_code_table_is_generated_and_exhaustively_correct(tmp_path):
     assert "verify: 0 mismatches" in r.stdout
 
 
-def test_fast_divide_exhaustive_over_bf16_pairs(tmp_path):
-    exe = _build(tmp_path, ROOT / "tests" / "native" / "check_markstein.c", "mk")
+def test_fast_quotient_exhaustive_over_bf16_pairs(tmp_path):
+    exe = _build(tmp_path, ROOT / "tests" / "native" / "check_encode_quotient.c", "quot")
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=900)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "0 differ with w >= 2^-100 and w/s normal" in r.stdout and "0 code mismatches" in r.stdout
+    assert "749099520 pairs" in r.stdout
+    assert ("0 reciprocal mismatches, 0 |q| > 1, 0 code mismatches, 0 flush-to-zero code mismatches"
+            in r.stdout)
 
 
 def test_three_plane_split_exhaustive(tmp_path):
