@@ -577,6 +577,218 @@ def summarize_trace(kt_db, bench_json=None) -> str:
     return text
 
 
+# Counter evidence: one fixed workload run under five rocprofv3 passes (FETCH_SIZE, WRITE_SIZE,
+# derived utilisation, raw instruction counts, kernel trace), each dispatch assigned to its phase
+# by kernel name and dispatch order. MI355X: 256 CUs, 1024 SIMDs.
+COUNTERS_JSON = ROOT / "profiles" / "counters_hot_kernels.json"
+CU_NUM, SIMD_NUM = 256, 1024
+COUNTER_PASSES = {
+    "fetch": "--pmc FETCH_SIZE",
+    "write": "--pmc WRITE_SIZE",
+    "util": "--pmc VALUBusy MfmaUtil LDSBankConflict",
+    "inst": "--pmc SQ_INSTS_VALU SQ_INSTS_LDS SQ_INSTS_MFMA SQ_LDS_IDX_ACTIVE SQ_WAVES GRBM_GUI_ACTIVE",
+    "trace": "--kernel-trace --stats",
+}
+
+
+def counter_workload(torch, H, manifest_path):
+    """The hot kernels at their BASELINE shapes, a fixed number of dispatches each, on one
+    stream, phases fenced by synchronize. Writes the phase manifest (kernel-name key, how many
+    dispatches of that key precede the phase, how many belong to it, algorithmic bytes and
+    operations per phase) for --summarize-counters."""
+    lib, st = H.encode_lib(), stream_handle(torch)
+    launched = {}
+    phases = []
+
+    def phase(name, key, count, fn, nbytes=None, ops=None, elements=None, note=""):
+        torch.cuda.synchronize()
+        phases.append({"name": name, "kernel": key, "skip": launched.get(key, 0), "count": count,
+                       "algorithmic_bytes": nbytes, "ops": ops, "elements": elements, "note": note})
+        fn()
+        torch.cuda.synchronize()
+        launched[key] = launched.get(key, 0) + count
+        log(f"counter workload: {name} ({count} dispatches)")
+
+    def encode_pin(w):
+        launched["k_encode_bf16_b64"] = launched.get("k_encode_bf16_b64", 0) + 1
+        return H.encode_bf16(w, 64)
+
+    g = torch.Generator(device="cuda").manual_seed(7001)
+    # copy calibration for the byte counters
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    phase("hbm_copy_256mib", "copyBuffer", 10, lambda: [dst.copy_(src) for _ in range(10)], nbytes=10 * 2 * (256 << 20),
+          note="torch device copy, the reference for scaling FETCH_SIZE / WRITE_SIZE")
+    del src, dst
+    # encode at the decode shape: 6 distinct inputs (704 MB, more than the 256 MB last-level cache)
+    N, K = GEMV_N, GEMV_K
+    ws = [(torch.randn(N * K, device="cuda", generator=g) * 0.02).to(torch.bfloat16) for _ in range(6)]
+    outs = [(torch.empty(N * K // 2, dtype=torch.uint8, device="cuda"), torch.empty(N * K // 2, dtype=torch.uint8, device="cuda"),
+             torch.empty(N * K // 64, dtype=torch.float32, device="cuda")) for _ in range(6)]
+    phase("encode_14336x4096", "k_encode_bf16_b64", 6,
+          lambda: [bound(lib.glint_encode_bf16_device, w, N * K, 64, *o, st)() for w, o in zip(ws, outs)],
+          nbytes=6 * 3.0625 * N * K, elements=6 * N * K)
+    del ws, outs
+    # encode over the Llama-3-8B tensor set (one dispatch per tensor, every size a multiple of 512)
+    shapes = llama3_8b_shapes()
+    total = sum(a * b for a, b in shapes)
+    ws = [(torch.randn(a * b, device="cuda", generator=g) * 0.02).to(torch.bfloat16) for a, b in shapes]
+    outs = [(torch.empty(w.numel() // 2, dtype=torch.uint8, device="cuda"),
+             torch.empty(w.numel() // 2, dtype=torch.uint8, device="cuda"),
+             torch.empty(w.numel() // 64, dtype=torch.float32, device="cuda")) for w in ws]
+    phase("encode_model_set", "k_encode_bf16_b64", len(shapes),
+          lambda: [bound(lib.glint_encode_bf16_device, w, w.numel(), 64, *o, st)() for w, o in zip(ws, outs)],
+          nbytes=3.0625 * total, elements=total, note="226 Llama-3-8B tensors, 8.03e9 weights")
+    del ws, outs
+    torch.cuda.empty_cache()
+    # decode GEMV (headline), 19 rotated pins
+    pins = []
+    for _ in range(19):
+        pins.append(encode_pin((torch.randn(N * K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)))
+    x = torch.randn(K, device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.empty(N, dtype=torch.bfloat16, device="cuda")
+    calls = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, y, 1, N, K, 64, st) for p in pins]
+    phase("gemv_m1_14336x4096", GEMV_KERNEL, 38, lambda: [c() for c in calls + calls], nbytes=38 * gemv_bytes(N, K))
+    # prefill on the gate shape, 6 rotated pins (373 MB)
+    pins = pins[:6]
+    for M, key, name in ((2048, "k_tile_big<2,GlintTileProducer,TileOutBF16>", "prefill_m2048_14336x4096"),
+                         (64, "k_tile_ss<64,", "prefill_m64_14336x4096")):
+        xm = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        ym = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        calls = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], xm, ym, M, N, K, 64, st) for p in pins]
+        phase(name, key, 6, lambda: [c() for c in calls], ops=6 * 2.0 * M * N * K,
+              nbytes=6 * (N * K * (1 + 4 / 64) + 2 * M * K + 2 * M * N))
+        del xm, ym
+    del pins
+    # INT8 GEMM at the INT8 config: the raw per-row / per-column GEMM and the attach ABI
+    M, N8, K8 = 2048, 8192, 8192
+    A = torch.randint(-127, 128, (M, K8), device="cuda", generator=g, dtype=torch.int8)
+    B = torch.randint(-127, 128, (N8, K8), device="cuda", generator=g, dtype=torch.int8)
+    sa = torch.rand(M, device="cuda", generator=g) * 0.019 + 1e-3
+    sb = torch.rand(N8, device="cuda", generator=g) * 0.019 + 1e-3
+    o8 = torch.empty(M, N8, dtype=torch.bfloat16, device="cuda")
+    phase("int8_gemm_2048x8192x8192", "k_int8_gemm_dma", 4,
+          lambda: [H.int8_gemm_scaled_bf16(A, B, sa, sb, out=o8) for _ in range(4)], ops=4 * 2.0 * M * N8 * K8)
+    del A, B, sa, sb, o8
+    p7 = H.p7_lib()
+    xb = torch.randn(M, K8, device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randint(-127, 128, (N8 * K8,), device="cuda", generator=g, dtype=torch.int8)
+    sc = torch.rand(N8 * K8 // 64, device="cuda", generator=g) * 0.02 + 1e-3
+    yf = torch.empty(M, N8, dtype=torch.float32, device="cuda")
+    xq = torch.empty(M * K8, dtype=torch.int8, device="cuda")
+    sx = torch.empty(M * K8 // 64, dtype=torch.float32, device="cuda")
+    lin = H.Int8MmaLinear(q.data_ptr(), sc.data_ptr(), N8, K8)
+    call = bound(p7.int8_mma_gemm, xb, lin, yf, M, xq, sx, st)
+    phase("int8_mma_gemm_abi_2048x8192x8192", "k_int8_mma_dma", 4, lambda: [call() for _ in range(4)],
+          ops=4 * 2.0 * M * N8 * K8, note="per-64 scales, kb-ordered f32 epilogue")
+    Path(manifest_path).write_text(json.dumps({"phases": phases, "cu_num": CU_NUM, "simd_num": SIMD_NUM}, indent=1) + "\n")
+
+
+def _dispatch_rows(db_path, key):
+    """{counter: value} per dispatch of kernels whose name (spaces removed) contains key,
+    ordered by dispatch id, with the dispatch's start and end."""
+    import sqlite3
+    cur = sqlite3.connect(db_path).cursor()
+    rows = {}
+    tables = {r[0] for r in cur.execute("select name from sqlite_master")}
+    if "counters_collection" in tables:
+        for did, name, ctr, val, start, end in cur.execute(
+                "select dispatch_id, kernel_name, counter_name, value, start, end from counters_collection"):
+            if key in name.replace(" ", ""):
+                r = rows.setdefault(did, {"start": start, "end": end})
+                r[ctr] = val
+    if not rows:
+        for did, name, start, end in cur.execute("select dispatch_id, name, start, end from kernels"):
+            if key in name.replace(" ", ""):
+                rows[did] = {"start": start, "end": end}
+    return [rows[d] for d in sorted(rows)]
+
+
+def summarize_counters(manifest, dbs, out_path=None) -> dict:
+    """Per-phase HBM traffic, utilisation and kernel time from the five passes, written to
+    out_path (profiles/counters_hot_kernels.json by default)."""
+    import statistics
+    man = json.loads(Path(manifest).read_text())
+    cu, simd = man["cu_num"], man["simd_num"]
+    by_phase = {}
+    for tag, db in dbs.items():
+        for ph in man["phases"]:
+            rows = _dispatch_rows(db, ph["kernel"])[ph["skip"]:ph["skip"] + ph["count"]]
+            if len(rows) != ph["count"]:
+                raise SystemExit(f"{db}: {ph['name']}: {len(rows)} of {ph['count']} dispatches of {ph['kernel']}")
+            by_phase.setdefault(ph["name"], {})[tag] = rows
+    copy = by_phase["hbm_copy_256mib"]
+    scale = {c: (256 << 20) / (statistics.mean(r[c] for r in copy[t]) * 1024.0)
+             for t, c in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE"))}
+    out = {"device": "MI355X (gfx950), one GPU", "cu_num": cu, "simd_num": simd,
+           "byte_scale": {"FETCH_SIZE": scale["FETCH_SIZE"], "WRITE_SIZE": scale["WRITE_SIZE"],
+                          "rule": "true bytes of 10 torch 256 MiB device copies / counter KiB * 1024"},
+           "formulas": {
+               "hbm_bytes": "sum over the phase of (FETCH_SIZE * fetch scale + WRITE_SIZE * write scale) * 1024",
+               "VALUBusy": "100 * SQ_ACTIVE_INST_VALU / CU_NUM / GRBM_GUI_ACTIVE (rocprofv3 derived, per dispatch)",
+               "MfmaUtil": "100 * SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * SIMD_NUM) (rocprofv3 derived)",
+               "LDSBankConflict": "100 * SQ_LDS_BANK_CONFLICT / GRBM_GUI_ACTIVE / CU_NUM (rocprofv3 derived)",
+               "lds_active_pct": "100 * SQ_LDS_IDX_ACTIVE / GRBM_GUI_ACTIVE / CU_NUM",
+               "per-dispatch percentages": "weighted by each dispatch's kernel-trace duration",
+               "kernel_us": "kernel-trace durations (begin to end), summed over the phase",
+               "hbm_frac": "algorithmic bytes / kernel time / 8 TB/s",
+               "mfma_frac": "operations / kernel time / dense peak (bf16 2.5 PFLOP/s, int8 5.0 POP/s)"},
+           "phases": {}}
+    for ph in man["phases"]:
+        d = by_phase[ph["name"]]
+        dur = [(r["end"] - r["start"]) / 1e3 for r in d["trace"]]
+        wsum = sum(dur)
+
+        def wavg(tag, ctr):
+            return sum(r[ctr] * w for r, w in zip(d[tag], dur)) / wsum
+
+        res = {"kernel": ph["kernel"], "dispatches": ph["count"], "note": ph["note"],
+               "kernel_us_total": wsum, "kernel_us_avg": wsum / len(dur)}
+        fetch = sum(r["FETCH_SIZE"] for r in d["fetch"]) * 1024.0 * scale["FETCH_SIZE"]
+        write = sum(r["WRITE_SIZE"] for r in d["write"]) * 1024.0 * scale["WRITE_SIZE"]
+        res.update({"hbm_fetch_bytes": fetch, "hbm_write_bytes": write})
+        if ph["algorithmic_bytes"]:
+            res["algorithmic_bytes"] = ph["algorithmic_bytes"]
+            res["traffic_over_algorithmic"] = (fetch + write) / ph["algorithmic_bytes"]
+            res["hbm_frac"] = ph["algorithmic_bytes"] / (wsum * 1e-6) / 1e9 / HBM_PEAK_GBS
+            res["counted_hbm_gbs"] = (fetch + write) / (wsum * 1e-6) / 1e9
+        if ph["ops"]:
+            peak = I8_PEAK_TOPS if "int8" in ph["name"] else BF16_PEAK_TFLOPS
+            res["tera_ops_per_s"] = ph["ops"] / (wsum * 1e-6) / 1e12
+            res["mfma_frac"] = res["tera_ops_per_s"] / peak
+        for c in ("VALUBusy", "MfmaUtil", "LDSBankConflict"):
+            res[c] = wavg("util", c)
+        res["lds_active_pct"] = sum(100.0 * r["SQ_LDS_IDX_ACTIVE"] / r["GRBM_GUI_ACTIVE"] / cu * w
+                                    for r, w in zip(d["inst"], dur)) / wsum
+        for c in ("SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA", "SQ_WAVES"):
+            res[c] = sum(r[c] for r in d["inst"])
+        if ph["elements"]:
+            res["valu_insts_per_512_elements"] = res["SQ_INSTS_VALU"] / (ph["elements"] / 512)
+        out["phases"][ph["name"]] = res
+    out["commands"] = [f"rocprofv3 {flags} -d <dir_{tag}> -o run -- python3 bench.py --counter-workload <dir_{tag}>/manifest.json"
+                       for tag, flags in COUNTER_PASSES.items()] + [
+        "python3 bench.py --summarize-counters <manifest.json> " +
+        " ".join(f"{t}=<dir_{t}>/run_results.db" for t in COUNTER_PASSES)]
+    Path(out_path or COUNTERS_JSON).write_text(json.dumps(out, indent=1) + "\n")
+    return out
+
+
+def load_counters():
+    """The headline figures of profiles/counters_hot_kernels.json for the bench line."""
+    try:
+        c = json.loads(COUNTERS_JSON.read_text())["phases"]
+    except Exception:
+        return None
+    pick = {"encode_model_set": ("hbm_frac", "traffic_over_algorithmic", "VALUBusy", "valu_insts_per_512_elements"),
+            "encode_14336x4096": ("hbm_frac", "traffic_over_algorithmic", "VALUBusy"),
+            "gemv_m1_14336x4096": ("hbm_frac", "traffic_over_algorithmic", "VALUBusy"),
+            "prefill_m2048_14336x4096": ("mfma_frac", "MfmaUtil", "LDSBankConflict", "lds_active_pct"),
+            "prefill_m64_14336x4096": ("hbm_frac", "mfma_frac", "MfmaUtil", "LDSBankConflict", "lds_active_pct"),
+            "int8_gemm_2048x8192x8192": ("mfma_frac", "MfmaUtil"),
+            "int8_mma_gemm_abi_2048x8192x8192": ("mfma_frac", "MfmaUtil", "VALUBusy")}
+    return {k: {f: round(c[k][f], 4) for f in fs if f in c[k]} for k, fs in pick.items() if k in c}
+
+
 def load_traffic():
     p = TRAFFIC_JSON
     if p.is_file():
@@ -602,6 +814,10 @@ def main() -> int:
                          "kmajor,hostabi,pintools) or 'all'")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
                     help="write the traffic figures from two rocprofv3 --pmc databases (no GPU needed)")
+    ap.add_argument("--counter-workload", metavar="MANIFEST",
+                    help="run the fixed hot-kernel workload for the rocprofv3 counter passes, write its manifest")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="ARG",
+                    help="MANIFEST tag=DB ... (tags fetch, write, util, inst, trace): write the counter summary")
     ap.add_argument("--summarize-trace", nargs="+", metavar="DB",
                     help="print the per-kernel table of a rocprofv3 --kernel-trace database [and bench JSON]")
     args = ap.parse_args()
@@ -610,6 +826,10 @@ def main() -> int:
         return 0
     if args.summarize_trace:
         print(summarize_trace(*args.summarize_trace[:2]))
+        return 0
+    if args.summarize_counters:
+        dbs = dict(a.split("=", 1) for a in args.summarize_counters[1:])
+        print(json.dumps(summarize_counters(args.summarize_counters[0], dbs), indent=1))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the GLINT hot path has no multi-GPU mode in this build "
@@ -623,6 +843,9 @@ def main() -> int:
     H.encode_lib()
     H.p7_lib()
     log(f"device {torch.cuda.get_device_name(0)}")
+    if args.counter_workload:
+        counter_workload(torch, H, args.counter_workload)
+        return 0
     if args.calibrate_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
         dst = torch.empty_like(src)
@@ -682,6 +905,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic()},
         "cpu_baseline": cpu,
+        "counters": load_counters(),
         "gemv": gemv,
         **extra,
     }
