@@ -10,9 +10,9 @@
  *   workgroup's channel slice (grid.y) and meet in LDS. Per element: one v_perm for the
  *   address, one lookup in the 64-copy PARENT table, one FMA by the wave-uniform x[c];
  *   the block scale is applied once per run of channels inside a 64-block.
- * k_select_topk — one workgroup: keys in LDS, the threshold by a two-level radix select
- *   (LDS histograms of the top 8 and low 7 key bits), then a block scan that writes the
- *   kept channels in ascending order.
+ * k_select_topk — one workgroup: keys in LDS, rank thresholds by a two-level radix select
+ *   (LDS histograms of the top 8 and low 7 key bits), the price / relational / floor rules,
+ *   then a block scan that writes the kept channels in ascending order.
  * k_apply_corr_km — the fold kernel's mapping (KM_CORR_RPL = 8 rows per lane) over the
  *   selected list (count read on the device), with the 256-entry delta table
  *   (CELLS - PARENT) in 64 lane copies.
@@ -269,27 +269,35 @@ __global__ __launch_bounds__(KM_T) void k_km_combine(const float *__restrict__ p
 #define SEL_T 1024
 #define SEL_MAX_K 32768
 
-/* T = the largest 15-bit key value with count(key >= T) >= nsel, found as the radix select
- * of two histograms: 256 bins of key >> 7, then 128 bins of key & 127 inside the chosen
- * bin. That is the same T the bit-by-bit bisection of the rule gives (the count is
- * non-increasing in T). nsel == 0 keeps nothing; nsel above K keeps everything. Then the
- * kept channels are written in ascending order through a block scan. */
-__global__ __launch_bounds__(SEL_T) void k_select_topk(const uint16_t *__restrict__ x, int K, int nsel,
-                                                       int32_t *__restrict__ idx, int32_t *__restrict__ cnt) {
+/* |x| of a 15-bit key for the relational threshold: (128 + mantissa) 2^(e - 134) with the
+ * exponent clamped to [-60, 40], 0 for zero and subnormal keys (an exact product). */
+__device__ __forceinline__ float sel_mag(int k) {
+    const int ex = k >> 7;
+    const int n = min(max(ex - 134, -60), 40);
+    return ex > 0 ? (float)(128 + (k & 127)) * __uint_as_float((uint32_t)(n + 127) << 23) : 0.0f;
+}
+
+/* Threshold T and the kept list (the rule in include/glint_select.h). rank(n) = the largest
+ * 15-bit T with count(key >= T) >= n is a radix select over two LDS histograms: 256 bins of
+ * key >> 7 (built once), then 128 bins of key & 127 inside the chosen bin; that is the T
+ * the rule's bit-by-bit bisection finds, since the count is non-increasing in T; n <= 0
+ * gives 32767 and n > K gives 0, as the bisection does. The relational price sums |x| in
+ * f32 over the 1024 threads' ranges of ceil(K / 1024) channels and then pairwise in LDS,
+ * the order the rule fixes. The kept channels are written in ascending order through a
+ * block scan. */
+__global__ __launch_bounds__(SEL_T) void k_select_topk(const uint16_t *__restrict__ x, int K, int nsel, int tkey,
+                                                       int nfloor, int32_t *__restrict__ idx, int32_t *__restrict__ cnt,
+                                                       int32_t *__restrict__ cnt_log, int slot) {
     __shared__ uint16_t keys[SEL_MAX_K];
     __shared__ int hc[256], hf[128]; /* coarse and fine histograms */
     __shared__ int wsum[SEL_T / 64];
+    __shared__ float red[SEL_T];
     __shared__ int s_bin, s_above, s_thr;
     const int t = threadIdx.x, lane = t & 63;
+    const int per = (K + SEL_T - 1) / SEL_T;
+    const int lo = min(t * per, K), hi = min(lo + per, K);
     if (t < 256)
         hc[t] = 0;
-    if (t < 128)
-        hf[t] = 0;
-    if (t == 0) {
-        s_bin = -1;
-        s_above = 0;
-        s_thr = nsel == 0 ? 32768 : 0; /* kept when no bin qualifies: nothing, or everything */
-    }
     __syncthreads();
     for (int i = t; i < K; i += SEL_T) {
         const int k = x[i] & 0x7FFF;
@@ -297,56 +305,103 @@ __global__ __launch_bounds__(SEL_T) void k_select_topk(const uint16_t *__restric
         atomicAdd(&hc[k >> 7], 1);
     }
     __syncthreads();
-    if (t < 64 && nsel > 0) { /* lane l: coarse bins 4 l .. 4 l + 3; suffix counts */
-        const int v0 = hc[4 * lane], v1 = hc[4 * lane + 1], v2 = hc[4 * lane + 2], v3 = hc[4 * lane + 3];
-        const int sum = v0 + v1 + v2 + v3;
-        int inc = sum; /* sum over lanes lane .. 63 */
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_down(inc, o, 64);
-            if (lane + o < 64)
-                inc += v;
-        }
-        const int c4 = inc - sum, c3 = c4 + v3, c2 = c3 + v2, c1 = c2 + v1, c0 = c1 + v0; /* c_j = count(bin >= 4 l + j) */
-        const int cs[5] = {c0, c1, c2, c3, c4};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (cs[j] >= nsel && cs[j + 1] < nsel) { /* exactly one bin, when count(all) >= nsel */
-                s_bin = 4 * lane + j;
-                s_above = cs[j + 1];
-            }
-    }
-    __syncthreads();
-    const int bin = s_bin;
-    if (bin >= 0) {
-        for (int i = t; i < K; i += SEL_T) {
-            const int k = keys[i];
-            if ((k >> 7) == bin)
-                atomicAdd(&hf[k & 127], 1);
+    /* every thread calls rank with the same n (its barriers are block-wide) */
+    auto rank = [&](int n) -> int {
+        if (n <= 0)
+            return 32767;
+        if (t < 128)
+            hf[t] = 0;
+        if (t == 0) {
+            s_bin = -1;
+            s_above = 0;
+            s_thr = 0; /* no bin qualifies when count(all) < n: everything is kept */
         }
         __syncthreads();
-        if (t < 64) { /* lane l: fine bins 2 l, 2 l + 1 */
-            const int need = nsel - s_above;
-            const int v0 = hf[2 * lane], v1 = hf[2 * lane + 1];
-            const int sum = v0 + v1;
-            int inc = sum;
+        if (t < 64) { /* lane l: coarse bins 4 l .. 4 l + 3; suffix counts */
+            const int v0 = hc[4 * lane], v1 = hc[4 * lane + 1], v2 = hc[4 * lane + 2], v3 = hc[4 * lane + 3];
+            const int sum = v0 + v1 + v2 + v3;
+            int inc = sum; /* sum over lanes lane .. 63 */
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const int v = __shfl_down(inc, o, 64);
                 if (lane + o < 64)
                     inc += v;
             }
-            const int c2 = inc - sum, c1 = c2 + v1, c0 = c1 + v0;
-            if (c0 >= need && c1 < need)
-                s_thr = (bin << 7) | (2 * lane);
-            if (c1 >= need && c2 < need)
-                s_thr = (bin << 7) | (2 * lane + 1);
+            const int c4 = inc - sum, c3 = c4 + v3, c2 = c3 + v2, c1 = c2 + v1, c0 = c1 + v0; /* c_j = count(bin >= 4 l + j) */
+            const int cs[5] = {c0, c1, c2, c3, c4};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (cs[j] >= n && cs[j + 1] < n) { /* exactly one bin, when count(all) >= n */
+                    s_bin = 4 * lane + j;
+                    s_above = cs[j + 1];
+                }
         }
         __syncthreads();
+        const int bin = s_bin;
+        if (bin >= 0) {
+            for (int i = t; i < K; i += SEL_T) {
+                const int k = keys[i];
+                if ((k >> 7) == bin)
+                    atomicAdd(&hf[k & 127], 1);
+            }
+            __syncthreads();
+            if (t < 64) { /* lane l: fine bins 2 l, 2 l + 1 */
+                const int need = n - s_above;
+                const int v0 = hf[2 * lane], v1 = hf[2 * lane + 1];
+                const int sum = v0 + v1;
+                int inc = sum;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int v = __shfl_down(inc, o, 64);
+                    if (lane + o < 64)
+                        inc += v;
+                }
+                const int c2 = inc - sum, c1 = c2 + v1, c0 = c1 + v0;
+                if (c0 >= need && c1 < need)
+                    s_thr = (bin << 7) | (2 * lane);
+                if (c1 >= need && c2 < need)
+                    s_thr = (bin << 7) | (2 * lane + 1);
+            }
+        }
+        __syncthreads();
+        const int r = s_thr;
+        __syncthreads(); /* s_thr is reused by the next call */
+        return r;
+    };
+    const int cap = rank(nsel);
+    int thr = max(cap, tkey);
+    if (tkey < 0) { /* relational price: tau = -tkey / 1024 times mean |x| */
+        float acc = 0.0f;
+        for (int i = lo; i < hi; ++i)
+            acc += sel_mag(keys[i]);
+        red[t] = acc;
+        __syncthreads();
+#pragma unroll
+        for (int off = SEL_T / 2; off >= 1; off >>= 1) {
+            if (t < off)
+                red[t] = red[t] + red[t + off];
+            __syncthreads();
+        }
+        float tv = red[0] / (float)K * (float)(-tkey) / 1024.0f;
+        int rk = 1;
+        if (tv > 0.0f) {
+            int e2 = 0;
+            while (tv >= 2.0f && e2 < 100) {
+                tv *= 0.5f;
+                ++e2;
+            }
+            while (tv < 1.0f && e2 > -120) {
+                tv *= 2.0f;
+                --e2;
+            }
+            rk = min(max(((e2 + 127) << 7) | (int)((tv - 1.0f) * 128.0f), 1), 32767);
+        }
+        thr = max(thr, rk);
     }
-    const int thr = s_thr;
-    const int per = (K + SEL_T - 1) / SEL_T;
-    const int lo = min(t * per, K), hi = min(lo + per, K);
+    if (nfloor > 0 && tkey != 0)
+        thr = max(cap, min(thr, rank(nfloor)));
+    if (nsel == 0)
+        thr = 32768;
     int mine = 0;
     for (int i = lo; i < hi; ++i)
         mine += keys[i] >= thr;
@@ -371,8 +426,11 @@ __global__ __launch_bounds__(SEL_T) void k_select_topk(const uint16_t *__restric
     for (int i = lo; i < hi; ++i)
         if (keys[i] >= thr)
             idx[pos++] = i;
-    if (t == 0)
+    if (t == 0) {
         cnt[0] = total;
+        if (cnt_log)
+            cnt_log[slot] = total;
+    }
 }
 
 /* ---------------------------------------------------------------- correction */
@@ -485,13 +543,18 @@ GLINT_API int glint_gemv_km_fold(const uint8_t *hole_k, const float *scales_k, c
     return km_launched();
 }
 
-GLINT_API int glint_select_topk(const uint16_t *x, int K, int nsel, int32_t *idx, int32_t *cnt, hipStream_t stream) {
+GLINT_API int glint_select_topk_ex(const uint16_t *x, int K, int nsel, int tkey, int nfloor, int32_t *idx,
+                                   int32_t *cnt, int32_t *cnt_log, int slot, hipStream_t stream) {
     if (!x || !idx || !cnt)
         return -1;
-    if (K < 1 || K > SEL_MAX_K || nsel < 0)
+    if (K < 1 || K > SEL_MAX_K || (cnt_log && slot < 0))
         return -2;
-    k_select_topk<<<1, SEL_T, 0, stream>>>(x, K, nsel, idx, cnt);
+    k_select_topk<<<1, SEL_T, 0, stream>>>(x, K, nsel, tkey, nfloor, idx, cnt, cnt_log, slot);
     return km_launched();
+}
+
+GLINT_API int glint_select_topk(const uint16_t *x, int K, int nsel, int32_t *idx, int32_t *cnt, hipStream_t stream) {
+    return glint_select_topk_ex(x, K, nsel, 0, 0, idx, cnt, nullptr, 0, stream);
 }
 
 GLINT_API int glint_apply_corr_km(const uint8_t *hole_k, const uint8_t *plug_k, const float *scales_k,

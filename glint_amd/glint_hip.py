@@ -62,6 +62,7 @@ _ENCODE_SIGS = {
     "glint_kmajor_pack": ([VP, VP, VP, I32, I32, VP, VP, VP, VP], I32),
     "glint_gemv_km_fold": ([VP, VP, VP, VP, I32, I32, I32, VP, VP], I32),
     "glint_select_topk": ([VP, I32, I32, VP, VP, VP], I32),
+    "glint_select_topk_ex": ([VP, I32, I32, I32, I32, VP, VP, VP, I32, VP], I32),
     "glint_apply_corr_km": ([VP, VP, VP, VP, VP, VP, VP, I32, I32, I32, VP, VP], I32),
 }
 
@@ -269,14 +270,21 @@ def gemv_km_fold(hole_k, scales_k, x, N: int, K: int, ksg: int = 1, y=None, part
     return y
 
 
-def select_topk(x, nsel: int, idx=None, cnt=None, stream=None):
-    """Kept channels of x (ascending) and their count, both on the device."""
+def select_topk(x, nsel: int, idx=None, cnt=None, stream=None, tkey: int = 0, nfloor: int = 0, cnt_log=None,
+                slot: int = 0):
+    """Kept channels of x (ascending) and their count, both on the device (the rank rule,
+    and the price / relational / floor rules when tkey or nfloor is given)."""
     torch = _torch()
     x = _as_u16(x)
     K = x.numel()
     idx = torch.empty(K, dtype=torch.int32, device=x.device) if idx is None else idx
     cnt = torch.empty(1, dtype=torch.int32, device=x.device) if cnt is None else cnt
-    _check(encode_lib().glint_select_topk(_p(x), K, nsel, _p(idx), _p(cnt), _stream(stream)), "glint_select_topk")
+    if tkey == 0 and nfloor == 0 and cnt_log is None:
+        _check(encode_lib().glint_select_topk(_p(x), K, nsel, _p(idx), _p(cnt), _stream(stream)), "glint_select_topk")
+    else:
+        _check(encode_lib().glint_select_topk_ex(_p(x), K, nsel, tkey, nfloor, _p(idx), _p(cnt),
+                                                 _p(cnt_log) if cnt_log is not None else None, slot,
+                                                 _stream(stream)), "glint_select_topk_ex")
     return idx, cnt
 
 

@@ -8,7 +8,8 @@
  *   scales_k [K/64][N] f32: scales_k[(c / 64) * N + r] = absmax[r * K/64 + c / 64];
  *   fold:       y[r] = sum_c (PARENT[h] * scale) * x[c], in slices (see below);
  *   selection:  key = bf16 bits & 0x7FFF, keep every channel with key >= T, T the largest
- *               value such that at least nsel channels have key >= T (ties kept);
+ *               value such that at least nsel channels have key >= T (ties kept), raised
+ *               by a fixed or relational price and lowered to a floor (glint_select_topk_ex);
  *   correction: y[r] += sum_i (CELLS[h][p] - PARENT[h]) * scale * x[c_i] over the kept
  *               channels in ascending order.
  * Fold plus the correction over every channel equals the full-cell GEMV up to the order
@@ -45,8 +46,27 @@ int glint_gemv_km_fold(const uint8_t *hole_k, const float *scales_k, const uint1
                        int ksg, float *part, struct ihipStream_t *stream);
 
 /* Channel selection on the device: writes the kept channels of x (BF16 bits [K]) to
- * idx in ascending order (at most K entries) and their number to cnt[0]. nsel == 0
- * keeps nothing; nsel >= K keeps everything. 1 <= K <= 32768.
+ * idx in ascending order (at most K entries) and their number to cnt[0] (and to
+ * cnt_log[slot] when cnt_log is not NULL). With key = bits & 0x7FFF and
+ * rank(n) = the largest 15-bit T with #{key >= T} >= n (32767 for n <= 0, 0 for n > K):
+ *   T = rank(nsel);
+ *   tkey > 0 (price): T = max(T, tkey);
+ *   tkey < 0 (relational price, tau = -tkey / 1024): T = max(T, key(tau * mean |x|)), the
+ *     mean summed in f32 over 1024 ranges of ceil(K / 1024) channels and a pairwise tree,
+ *     |x| = (128 + mantissa) 2^(exponent - 134) with the power clamped to [-60, 40] (0 for
+ *     zero and subnormal keys), t = (sum / K) * (-tkey) / 1024 in f32, key(t) = biased
+ *     exponent << 7 | 7 truncated mantissa bits, clamped to [1, 32767], 1 when t <= 0;
+ *   nfloor > 0 and tkey != 0: T = max(rank(nsel), min(T, rank(nfloor)));
+ *   nsel == 0: nothing is kept.
+ * Every channel with key >= T is kept (ties at T included). 1 <= K <= 32768; slot >= 0
+ * when cnt_log is given.
+ * Reference: mojo/p7_select_device.mojo:8-151 (select_topk with tkey, nfloor, cnt_log). */
+int glint_select_topk_ex(const uint16_t *x, int K, int nsel, int tkey, int nfloor, int32_t *idx, int32_t *cnt,
+                         int32_t *cnt_log, int slot, struct ihipStream_t *stream);
+
+/* The rank rule alone: glint_select_topk_ex with tkey = 0, nfloor = 0, no count log.
+ * nsel == 0 keeps nothing; nsel >= K keeps everything; nsel < 0 keeps the channels with
+ * key 0x7FFF (T = 32767, as the reference's bisection leaves it).
  * Reference: mojo/p7_select_device.mojo:1-151 (select_topk, the rank rule). */
 int glint_select_topk(const uint16_t *x, int K, int nsel, int32_t *idx, int32_t *cnt, struct ihipStream_t *stream);
 

@@ -429,26 +429,108 @@ EXPORT void oracle_gemv_km_fold(const uint8_t *hole_k, const float *scales_k, co
     }
 }
 
-/* Selection (p7_select_device.mojo:1-151, the rank rule): key = bf16 bits & 0x7FFF; T is
- * the largest 15-bit value with #{key >= T} >= nsel, found bit by bit from the top;
- * nsel == 0 selects nothing. Writes the kept channels in ascending order, returns the count. */
-EXPORT int oracle_select_topk(const uint16_t *x, int K, int nsel, int32_t *idx) {
+/* Selection (p7_select_device.mojo:1-151): key = bf16 bits & 0x7FFF.
+ *   rank(n): the largest 15-bit T with #{key >= T} >= n, found bit by bit from the top
+ *            (:31-48); n <= 0 leaves every bit set (T = 32767), n > K leaves T = 0.
+ *   T = rank(nsel) (the cap);
+ *   tkey > 0: T = max(T, tkey) (price, :51-54);
+ *   tkey < 0: tau = -tkey / 1024, m = mean |x| summed in f32 over 1024 thread ranges of
+ *             ceil(K / 1024) channels and a pairwise tree (:55-77), t = m * tau as
+ *             (sum / K) * (-tkey) / 1024 in f32, its key r = biased exponent << 7 | 7 mantissa
+ *             bits by truncation, clamped to [1, 32767], 1 when t <= 0 (:78-92);
+ *             T = max(T, r);
+ *   nfloor > 0 and tkey != 0: T = max(cap, min(T, rank(nfloor))) (:93-114);
+ *   nsel == 0: T = 32768, nothing kept (:115-117).
+ * Writes the kept channels in ascending order, returns the count. */
+static int sel_rank(const uint16_t *x, int K, int n) {
     int thr = 0;
     for (int bi = 0; bi < 15; ++bi) {
         const int cand = thr | (1 << (14 - bi));
         int cnt = 0;
         for (int i = 0; i < K; ++i)
             cnt += (x[i] & 0x7FFF) >= cand;
-        if (cnt >= nsel)
+        if (cnt >= n)
             thr = cand;
+    }
+    return thr;
+}
+
+/* |x| of a key from its exponent and mantissa fields, 2^(e-134) clamped to
+ * [2^-60, 2^40]; 0 for zero and subnormal keys (p7_select_device.mojo:60-74) */
+static float sel_mag(int k) {
+    const int ex = k >> 7;
+    if (ex <= 0)
+        return 0.0f;
+    int n = ex - 134;
+    n = n > 40 ? 40 : n < -60 ? -60 : n;
+    return ldexpf((float)(128 + (k & 127)), n); /* exact: a power-of-two scale of an 8-bit integer */
+}
+
+EXPORT int oracle_select_price_key(const uint16_t *x, int K, int tkey) {
+    enum { SB = 1024 };
+    float red[SB];
+    const int per = (K + SB - 1) / SB;
+    for (int t = 0; t < SB; ++t) {
+        const int lo = t * per, hi = lo + per < K ? lo + per : K;
+        float acc = 0.0f;
+        for (int i = lo; i < hi; ++i)
+            acc += sel_mag(x[i] & 0x7FFF);
+        red[t] = acc;
+    }
+    for (int off = SB / 2; off >= 1; off >>= 1)
+        for (int t = 0; t < off; ++t)
+            red[t] = red[t] + red[t + off];
+    float tv = red[0] / (float)K * (float)(-tkey) / 1024.0f;
+    int rk = 1;
+    if (tv > 0.0f) {
+        int e2 = 0;
+        while (tv >= 2.0f && e2 < 100) {
+            tv *= 0.5f;
+            ++e2;
+        }
+        while (tv < 1.0f && e2 > -120) {
+            tv *= 2.0f;
+            --e2;
+        }
+        rk = ((e2 + 127) << 7) | (int)((tv - 1.0f) * 128.0f);
+        rk = rk < 1 ? 1 : rk > 32767 ? 32767 : rk;
+    }
+    return rk;
+}
+
+EXPORT int oracle_select_threshold(const uint16_t *x, int K, int nsel, int tkey, int nfloor) {
+    const int cap = sel_rank(x, K, nsel);
+    int thr = cap;
+    if (tkey > thr)
+        thr = tkey;
+    if (tkey < 0) {
+        const int rk = oracle_select_price_key(x, K, tkey);
+        if (rk > thr)
+            thr = rk;
+    }
+    if (nfloor > 0 && tkey != 0) {
+        const int thf = sel_rank(x, K, nfloor);
+        if (thf < thr)
+            thr = thf;
+        if (thr < cap)
+            thr = cap;
     }
     if (nsel == 0)
         thr = 32768;
+    return thr;
+}
+
+EXPORT int oracle_select_ex(const uint16_t *x, int K, int nsel, int tkey, int nfloor, int32_t *idx) {
+    const int thr = oracle_select_threshold(x, K, nsel, tkey, nfloor);
     int n = 0;
     for (int i = 0; i < K; ++i)
         if ((x[i] & 0x7FFF) >= thr)
             idx[n++] = i;
     return n;
+}
+
+EXPORT int oracle_select_topk(const uint16_t *x, int K, int nsel, int32_t *idx) {
+    return oracle_select_ex(x, K, nsel, 0, 0, idx);
 }
 
 /* Plug correction over the selected channels (p7_select_device.mojo:208-236, 253-302):

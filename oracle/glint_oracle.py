@@ -223,6 +223,9 @@ class Oracle:
             "oracle_kmajor_pack": ([vp, vp, vp, i32, i32, vp, vp, vp], None),
             "oracle_gemv_km_fold": ([vp, vp, vp, i32, i32, i32, vp], None),
             "oracle_select_topk": ([vp, i32, i32, vp], i32),
+            "oracle_select_ex": ([vp, i32, i32, i32, i32, vp], i32),
+            "oracle_select_threshold": ([vp, i32, i32, i32, i32], i32),
+            "oracle_select_price_key": ([vp, i32, i32], i32),
             "oracle_apply_corr_km": ([vp, vp, vp, vp, vp, i32, i32, i32, i32, vp], None),
             "oracle_threads": ([], i32),
         }
@@ -372,6 +375,20 @@ class Oracle:
         idx = np.empty(max(K, 1), np.int32)
         n = self.lib.oracle_select_topk(_ptr(x_u16), K, nsel, _ptr(idx))
         return idx[:n].copy()
+
+    def select_ex(self, x_u16, K: int, nsel: int, tkey: int = 0, nfloor: int = 0) -> np.ndarray:
+        x_u16 = np.ascontiguousarray(x_u16, np.uint16)
+        idx = np.empty(max(K, 1), np.int32)
+        n = self.lib.oracle_select_ex(_ptr(x_u16), K, nsel, tkey, nfloor, _ptr(idx))
+        return idx[:n].copy()
+
+    def select_threshold(self, x_u16, K: int, nsel: int, tkey: int = 0, nfloor: int = 0) -> int:
+        x_u16 = np.ascontiguousarray(x_u16, np.uint16)
+        return int(self.lib.oracle_select_threshold(_ptr(x_u16), K, nsel, tkey, nfloor))
+
+    def select_price_key(self, x_u16, K: int, tkey: int) -> int:
+        x_u16 = np.ascontiguousarray(x_u16, np.uint16)
+        return int(self.lib.oracle_select_price_key(_ptr(x_u16), K, tkey))
 
     def apply_corr_km(self, hole_k, plug_k, scales_k, x_u16, idx, N: int, K: int, y, ks: int = 1) -> np.ndarray:
         arrs = [np.ascontiguousarray(a, t) for a, t in ((hole_k, np.uint8), (plug_k, np.uint8),

@@ -65,14 +65,39 @@ def test_select_matches_oracle(oracle, K):
     if K > 200:
         x[100:160] = x[3]  # ties at many thresholds
     dx = dev(x)
-    for nsel in sorted({0, 1, 2, K // 10, K // 2, K - 1, K, K + 3}):
-        if nsel < 0:
-            continue
+    for nsel in sorted({-1, 0, 1, 2, K // 10, K // 2, K - 1, K, K + 3}):
         want = oracle.select_topk(x, K, nsel)
         idx, cnt = H.select_topk(dx, nsel)
         n = int(host(cnt)[0])
         assert n == want.size, (nsel, n, want.size)
         assert np.array_equal(host(idx)[:n], want), nsel
+
+
+@pytest.mark.parametrize("K", [1, 100, 4096, 14336, 32768])
+def test_select_price_floor_and_log_match_oracle(oracle, K):
+    """glint_select_topk_ex: fixed price (tkey > 0), relational price (tkey < 0, the f32
+    mean in the rule's order), the floor, and the count log slot, against the oracle."""
+    torch = torch_cuda()
+    print(f"select_ex K={K}", flush=True)
+    rng = np.random.default_rng(K + 5)
+    x = G.f32_to_bf16_bits((rng.normal(0, 1, K) * 2.0 ** rng.integers(-6, 6, K)).astype(np.float32))
+    if K > 64:
+        x[10:40] = x[3]
+        x[50] = 0x7F80  # inf key, clamped in the mean
+        x[51] = 0x0003  # subnormal key, 0 in the mean
+    dx = dev(x)
+    keys = (x & 0x7FFF).astype(np.int64)
+    log = torch.full((8,), -7, dtype=torch.int32, device="cuda")
+    cases = [(max(K // 10, 1), int(np.median(keys)), 0), (max(K // 10, 1), -1024, 0), (max(K // 10, 1), -300, 0),
+             (max(K // 2, 1), -4000, max(K // 20, 1)), (max(K // 50, 1), 32000, max(K // 5, 1)),
+             (max(K // 50, 1), -1, 3), (0, -1024, 5), (-1, 100, 2), (K, -2048, 1), (3, 0, 2)]
+    for slot, (nsel, tkey, nfloor) in enumerate(cases):
+        want = oracle.select_ex(x, K, nsel, tkey, nfloor)
+        idx, cnt = H.select_topk(dx, nsel, tkey=tkey, nfloor=nfloor, cnt_log=log, slot=slot % 8)
+        n = int(host(cnt)[0])
+        assert n == want.size, (nsel, tkey, nfloor, n, want.size)
+        assert np.array_equal(host(idx)[:n], want), (nsel, tkey, nfloor)
+        assert int(host(log)[slot % 8]) == n
 
 
 @pytest.mark.parametrize("N,K,frac,ks", [(96, 640, 0.1, 1), (1024, 320, 0.5, 3), (2080, 1024, 0.3, 2),
@@ -117,7 +142,8 @@ def test_argument_codes():
     assert lib.glint_gemv_km_fold(P(b), P(f), P(b), P(f), 40, 128, 1, None, None) == -2  # N % 32
     assert lib.glint_select_topk(P(b), 0, 1, P(i), P(i), None) == -2
     assert lib.glint_select_topk(P(b), 40000, 1, P(i), P(i), None) == -2
-    assert lib.glint_select_topk(P(b), 64, -1, P(i), P(i), None) == -2
+    assert lib.glint_select_topk_ex(P(b), 64, 1, 0, 0, P(i), P(i), P(i), -1, None) == -2  # slot < 0 with a log
+    assert lib.glint_select_topk_ex(None, 64, 1, 0, 0, P(i), P(i), None, 0, None) == -1
     assert lib.glint_apply_corr_km(P(b), P(b), P(f), P(b), P(i), P(i), P(f), 32, 64, 2, None, None) == -1
     assert lib.glint_apply_corr_km(P(b), P(b), P(f), P(b), P(i), P(i), P(f), 48, 64, 1, None, None) == -2
     torch.cuda.synchronize()

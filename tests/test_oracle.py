@@ -542,6 +542,82 @@ def test_select_matches_a_sort(oracle):
         assert nsel == 0 or got.size >= min(nsel, K)
 
 
+def _rank_brute(keys, n):
+    """The largest 15-bit T with #{key >= T} >= n, by trying every T (0 when none)."""
+    counts = np.cumsum(np.bincount(keys, minlength=32768)[::-1])[::-1]  # counts[T] = #{key >= T}
+    ok = np.flatnonzero(counts >= n)
+    return int(ok.max()) if ok.size else 0
+
+
+def _key_of(t):
+    """The rule's key of a positive float: biased exponent << 7 | 7 truncated mantissa bits."""
+    m, e = np.frexp(np.float64(t))  # t = m 2^e, m in [0.5, 1)
+    return int(((e - 1 + 127) << 7) | int((m * 2 - 1) * 128))
+
+
+def test_select_rules_against_brute_force(oracle):
+    """Threshold of the rank, price, relational and floor rules (p7_select_device.mojo:8-151)
+    against a brute-force rank and a float64 mean: rank(n) for every n (n <= 0 -> 32767);
+    tkey > 0 raises T to tkey; tkey < 0 raises it to key(tau mean|x|) (skipping draws whose
+    tau mean|x| sits within 1e-4 of a 7-bit key boundary, where f32 order decides);
+    nfloor lowers a price to the floor's rank but never below the cap; nsel == 0 keeps nothing."""
+    rng = np.random.default_rng(11)
+    for trial in range(40):
+        K = int(rng.integers(1, 3000))
+        x = G.f32_to_bf16_bits((rng.normal(0, 1, K) * 2.0 ** rng.integers(-8, 8, K)).astype(np.float32))
+        if trial % 5 == 0:
+            x[: K // 3] = x[0]  # ties
+        keys = (x & 0x7FFF).astype(np.int64)
+        for nsel in sorted({-1, 1, 2, K // 7, K // 2, K, K + 1}):
+            cap = 32767 if nsel <= 0 else _rank_brute(keys, nsel)
+            assert oracle.select_threshold(x, K, nsel) == cap, (trial, nsel)
+            tk = int(rng.integers(1, 32768))
+            assert oracle.select_threshold(x, K, nsel, tkey=tk) == max(cap, tk)
+            tau = int(rng.integers(1, 4096))
+            ex = keys >> 7
+            mag = np.where(ex > 0, (128 + (keys & 127)) * 2.0 ** np.clip(ex - 134, -60, 40), 0.0)
+            t = mag.sum() / K * tau / 1024
+            rel = oracle.select_price_key(x, K, -tau)
+            if t > 0:
+                lo, hi = _key_of(t * (1 - 1e-4)), _key_of(t * (1 + 1e-4))
+                if lo == hi:
+                    assert rel == min(max(lo, 1), 32767), (trial, tau, t)
+            assert oracle.select_threshold(x, K, nsel, tkey=-tau) == max(cap, rel)
+            nf = int(rng.integers(1, K + 1))
+            for tkey in (tk, -tau):
+                price = max(cap, tkey if tkey > 0 else rel)
+                want = max(cap, min(price, _rank_brute(keys, nf)))
+                assert oracle.select_threshold(x, K, nsel, tkey=tkey, nfloor=nf) == want
+            assert oracle.select_threshold(x, K, nsel, tkey=0, nfloor=nf) == cap  # no price: no floor
+        assert oracle.select_ex(x, K, 0, tkey=-tau, nfloor=3).size == 0
+        thr = oracle.select_threshold(x, K, K // 3 + 1, tkey=-tau, nfloor=5)
+        assert np.array_equal(oracle.select_ex(x, K, K // 3 + 1, tkey=-tau, nfloor=5), np.flatnonzero(keys >= thr))
+
+
+def test_select_relational_known_answers(oracle):
+    """Equal magnitudes make mean|x| exact: |x| = 1 for all channels gives key(tau) for tau =
+    -tkey / 1024; zero and subnormal keys count 0 but still divide by K; an inf key is read as
+    (128) 2^40 by the clamp; nsel < 0 leaves T = 32767, so only 0x7FFF keys are kept."""
+    one = np.full(1000, 0x3F80, np.uint16)
+    one[::2] |= 0x8000
+    assert oracle.select_price_key(one, 1000, -1024) == 0x3F80  # tau 1
+    assert oracle.select_price_key(one, 1000, -512) == 0x3F00   # tau 1/2
+    assert oracle.select_price_key(one, 1000, -1536) == 0x3FC0  # tau 3/2
+    assert oracle.select_ex(one, 1000, 1, tkey=-1536).size == 0
+    assert oracle.select_ex(one, 1000, 1, tkey=-1024).size == 1000
+    half = one.copy()
+    half[500:] = 0x0001  # subnormal: contributes 0
+    assert oracle.select_price_key(half, 1000, -1024) == 0x3F00  # mean 1/2
+    z = np.zeros(64, np.uint16)
+    assert oracle.select_price_key(z, 64, -1024) == 1  # t = 0
+    inf = np.zeros(1024, np.uint16)
+    inf[0] = 0x7F80  # 2^47 / 1024 = 2^37
+    assert oracle.select_price_key(inf, 1024, -1024) == (37 + 127) << 7
+    nan = np.array([0x7FFF, 0x3F80, 0xFFFF, 0x0000], np.uint16)
+    assert np.array_equal(oracle.select_ex(nan, 4, -1), [0, 2])
+    assert oracle.select_ex(nan, 4, 0).size == 0
+
+
 def test_fold_plus_full_correction_is_the_htile_sum(oracle):
     """PARENT + (CELLS - PARENT) = CELLS: fold plus the correction over every channel is the
     H-TILE GEMV up to f32 rounding, bounded by (K + 4) 2^-23 sum |terms| against float64."""
