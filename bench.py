@@ -461,12 +461,26 @@ def bench_pin_tools(tensors: int = 16):
             "unpin_bf16_out_gbs": gb / t_unpin}
 
 
-def cpu_baseline(seconds_target: float = 20.0):
-    """The CPU path beside the GPU, on this host: the repo's C restatement of the reference
-    host path (oracle/glint_oracle.c, OpenMP over the threads it reports) running the
-    headline GEMV (expand-on-the-fly H-TILE, f32 accumulate) at full size, and encoding the
-    CPU-reference configuration (4096x4096, seed 1001, 0.1% outliers x10). Also the numpy
-    restatement (one core) on a 256-row sample. Each leg is repeated for a bounded time."""
+def cpu_model() -> str:
+    """The host CPU's model name (the lscpu 'Model name' line, read from /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(seconds_target: float = 24.0):
+    """The CPU path beside the GPU, on this host, each leg repeated for a bounded time:
+    the repo's C restatement of the reference host path (oracle/glint_oracle.c, OpenMP over
+    the threads it reports) running the headline GEMV (expand-on-the-fly H-TILE, f32
+    accumulate) at full size and encoding the CPU-reference configuration (4096x4096, seed
+    1001, 0.1% outliers x10); the numpy restatement (one core) of encode, expand and a GEMV
+    on row samples; numpy expand + BLAS x @ W^T at the prefill shape (a row sample of W); and
+    the C int32 INT8 GEMM on a full-row sample of 2048x8192x8192."""
+    import os
     import numpy as np
     from oracle import glint_oracle as G
     orc = G.Oracle()
@@ -480,33 +494,66 @@ def cpu_baseline(seconds_target: float = 20.0):
     def rate(fn, budget):
         fn()
         t0, reps = time.perf_counter(), 0
-        while time.perf_counter() - t0 < budget:
+        while time.perf_counter() - t0 < budget or reps == 0:
             fn()
             reps += 1
         return (time.perf_counter() - t0) / reps, reps
 
-    gemv_s, gemv_reps = rate(lambda: orc.htile_f32(hole, plug, am, x, 1, N, K, 64), seconds_target * 0.4)
+    T = seconds_target
+    gemv_s, gemv_reps = rate(lambda: orc.htile_f32(hole, plug, am, x, 1, N, K, 64), T * 0.3)
     rng = np.random.default_rng(1001)
     n0 = 4096 * 4096
     w0 = rng.normal(0.0, 0.02, n0).astype(np.float32)
     w0[rng.choice(n0, n0 // 1000, replace=False)] *= np.float32(10.0)
     u0 = G.f32_to_bf16_bits(w0)
-    enc_s, enc_reps = rate(lambda: orc.encode_bf16(u0, 64), seconds_target * 0.3)
+    enc_s, enc_reps = rate(lambda: orc.encode_bf16(u0, 64), T * 0.2)
+    # numpy restatement, one core: encode / expand of 256 rows of the 4096^2 config, GEMV rows
     rows = 256
+    ws0 = G.bf16_bits_to_f32(u0[:rows * 4096])
+    npe_s, npe_reps = rate(lambda: G.encode_f32(ws0, 64), T * 0.1)
+    h0, p0, a0 = G.encode_f32(ws0, 64)
+    npx_s, npx_reps = rate(lambda: G.expand(h0, p0, a0, rows * 4096, 64), T * 0.05)
     hs, ps, ams = hole[:rows * K // 2], plug[:rows * K // 2], am[:rows * K // 64]
     xf = G.bf16_bits_to_f32(x)
-    np_s, np_reps = rate(lambda: G.expand(hs, ps, ams, rows * K, 64).reshape(rows, K) @ xf, seconds_target * 0.2)
+    np_s, np_reps = rate(lambda: G.expand(hs, ps, ams, rows * K, 64).reshape(rows, K) @ xf, T * 0.05)
+    # numpy expand + BLAS GEMM at the prefill shape (M 512 x 4096 against 1024 of W's 14336 rows)
+    Mp, rows_p = 512, 1024
+    Xp = np.random.default_rng(3001).normal(0.0, 1.0, (Mp, K)).astype(np.float32)
+    hp, pp, ap_ = hole[:rows_p * K // 2], plug[:rows_p * K // 2], am[:rows_p * K // 64]
+    pf_s, pf_reps = rate(lambda: Xp @ G.expand(hp, pp, ap_, rows_p * K, 64).reshape(rows_p, K).T, T * 0.1)
+    try:
+        from threadpoolctl import threadpool_info
+        blas_threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"),
+                           default=None)
+    except Exception:
+        blas_threads = None
+    # C int32 INT8 GEMM, rows [0, 32) of the 2048 x 8192 x 8192 config
+    M8, N8, K8, r8 = 2048, 8192, 8192, 32
+    g8 = np.random.default_rng(5001)
+    A = g8.integers(-127, 128, (M8, K8), dtype=np.int8)
+    B = np.random.default_rng(5002).integers(-127, 128, (N8, K8), dtype=np.int8)
+    i8_s, i8_reps = rate(lambda: orc.int8_gemm_i32(A, B, M8, N8, K8, 0, r8), T * 0.2)
     threads = orc.threads()
     return {
         "value": gemv_bytes(N, K) / gemv_s / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
         "sample": f"C oracle H-TILE GEMV 14336x4096 (bs 64, bf16 x, f32 accumulate), full size, "
-                  f"{gemv_reps} runs in ~{seconds_target * 0.4:.0f} s, OpenMP {threads} threads",
+                  f"{gemv_reps} runs in ~{T * 0.3:.0f} s, OpenMP {threads} threads",
+        "cpu_model": cpu_model(), "nproc": os.cpu_count(),
         "gemv_us": gemv_s * 1e6,
         "encode_bf16_in_gbs": 2 * n0 / enc_s / 1e9, "encode_threads": threads,
         "encode_sample": f"C oracle encode of the 4096x4096 CPU-reference config (seed 1001, 0.1% outliers), "
                          f"{enc_reps} runs",
+        "numpy_encode_gbs": 2 * rows * 4096 / npe_s / 1e9, "numpy_expand_f32_out_gbs": 4 * rows * 4096 / npx_s / 1e9,
         "numpy_gemv_gbs": gemv_bytes(rows, K) / np_s / 1e9, "numpy_cores": 1,
-        "numpy_sample": f"numpy glint_np restatement: expand + x @ W^T of {rows}x{K} rows, {np_reps} runs",
+        "numpy_sample": f"numpy restatement (oracle/glint_oracle.py), one core: encode_f32 of 256 rows of the 4096^2 "
+                        f"config ({npe_reps} runs), expand of the same ({npx_reps} runs), expand + x @ W^T of "
+                        f"{rows}x{K} GEMV rows ({np_reps} runs)",
+        "numpy_prefill_tflops": 2.0 * Mp * rows_p * K / pf_s / 1e12, "blas_threads": blas_threads,
+        "numpy_prefill_sample": f"numpy expand + BLAS X[{Mp}x{K}] @ W^T over {rows_p} of the 14336 gate rows, "
+                                f"{pf_reps} runs",
+        "int8_cpu_tops": 2.0 * r8 * N8 * K8 / i8_s / 1e12, "int8_threads": threads,
+        "int8_sample": f"C oracle int32 GEMM, rows [0, {r8}) of A[2048x8192] against all of B[8192x8192] "
+                       f"(full rows), {i8_reps} runs",
     }
 
 
