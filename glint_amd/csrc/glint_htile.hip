@@ -215,12 +215,16 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #ifndef GEMV_G1_DIV
 #define GEMV_G1_DIV 2 /* one row group per workgroup (G == 1: S = K / 2048 >= 5, K >= 10240): resident grid / this */
 #endif
+#ifndef GEMV_X_DEPTH_S2
+#define GEMV_X_DEPTH_S2 1 /* rows of loads in flight per wave at S <= 2 slices (K <= 4096) */
+#endif
 #ifndef GEMV_X_DEPTH
-#define GEMV_X_DEPTH 2 /* rows of loads in flight per wave (3 and 4 measured 2% and 12% slower) */
+#define GEMV_X_DEPTH 2 /* rows of loads in flight per wave at S > 2 (3 and 4 measured 2% and 12% slower) */
 #endif
 #ifndef GEMV_X_PRE
-#define GEMV_X_PRE GEMV_X_DEPTH /* of those, rows issued before the table fill's barrier */
+#define GEMV_X_PRE 8 /* most rows issued before the table fill's barrier */
 #endif
+#define GEMV_X_PRE_OF(D) ((GEMV_X_PRE) < (D) ? (GEMV_X_PRE) : (D))
 #ifndef GEMV_X_NO_RELOAD
 #define GEMV_X_NO_RELOAD 1 /* the ring loads no row past the wave's last */
 #endif
@@ -295,7 +299,7 @@ __device__ __forceinline__ void glint_cells_fill_sstore(float *ltab, const Glint
  * XC blockDim.x >= K / 8; threads past the last chunk load it again and store nothing), the
  * G waves of a slice then read it from LDS instead of each loading it from L2. XC == 0:
  * each wave loads its slice itself (G == 1, no repeats). */
-template <int EL, bool OUT_BF16, int XC>
+template <int EL, bool OUT_BF16, int XC, int DEPTH>
 __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE))) void k_htile_gemv_xreg(
     const void *__restrict__ hole, const void *__restrict__ plug, const float *__restrict__ absmax,
     const glint_u32x4 *__restrict__ x, void *__restrict__ y, int N, int K, int G, int rows_per_wg) {
@@ -330,9 +334,9 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
             xv[q] = x[j * Q + q];
     }
     __builtin_amdgcn_sched_barrier(0);
-    GemvRow<EL> buf[GEMV_X_DEPTH];
+    GemvRow<EL> buf[DEPTH];
 #pragma unroll
-    for (int d = 0; d < GEMV_X_PRE; ++d)
+    for (int d = 0; d < GEMV_X_PRE_OF(DEPTH); ++d)
         gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, j, buf[d]);
     __builtin_amdgcn_sched_barrier(0);
     glint_cells_fill_sstore(ltab, fill);
@@ -360,7 +364,7 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
     if (XC > 0)
         __syncthreads(); /* x is read out before the row partials reuse its LDS */
 #pragma unroll
-    for (int d = GEMV_X_PRE; d < GEMV_X_DEPTH; ++d)
+    for (int d = GEMV_X_PRE_OF(DEPTH); d < DEPTH; ++d)
         gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, j, buf[d]);
 
     auto compute_row = [&](int i, const GemvRow<EL> &row) {
@@ -394,34 +398,34 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
      * a request for nothing. */
     int i = 0;
 #if GEMV_X_NO_RELOAD
-    for (; i + 2 * GEMV_X_DEPTH <= my; i += GEMV_X_DEPTH) {
+    for (; i + 2 * DEPTH <= my; i += DEPTH) {
 #pragma unroll
-        for (int d = 0; d < GEMV_X_DEPTH; ++d) {
+        for (int d = 0; d < DEPTH; ++d) {
             compute_row(i + d, buf[d]);
-            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + GEMV_X_DEPTH), nch, j, buf[d]);
+            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, j, buf[d]);
         }
     }
 #pragma unroll
-    for (int d = 0; d < GEMV_X_DEPTH; ++d)
+    for (int d = 0; d < DEPTH; ++d)
         if (i + d < my) {
             compute_row(i + d, buf[d]);
-            if (i + d + GEMV_X_DEPTH < my)
-                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + GEMV_X_DEPTH), nch, j, buf[d]);
+            if (i + d + DEPTH < my)
+                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, j, buf[d]);
         }
 #pragma unroll
-    for (int d = 0; d < GEMV_X_DEPTH; ++d)
-        if (i + GEMV_X_DEPTH + d < my)
-            compute_row(i + GEMV_X_DEPTH + d, buf[d]);
+    for (int d = 0; d < DEPTH; ++d)
+        if (i + DEPTH + d < my)
+            compute_row(i + DEPTH + d, buf[d]);
 #else
-    for (; i + GEMV_X_DEPTH <= my; i += GEMV_X_DEPTH) {
+    for (; i + DEPTH <= my; i += DEPTH) {
 #pragma unroll
-        for (int d = 0; d < GEMV_X_DEPTH; ++d) {
+        for (int d = 0; d < DEPTH; ++d) {
             compute_row(i + d, buf[d]);
-            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + GEMV_X_DEPTH), nch, j, buf[d]);
+            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, j, buf[d]);
         }
     }
 #pragma unroll
-    for (int d = 0; d < GEMV_X_DEPTH - 1; ++d)
+    for (int d = 0; d < DEPTH - 1; ++d)
         if (i + d < my)
             compute_row(i + d, buf[d]);
 #endif
@@ -537,8 +541,10 @@ static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, cons
                                   void *y, int N, int K, hipStream_t st) {
     const int S = K / (64 * GEMV_X_EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
     /* K / 8 chunks of x over 64 S G threads: 4 / G per thread */
-    auto kern = G >= 4 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 1>
-                       : (G >= 2 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 2> : k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 0>);
+    /* S <= 2 (G >= 4): one row in flight per wave; more slices: GEMV_X_DEPTH */
+    auto kern = S <= 2 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 1, GEMV_X_DEPTH_S2>
+                       : (G >= 2 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 2, GEMV_X_DEPTH>
+                                 : k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 0, GEMV_X_DEPTH>);
     const int64_t resident =
         std::max<int64_t>(glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4) / (G == 1 ? GEMV_G1_DIV : 1), 1);
     const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
