@@ -383,10 +383,12 @@ def bench_w8a16(torch, H, steps: int, copies: int = 6):
     return out
 
 
-def bench_kmajor(torch, H, steps: int = 100, copies: int = 20):
+def bench_kmajor(torch, H, steps: int = 200, copies: int = 20):
     """The K-major decode step at the decode shape (N 14336, K 4096): fold GEMV (HBM bytes:
     hole_k N K / 2 + scales_k N K / 16 + x + y), device selection of 10% of the channels,
-    and the plug correction over them. Pins rotate over `copies` (about 1.3 GB)."""
+    and the plug correction over them, each timed alone and as one step (three launches
+    back to back, C ABI through pre-bound ctypes calls). Pins rotate over `copies` (about
+    1.3 GB)."""
     N, K = GEMV_N, GEMV_K
     g = torch.Generator(device="cuda").manual_seed(4242)
     pins = []
@@ -398,18 +400,32 @@ def bench_kmajor(torch, H, steps: int = 100, copies: int = 20):
     x = torch.randn(K, device="cuda", generator=g).to(torch.bfloat16)
     y = torch.empty(N, dtype=torch.float32, device="cuda")
     part = torch.empty(32 * N, dtype=torch.float32, device="cuda")
-    ksg, ks = 16, 16  # 16 fold slices: the fastest count at 8 rows per lane (13.7 us against 14.4 at 32)
+    idx = torch.empty(K, dtype=torch.int32, device="cuda")
+    cnt = torch.empty(1, dtype=torch.int32, device="cuda")
+    lib, st = H.encode_lib(), stream_handle(torch)
+    ksg, ks, nsel = 16, 8, K // 10
     fold_bytes = N * K / 2 + N * K / 16 + 2 * K + 4 * N
-    ms_fold = timed(torch, [lambda pk=pk: H.gemv_km_fold(pk[0], pk[2], x, N, K, ksg, y=y, part=part) for pk in pins],
-                    steps, 10)
-    idx, cnt = H.select_topk(x, K // 10)
-    ms_sel = timed(torch, [lambda: H.select_topk(x, K // 10, idx=idx, cnt=cnt)], steps, 10)
-    ms_corr = timed(torch, [lambda pk=pk: H.apply_corr_km(pk[0], pk[1], pk[2], x, idx, cnt, y, N, K, ks, part=part)
-                            for pk in pins], steps, 10)
+    folds = [bound(lib.glint_gemv_km_fold, pk[0], pk[2], x, y, N, K, ksg, part, st) for pk in pins]
+    sel = bound(lib.glint_select_topk, x, K, nsel, idx, cnt, st)
+    corrs = [bound(lib.glint_apply_corr_km, pk[0], pk[1], pk[2], x, idx, cnt, y, N, K, ks, part, st) for pk in pins]
+    settle(torch, folds, 0.05)
+    ms_fold = timed(torch, folds, steps, 10)
+    ms_sel = timed(torch, [sel], steps, 10)
+    sel()
+    ms_corr = timed(torch, corrs, steps, 10)
+
+    def step_of(i):
+        def run():
+            folds[i]()
+            sel()
+            corrs[i]()
+        return run
+    ms_step = timed(torch, [step_of(i) for i in range(copies)], steps, 10)
     del pins
     return {"config": f"N {N} K {K}, fold ksg {ksg}, 10% of channels selected, correction ks {ks}",
             "fold_ms": ms_fold, "fold_gbs": fold_bytes / ms_fold / 1e6, "fold_frac": fold_bytes / ms_fold / 1e6 / HBM_PEAK_GBS,
-            "select_ms": ms_sel, "corr_ms": ms_corr, "selected": int(cnt.item())}
+            "select_ms": ms_sel, "corr_ms": ms_corr, "step_ms": ms_step, "selected": int(cnt.item()),
+            "resident_bytes_per_weight": 0.5 + 4 / 64, "full_gemv_resident_bytes_per_weight": 1 + 4 / 64}
 
 
 def bench_copy_ceiling(torch, mib: int = 1024):

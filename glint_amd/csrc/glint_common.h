@@ -143,6 +143,14 @@ __device__ __forceinline__ uint32_t glint_codes_odd(uint32_t H, uint32_t P) {
     return (H & 0xF0F0F0F0u) | ((P >> 4) & 0x0F0F0F0Fu);
 }
 
+/* A split-K workspace (tile_mfma.h): f32 partials plus one arrival counter per output
+ * tile, counters zero between launches. */
+struct GlintSplitWs {
+    float *part;
+    unsigned *ctr;
+    size_t part_floats, nctr; /* capacities */
+};
+
 /* ------------------------------------------------------------- device helpers */
 typedef uint32_t glint_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t glint_u32x2 __attribute__((ext_vector_type(2)));

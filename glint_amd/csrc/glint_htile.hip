@@ -666,6 +666,10 @@ GLINT_API int glint_htile_workspace_reserve(struct ihipStream_t *stream) {
     return glint_split_ws_stream((hipStream_t)stream, ws) ? 0 : -1;
 }
 
+/* Library-internal (not exported): the stream's split-K workspace, for the K-major
+ * kernels' slice reductions (one workspace cache per library). */
+bool glint_stream_workspace(hipStream_t st, GlintSplitWs *ws) { return glint_split_ws_stream(st, *ws); }
+
 /* Library-internal (not exported): the BF16-out launch with the caller's split-K
  * workspace in place of the stream's own. Used by the no-allocation entry point. */
 int glint_htile_bf16_launch_ws(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax, const void *d_x,

@@ -7,7 +7,9 @@
  *   the row-major planes, 4-byte stores of the K-major rows.
  * k_gemv_km_fold — a lane owns KM_FOLD_RPL = 8 output rows (4 B of a K-major hole row), so
  *   a wave reads 256 B contiguous per channel; the 8 waves of a workgroup take 8 parts of the
- *   workgroup's channel slice (grid.y) and meet in LDS. Per element: one v_perm for the
+ *   workgroup's channel slice (grid.y) and meet in LDS; the slices of a row block meet in
+ *   the last of its workgroups to finish (arrival counters), in slice order. Per element:
+ *   one v_perm for the
  *   address, one lookup in the 64-copy PARENT table, one FMA by the wave-uniform x[c];
  *   the block scale is applied once per run of channels inside a 64-block.
  * k_select_topk — one workgroup: keys in LDS, rank thresholds by a two-level radix select
@@ -90,7 +92,10 @@ __global__ __launch_bounds__(KM_T) void k_kmajor_scales(const float *__restrict_
 /* ------------------------------------------------------------------ fold GEMV */
 #define KM_SUB 8                /* waves per workgroup = parts of a channel slice */
 #define KM_WG (64 * KM_SUB)
-#define KM_U 4                  /* channels per batch (two batches in flight per wave) */
+#ifndef KM_U
+#define KM_U 4 /* channels per batch (two batches in flight per wave); a multiple of 4 dividing 64 */
+#endif
+static_assert(KM_U % 4 == 0 && 64 % KM_U == 0, "fold batch");
 #ifndef KM_FOLD_RPL
 #define KM_FOLD_RPL 8 /* fold: output rows per lane (8, 16 or 32) */
 #endif
@@ -136,11 +141,18 @@ __device__ __forceinline__ void km_lookup_fma(const float *lds, const uint32_t (
         acc[j] = fmaf(tv[j], xv, acc[j]);
 }
 
-/* The workgroup's KM_SUB part sums (one per wave) meet in LDS and are added in order;
- * the sum of rows r0 + rr goes to dst[rr] (plus dst[rr] first when ADD). */
+/* The workgroup's KM_SUB part sums meet in LDS and are added in order (row sum v of row
+ * r0 + rr). One slice (nsl == 1): y[r] = v, plus y[r] first when ADD. Several slices, no
+ * ctr: v goes to part[sl N + r] and k_km_combine adds the slices. Several with ctr: the
+ * slices meet in the last workgroup of the row block to arrive. Each stores v to
+ * part[sl N + r] with device-coherent stores, all complete before the barrier ahead of its
+ * counter increment; the last one adds the slices' rows in slice order (its own from LDS),
+ * as k_km_combine does, adds y when ADD, stores y and sets ctr[bx] back to zero. */
 template <bool ADD, int RPL>
-__device__ __forceinline__ void km_combine_parts(float *lds, const float (&tot)[RPL], int r0, int N, float *dst) {
+__device__ __forceinline__ void km_finish(float *lds, const float (&tot)[RPL], int r0, int N, float *__restrict__ y,
+                                          float *__restrict__ part, unsigned *ctr, int nsl, int sl) {
     constexpr int ROWS = 64 * RPL;
+    __shared__ unsigned s_last;
     const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
     __syncthreads(); /* the lookup table is dead: the part sums go over it */
 #pragma unroll
@@ -155,8 +167,50 @@ __device__ __forceinline__ void km_combine_parts(float *lds, const float (&tot)[
 #pragma unroll
         for (int k = 1; k < KM_SUB; ++k)
             v = v + lds[k * ROWS + rr];
-        dst[rr] = ADD ? dst[rr] + v : v;
+        if (nsl == 1)
+            y[r0 + rr] = ADD ? y[r0 + rr] + v : v;
+        else if (!ctr)
+            part[(int64_t)sl * N + r0 + rr] = v;
+        else {
+            lds[rr] = v; /* only this thread reads lds[rr] again */
+            __hip_atomic_store(part + (int64_t)sl * N + r0 + rr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
+    if (nsl == 1 || !ctr)
+        return;
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(&ctr[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)nsl - 1u;
+    __syncthreads();
+    if (!s_last)
+        return;
+    for (int rr = threadIdx.x; rr < ROWS; rr += KM_WG) {
+        if (r0 + rr >= N)
+            break;
+        const float own = lds[rr];
+        const float *col = part + r0 + rr;
+        float acc = 0.f;
+        for (int s0 = 0; s0 < nsl; s0 += 8) { /* 8 slices' loads in flight, added in order */
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                v[i] = __hip_atomic_load(col + (int64_t)min(s0 + i, nsl - 1) * N, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int s = s0 + i;
+                if (s < nsl) {
+                    const float t = s == sl ? own : v[i];
+                    acc = s == 0 ? t : acc + t;
+                }
+            }
+        }
+        y[r0 + rr] = ADD ? y[r0 + rr] + acc : acc;
+    }
+    if (threadIdx.x == 0)
+        __hip_atomic_store(&ctr[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* Workgroup (row block bx, channel slice by): wave q walks part q of the slice as runs of
@@ -165,8 +219,8 @@ __device__ __forceinline__ void km_combine_parts(float *lds, const float (&tot)[
 template <int RPL>
 __global__ __launch_bounds__(KM_WG) void k_gemv_km_fold(const uint8_t *__restrict__ hole_bytes,
                                                         const float *__restrict__ scales_k,
-                                                        const uint16_t *__restrict__ x, float *__restrict__ out, int N,
-                                                        int ksl) {
+                                                        const uint16_t *__restrict__ x, float *__restrict__ y,
+                                                        float *__restrict__ part, unsigned *ctr, int N, int ksl) {
     constexpr int ROWS = 64 * RPL, NW = RPL / 8; /* rows per workgroup, code words per lane */
     using HV = typename std::conditional<RPL == 32, glint_u32x4,
                                          typename std::conditional<RPL == 16, glint_u32x2, uint32_t>::type>::type;
@@ -206,10 +260,15 @@ __global__ __launch_bounds__(KM_WG) void k_gemv_km_fold(const uint8_t *__restric
             for (int j = 0; j < RPL; ++j)
                 acc[j] = 0.f;
         }
-        /* the batch's 4 x values in one wave-uniform 8-B load, waited for once before the
+        /* the batch's KM_U x values in wave-uniform 8-B loads, waited for once before the
          * lookups (a scalar load per channel would make every lookup wait for it) */
-        const glint_u32x2 xw = *(const glint_u32x2 *)(x + c);
-        const uint32_t xs[2] = {xw.x, xw.y};
+        uint32_t xs[KM_U / 2];
+#pragma unroll
+        for (int k = 0; k < KM_U / 4; ++k) {
+            const glint_u32x2 xw = *(const glint_u32x2 *)(x + c + 4 * k);
+            xs[2 * k] = xw.x;
+            xs[2 * k + 1] = xw.y;
+        }
 #pragma unroll
         for (int u = 0; u < KM_U; ++u) {
             const float xv = (u & 1) ? glint_bf16hi(xs[u >> 1]) : glint_bf16lo(xs[u >> 1]);
@@ -239,7 +298,7 @@ __global__ __launch_bounds__(KM_WG) void k_gemv_km_fold(const uint8_t *__restric
     }
     if (c < c1)
         batch(c, wa);
-    km_combine_parts<false, RPL>(lds, tot, r0, N, out + (int64_t)blockIdx.y * N + r0);
+    km_finish<false, RPL>(lds, tot, r0, N, y, part, ctr, gridDim.y, blockIdx.y);
 }
 
 /* y[r] = ((part[r] + part[N + r]) + ...) + part[(ks - 1) N + r], plus y[r] first when ADD. */
@@ -445,7 +504,7 @@ __global__ __launch_bounds__(KM_WG) void k_apply_corr_km(const uint8_t *__restri
                                                          const float *__restrict__ scales_k,
                                                          const uint16_t *__restrict__ x, const int32_t *__restrict__ idx,
                                                          const int32_t *__restrict__ cnt, float *__restrict__ y,
-                                                         float *__restrict__ part, int N, int ks) {
+                                                         float *__restrict__ part, unsigned *ctr, int N, int ks) {
     constexpr int ROWS = 64 * RPL, NW = RPL / 8; /* rows per workgroup, code words per lane */
     using HV = typename std::conditional<RPL == 32, glint_u32x4,
                                          typename std::conditional<RPL == 16, glint_u32x2, uint32_t>::type>::type;
@@ -505,14 +564,23 @@ __global__ __launch_bounds__(KM_WG) void k_apply_corr_km(const uint8_t *__restri
     }
     if (cur >= 0)
         flush();
-    if (ks > 1)
-        km_combine_parts<false, RPL>(lds, tot, r0, N, part + (int64_t)blockIdx.y * N + r0);
-    else
-        km_combine_parts<true, RPL>(lds, tot, r0, N, y + r0);
+    km_finish<true, RPL>(lds, tot, r0, N, y, part, ctr, ks, blockIdx.y);
 }
 
 /* -------------------------------------------------------------------- C ABI */
 static int km_launched() { return hipGetLastError() == hipSuccess ? 0 : -3; }
+
+bool glint_stream_workspace(hipStream_t st, GlintSplitWs *ws); /* glint_htile.hip */
+
+/* Arrival counters for `blocks` row blocks: the stream's split-K workspace counters (zero
+ * between launches), or null when the stream has none (a capture on a stream that never
+ * ran a split launch) or too few: the slices then meet in k_km_combine. */
+static unsigned *km_counters(hipStream_t st, unsigned blocks) {
+    GlintSplitWs ws;
+    if (!glint_stream_workspace(st, &ws) || ws.nctr < blocks)
+        return nullptr;
+    return ws.ctr;
+}
 
 GLINT_API int glint_kmajor_pack(const uint8_t *hole, const uint8_t *plug, const float *absmax, int N, int K,
                                 uint8_t *hole_k, uint8_t *plug_k, float *scales_k, hipStream_t stream) {
@@ -537,8 +605,9 @@ GLINT_API int glint_gemv_km_fold(const uint8_t *hole_k, const float *scales_k, c
         !glint_aligned(scales_k, 16) || !glint_aligned(x, 16))
         return -2;
     const dim3 grid((N + 64 * KM_FOLD_RPL - 1) / (64 * KM_FOLD_RPL), ksg);
-    k_gemv_km_fold<KM_FOLD_RPL><<<grid, KM_WG, 0, stream>>>(hole_k, scales_k, x, ksg > 1 ? part : y, N, K / ksg);
-    if (ksg > 1)
+    unsigned *ctr = ksg > 1 ? km_counters(stream, grid.x) : nullptr;
+    k_gemv_km_fold<KM_FOLD_RPL><<<grid, KM_WG, 0, stream>>>(hole_k, scales_k, x, y, part, ctr, N, K / ksg);
+    if (ksg > 1 && !ctr)
         k_km_combine<false><<<(N + KM_T - 1) / KM_T, KM_T, 0, stream>>>(part, y, N, ksg);
     return km_launched();
 }
@@ -566,8 +635,10 @@ GLINT_API int glint_apply_corr_km(const uint8_t *hole_k, const uint8_t *plug_k, 
         !glint_aligned(plug_k, 16) || !glint_aligned(scales_k, 16))
         return -2;
     const dim3 grid((N + 64 * KM_CORR_RPL - 1) / (64 * KM_CORR_RPL), ks);
-    k_apply_corr_km<KM_CORR_RPL><<<grid, KM_WG, 0, stream>>>(hole_k, plug_k, scales_k, x, idx, cnt, y, part, N, ks);
-    if (ks > 1)
+    unsigned *ctr = ks > 1 ? km_counters(stream, grid.x) : nullptr;
+    k_apply_corr_km<KM_CORR_RPL><<<grid, KM_WG, 0, stream>>>(hole_k, plug_k, scales_k, x, idx, cnt, y, part, ctr, N,
+                                                             ks);
+    if (ks > 1 && !ctr)
         k_km_combine<true><<<(N + KM_T - 1) / KM_T, KM_T, 0, stream>>>(part, y, N, ks);
     return km_launched();
 }

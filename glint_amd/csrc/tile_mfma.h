@@ -824,11 +824,6 @@ __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restric
  * <= 2 x CUs) and the largest split tile is 256 x 128 (32768 floats), so CUs x 32768
  * floats and 2 x CUs counters always suffice; tile_split_plan checks the plan against the
  * capacity and runs unsplit where it would not fit. */
-struct GlintSplitWs {
-    float *part;
-    unsigned *ctr;
-    size_t part_floats, nctr; /* capacities */
-};
 #define GLINT_SPLIT_TILE_FLOATS_MAX 32768
 static inline size_t glint_split_ctr_bytes(size_t nctr) { return (nctr * sizeof(unsigned) + 255) & ~(size_t)255; }
 
