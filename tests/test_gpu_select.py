@@ -2,6 +2,9 @@
 fold GEMV, channel selection and plug correction, each bit for bit against the oracle
 (the kernels keep the oracle's summation orders), plus the chained decode step and the
 argument codes."""
+import ctypes
+import os
+
 import numpy as np
 import pytest
 
@@ -125,6 +128,41 @@ def test_decode_step_matches_oracle(oracle, N, K, frac, ks):
         ref, absum = oracle.htile_f64(h, p, am, x, 1, N, K, 64)
         assert np.all(np.abs(got.astype(np.float64) - ref[0]) <= (K + 4) * 2.0 ** -23 * absum[0] * 2)
     del torch
+
+
+def test_correction_reads_plug_rows_from_pinned_host_memory(oracle):
+    """The reference keeps the K-major plug plane in pinned host memory and reads only the
+    selected channels' rows (mojo/p7_glint_select_decode.mojo:1-4). The same call with
+    plug_k in pinned host memory (read over the bus, zero copy) gives the bytes of the
+    device-resident plug, and the oracle's, at the decode shape."""
+    torch = torch_cuda()
+    N, K, ks = 14336, 4096, 8
+    print(f"host plug correction N={N} K={K} ks={ks}", flush=True)
+    h, p, am = _pin(oracle, N, K, 99)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    x = _x(K, 1234)
+    dhk, dsk, dx = dev(hk), dev(sk), dev(x)
+    # mapped pinned host memory and its device address (hipHostMalloc + hipHostGetDevicePointer)
+    hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+    hbuf, dptr = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipHostMalloc(ctypes.byref(hbuf), ctypes.c_size_t(pk.nbytes), ctypes.c_uint(0x2)) == 0  # Mapped
+    try:
+        assert hip.hipHostGetDevicePointer(ctypes.byref(dptr), hbuf, ctypes.c_uint(0)) == 0 and dptr.value
+        ctypes.memmove(hbuf, pk.ctypes.data, pk.nbytes)
+        y0 = H.gemv_km_fold(dhk, dsk, dx, N, K, 16)
+        idx, cnt = H.select_topk(dx, K // 10)
+        y_dev = H.apply_corr_km(dhk, dev(pk), dsk, dx, idx, cnt, y0.clone(), N, K, ks)
+        y_host = y0.clone()
+        lib = H.encode_lib()
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        assert lib.glint_apply_corr_km(P(dhk), dptr, P(dsk), P(dx), P(idx), P(cnt), P(y_host), N, K, ks,
+                                       P(torch.empty(ks * N, dtype=torch.float32, device="cuda")), None) == 0
+    finally:
+        torch.cuda.synchronize()  # nothing may still read the buffer when it is freed
+        hip.hipHostFree(hbuf)
+    assert host(y_host).tobytes() == host(y_dev).tobytes()
+    want = oracle.apply_corr_km(hk, pk, sk, x, oracle.select_topk(x, K, K // 10), N, K, host(y0), ks)
+    assert host(y_host).tobytes() == want.tobytes()
 
 
 def test_argument_codes():
