@@ -144,9 +144,9 @@ SPLIT_SHAPES = [(64, 64, 2368), (40, 200, 1088), (64, 14336, 4096), (64, 4096, 1
 @pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
 def test_bf16_split_k(oracle, M, N, K):
     """Shapes whose output tiles alone would leave most of the device idle split K over
-    several workgroups per tile (K = 64 * 37 gives a ragged last split; M <= 64 with
-    K % 256 == 0 runs the streamed-weight tile, with an odd count of 256-wide super-steps
-    at K = 2304 and 768 and ragged M and N); the last workgroup
+    several workgroups per tile (K = 64 * 37 gives a ragged last split; K = 2304 and 768
+    give odd counts of 4-step super-steps with ragged M and N; M = 2 the smallest tile
+    M); the last workgroup
     of a tile adds the partial tiles in split order. Checked: relative Frobenius error
     against fp32 on the expanded weights (a lost or doubled partial fails it), every row
     bounded, bitwise-equal repeats, and bitwise-equal results from two streams running at
