@@ -165,6 +165,56 @@ def test_correction_reads_plug_rows_from_pinned_host_memory(oracle):
     assert host(y_host).tobytes() == want.tobytes()
 
 
+def test_decode_step_under_graph_capture(oracle):
+    """Fold, select and correction captured into one graph, on a stream that has a split
+    workspace (the slices meet in-kernel through its counters) and on one that has none
+    (the capture cannot allocate: the slices meet in the combine kernel). Every replay,
+    with eager decode steps and synchronisations between them, equals the eager result
+    bit for bit."""
+    torch = torch_cuda()
+    N, K, ksg, ks = 4096, 4096, 16, 8
+    print(f"graph capture decode step N={N} K={K}", flush=True)
+    h, p, am = _pin(oracle, N, K, 4501)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    x, x2 = _x(K, 4502), _x(K, 4503)
+    dhk, dpk, dsk, dx, dx2 = dev(hk), dev(pk), dev(sk), dev(x), dev(x2)
+    part = torch.empty(32 * N, dtype=torch.float32, device="cuda")
+
+    def step(xx, y, idx, cnt, stream):
+        H.gemv_km_fold(dhk, dsk, xx, N, K, ksg, y=y, part=part, stream=stream)
+        H.select_topk(xx, K // 10, idx=idx, cnt=cnt, stream=stream)
+        H.apply_corr_km(dhk, dpk, dsk, xx, idx, cnt, y, N, K, ks, part=part, stream=stream)
+
+    for warm in (True, False):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        y = torch.empty(N, dtype=torch.float32, device="cuda")
+        idx = torch.empty(K, dtype=torch.int32, device="cuda")
+        cnt = torch.empty(1, dtype=torch.int32, device="cuda")
+        ye = torch.empty_like(y)
+        if warm:
+            assert H.encode_lib().glint_htile_workspace_reserve(ctypes.c_void_p(s.cuda_stream)) == 0
+        s.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            step(dx, y, idx, cnt, s)
+        torch.cuda.synchronize()
+        want = oracle.apply_corr_km(hk, pk, sk, x, oracle.select_topk(x, K, K // 10), N, K,
+                                    oracle.gemv_km_fold(hk, sk, x, N, K, ksg), ks)
+        want2 = oracle.apply_corr_km(hk, pk, sk, x2, oracle.select_topk(x2, K, K // 10), N, K,
+                                     oracle.gemv_km_fold(hk, sk, x2, N, K, ksg), ks)
+        for rep in range(3):
+            y.zero_()
+            graph.replay()
+            with torch.cuda.stream(s):
+                e_idx, e_cnt = torch.empty_like(idx), torch.empty_like(cnt)
+                step(dx2, ye, e_idx, e_cnt, s)
+            torch.cuda.synchronize()
+            assert host(y).tobytes() == want.tobytes(), (warm, rep)
+            assert host(ye).tobytes() == want2.tobytes(), (warm, rep)
+        del graph
+
+
 def test_argument_codes():
     torch = torch_cuda()
     lib = H.encode_lib()
