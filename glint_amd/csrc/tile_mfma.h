@@ -75,6 +75,26 @@ struct TileOutF32 {
 /* GLINT planes, bs = 64: weight = CELLS[h][p] * absmax, through the 32-copy LDS cell
  * table (lane l reads copy l % 32). A 64-copy table, whose lookup address is one
  * v_perm_b32, measured 3% slower here: its fill doubles and the LDS budget tightens. */
+/* Weight loads of the tile producers. A tile GEMM reads every weight once per block of x
+ * rows, so the loads keep the default cache policy and the blocks after the first find the
+ * weights in L2. With the nontemporal hint (right for the M = 1 GEMV, which reads each weight
+ * once) every block fetched them again from beyond L2: on the 14336 x 4096 gate shape M = 512
+ * went 91.9 -> 82.5 us, M = 2048 325.5 -> 264.4 us with plain loads; M <= 128 moved by 1-3%.
+ * TILE_W_NT_STEP / TILE_W_NT_SS = 1 restore the hint for the per-step (k_tile_mfma,
+ * k_tile_big) and the super-step (k_tile_ss) loads. */
+#ifndef TILE_W_NT_STEP
+#define TILE_W_NT_STEP 0
+#endif
+#ifndef TILE_W_NT_SS
+#define TILE_W_NT_SS 0
+#endif
+template <int NT, class V> __device__ __forceinline__ V tile_wload(const V *p) {
+    if constexpr (NT != 0)
+        return __builtin_nontemporal_load(p);
+    else
+        return *p;
+}
+
 struct GlintTileProducer {
     const glint_u32x2 *hole, *plug; /* 8 B = 16 elements of each plane */
     const float *absmax;
@@ -92,8 +112,8 @@ struct GlintTileProducer {
     }
     __device__ __forceinline__ void load(Regs &r, int row, int quarter, int kb) const {
         const int64_t q = (int64_t)row * (K >> 4) + kb * 4 + quarter;
-        r.h = __builtin_nontemporal_load(&hole[q]);
-        r.p = __builtin_nontemporal_load(&plug[q]);
+        r.h = tile_wload<TILE_W_NT_STEP>(&hole[q]);
+        r.p = tile_wload<TILE_W_NT_STEP>(&plug[q]);
         r.a = absmax[(int64_t)row * (K >> 6) + kb];
     }
     /* load() with the row given as base = row * K / 16 (8-B units), for N * K < 2^36: one
@@ -102,8 +122,8 @@ struct GlintTileProducer {
     __device__ __forceinline__ uint32_t row_base(int row) const { return (uint32_t)row * (uint32_t)(K >> 4); }
     __device__ __forceinline__ void load_at(Regs &r, uint32_t base, int quarter, int kb) const {
         const uint32_t q = base + (uint32_t)(kb * 4 + quarter);
-        r.h = __builtin_nontemporal_load(&hole[q]);
-        r.p = __builtin_nontemporal_load(&plug[q]);
+        r.h = tile_wload<TILE_W_NT_STEP>(&hole[q]);
+        r.p = tile_wload<TILE_W_NT_STEP>(&plug[q]);
         r.a = absmax[(base >> 2) + (uint32_t)kb];
     }
     /* v[8 q + 2 b] / v[8 q + 2 b + 1]: cells of the even / odd element of byte b of word q */
@@ -167,8 +187,8 @@ struct GlintTileProducer {
     __device__ __forceinline__ void sload(SRegs &r, int row, int step0, int c, int last) const {
         const int kb = min(step0 + (c >> 1), last);
         const int64_t i = (int64_t)row * (K >> 5) + kb * 2 + (c & 1);
-        r.h = __builtin_nontemporal_load((const glint_u32x4 *)hole + i);
-        r.p = __builtin_nontemporal_load((const glint_u32x4 *)plug + i);
+        r.h = tile_wload<TILE_W_NT_SS>((const glint_u32x4 *)hole + i);
+        r.p = tile_wload<TILE_W_NT_SS>((const glint_u32x4 *)plug + i);
         r.a = absmax[(int64_t)row * (K >> 6) + kb];
     }
     __device__ __forceinline__ void slookup(const SRegs &r, int h, float (&v)[16], int lane) const {
@@ -198,14 +218,14 @@ struct Int8PinTileProducer {
     };
     __device__ __forceinline__ void setup(float *, float *) {}
     __device__ __forceinline__ void load(Regs &r, int row, int quarter, int kb) const {
-        r.w = __builtin_nontemporal_load(&q[(int64_t)row * (K >> 4) + kb * 4 + quarter]);
+        r.w = tile_wload<TILE_W_NT_STEP>(&q[(int64_t)row * (K >> 4) + kb * 4 + quarter]);
         r.s = scale[(int64_t)row * (K >> 6) + kb];
     }
     /* load() with the row given as base = row * K / 16 (16-B units), for N * K < 2^36 */
     static constexpr int REG_WORDS = 5; /* w, s: the leading words of Regs */
     __device__ __forceinline__ uint32_t row_base(int row) const { return (uint32_t)row * (uint32_t)(K >> 4); }
     __device__ __forceinline__ void load_at(Regs &r, uint32_t base, int quarter, int kb) const {
-        r.w = __builtin_nontemporal_load(&q[base + (uint32_t)(kb * 4 + quarter)]);
+        r.w = tile_wload<TILE_W_NT_STEP>(&q[base + (uint32_t)(kb * 4 + quarter)]);
         r.s = scale[(base >> 2) + (uint32_t)kb];
     }
     __device__ __forceinline__ void lookup(const Regs &r, float (&v)[16], int) const {
@@ -233,7 +253,7 @@ struct Int8PinTileProducer {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int kb = min(step0 + sstep(c, h), last);
-            r.w[h] = __builtin_nontemporal_load(&q[(int64_t)row * (K >> 4) + kb * 4 + (c & 3)]);
+            r.w[h] = tile_wload<TILE_W_NT_SS>(&q[(int64_t)row * (K >> 4) + kb * 4 + (c & 3)]);
             r.s[h] = scale[(int64_t)row * (K >> 6) + kb];
         }
     }
