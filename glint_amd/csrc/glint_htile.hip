@@ -596,6 +596,9 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             planned = tile_ss_launch<128, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 1, fixed);
         else if (TILE_BIG && tile_big_fits(M, N, K) && tile_big_pays(M, N))
             planned = tile_big_launch<TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, fixed);
+        else if (TILE_BIG && tile_big_fits(M, N, K) && tile_big_split_fills(M, N, K) &&
+                 tile_big_split_launch<TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, fixed))
+            planned = true;
         else
             planned = tile_mfma_launch<MF2_BM, MF2_BN, 4, 2, TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N,
                                                                                                        K, st, fixed);

@@ -840,11 +840,11 @@ __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restric
 /* A split-K workspace: f32 partial tiles plus one arrival counter per output tile. The
  * counters are zero between launches: the last workgroup of each tile clears its own, so
  * a workspace stays valid as long as every launch that used it ran to completion.
- * Capacity: a split plan has at most one partial tile per workgroup slot (tiles x splits
- * <= 2 x CUs) and the largest split tile is 256 x 128 (32768 floats), so CUs x 32768
- * floats and 2 x CUs counters always suffice; tile_split_plan checks the plan against the
- * capacity and runs unsplit where it would not fit. */
-#define GLINT_SPLIT_TILE_FLOATS_MAX 32768
+ * Capacity: the 256 x 256 tiles (65536 floats) split only to fill each CU once (tiles x
+ * splits <= CUs), the 256 x 128 ones likewise, the smaller ones at most 2 x CUs x 8192
+ * floats, so CUs x 65536 floats and 2 x CUs counters always suffice; tile_split_plan checks
+ * the plan against the capacity and runs unsplit where it would not fit. */
+#define GLINT_SPLIT_TILE_FLOATS_MAX 65536
 static inline size_t glint_split_ctr_bytes(size_t nctr) { return (nctr * sizeof(unsigned) + 255) & ~(size_t)255; }
 
 /* Zero n counters on a stream (a kernel, not a memset node, so it is also safe to record
@@ -979,9 +979,32 @@ static bool tile_big_launch(const P &p, const uint16_t *x, typename Out::T *y, i
     const unsigned gx = (unsigned)((N + 255) / 256), gy = (unsigned)((M + 255) / 256);
     int kps, ks;
     GlintSplitWs ws;
-    /* 256 x 256 partials exceed the workspace's per-slot tile; tile_big_pays only picks this
-     * kernel with about a tile per CU, where the plan does not split anyway */
     if (!tile_split_plan(st, gx, gy, K >> 6, (size_t)256 * 256, kps, ks, ws, 1, fixed))
+        return false;
+    k_tile_big<R, P, Out><<<dim3(gx, gy, (unsigned)ks), 512, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
+    return true;
+}
+
+/* Where the 256 x 256 tiles are too few to pay on their own but split K makes them fill
+ * every CU exactly once (4096 x 14336 at M = 1024: 64 tiles x 4 splits; M = 2048: 128 x 2),
+ * k_tile_big with split K beats k_tile_mfma's 256 x 128 tiles by 7-8%; where the split
+ * leaves CUs idle it loses (M = 512 on either shape). */
+static inline bool tile_big_split_fills(int M, int N, int K) {
+    const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    const int kps = glint_split_kps(tiles, glint_cu_count(), K >> 6, TILE_SPLIT_MIN_STEPS);
+    const int64_t ks = ((K >> 6) + kps - 1) / kps;
+    return ks > 1 && tiles * ks == glint_cu_count();
+}
+/* k_tile_big split as tile_big_split_fills plans it; launches nothing and returns false if
+ * the plan does not come out split (no workspace, or `fixed` too small), so the caller can
+ * take the 256 x 128 tiles instead. */
+template <int R, class P, class Out>
+static bool tile_big_split_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K,
+                                  hipStream_t st, const GlintSplitWs *fixed = nullptr) {
+    const unsigned gx = (unsigned)((N + 255) / 256), gy = (unsigned)((M + 255) / 256);
+    int kps, ks;
+    GlintSplitWs ws;
+    if (!tile_split_plan(st, gx, gy, K >> 6, (size_t)256 * 256, kps, ks, ws, 1, fixed) || ks <= 1)
         return false;
     k_tile_big<R, P, Out><<<dim3(gx, gy, (unsigned)ks), 512, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
     return true;

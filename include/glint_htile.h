@@ -34,7 +34,7 @@ int launch_glint_htile_s3_f32(const uint8_t *d_hole, const uint8_t *d_plug, cons
  * 1e-2 relative Frobenius error of an f32 GEMM on the expanded weights; results are
  * deterministic (split K adds its partial tiles in a fixed order).
  * Split-K workspace (M > 1 on the MFMA routes, both outputs): one per (device, stream),
- * allocated at full size (CUs x 128 KiB of partials plus counters, 32 MiB on MI355X) by
+ * allocated at full size (CUs x 256 KiB of partials plus counters, 64 MiB on MI355X) by
  * the first call that splits, its counters zeroed by a kernel on the stream, never grown
  * or freed. hipStreamPerThread gets one per host thread. A launch captured into a graph
  * keeps the workspace it bound for the graph; the next eager call on that stream gets a
@@ -52,7 +52,7 @@ int glint_htile_workspace_reserve(struct ihipStream_t *stream);
 /* No reference counterpart. For callers that cannot allocate (code under graph capture,
  * tight serving loops, harnesses that forbid hipMalloc): launch_glint_htile_bf16_stream
  * with the split-K partials and counters in a static per-GPU scratch array of the library
- * (32 MiB plus 4 KiB, held until the process ends) instead of a per-stream workspace. Same
+ * (64 MiB plus 4 KiB, held until the process ends) instead of a per-stream workspace. Same
  * kernels, split plan and results; allocates nothing. Calls that overlap on one GPU share
  * the array and race. Returns the codes above, or -5 when the split plan would need more
  * than the array holds (possible only on a part with more than 256 CUs). */

@@ -32,7 +32,7 @@ typedef struct {
  * Before checking its arguments it returns, and clears, an error already pending on the
  * calling thread (hipGetLastError), without launching.
  * At m > 4 the first call on a stream at a given size may allocate the stream's split-K
- * workspace (hipMalloc, at most 32 MiB, kept until exit); during graph capture it is not
+ * workspace (hipMalloc, at most 64 MiB, kept until exit); during graph capture it is not
  * grown and the GEMM runs unsplit. Results are deterministic.
  * Reference: include/int8_tile_gemm.h:20-27 (cuda/int8_tile_gemm.cu:169-180). */
 int int8_tile_gemm_bf16(const void *x_bf16, Int8PinLinear w, float *y, int m, struct ihipStream_t *stream);

@@ -138,7 +138,8 @@ def test_bf16_prefill_tiles_rel_frobenius(oracle, M, N, K):
 
 
 SPLIT_SHAPES = [(64, 64, 2368), (40, 200, 1088), (64, 14336, 4096), (64, 4096, 14336), (200, 512, 8192),
-                (512, 4096, 14336), (17, 1000, 2304), (33, 136, 768), (2, 14336, 4096)]
+                (512, 4096, 14336), (17, 1000, 2304), (33, 136, 768), (2, 14336, 4096),
+                (1024, 4096, 14336), (1000, 4000, 14336)]
 
 
 @pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
@@ -146,8 +147,8 @@ def test_bf16_split_k(oracle, M, N, K):
     """Shapes whose output tiles alone would leave most of the device idle split K over
     several workgroups per tile (K = 64 * 37 gives a ragged last split; K = 2304 and 768
     give odd counts of 4-step super-steps with ragged M and N; M = 2 the smallest tile
-    M); the last workgroup
-    of a tile adds the partial tiles in split order. Checked: relative Frobenius error
+    M; M = 1024 and 1000 the 256 x 256 tiles split 4 ways, the latter with ragged tiles);
+    the last workgroup of a tile adds the partial tiles in split order. Checked: relative Frobenius error
     against fp32 on the expanded weights (a lost or doubled partial fails it), every row
     bounded, bitwise-equal repeats, and bitwise-equal results from two streams running at
     once (each stream has its own partials and counters)."""

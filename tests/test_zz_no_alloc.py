@@ -30,7 +30,7 @@ def test_noalloc_matches_allocating_entry():
     lib = H.encode_lib()
     ref_fn, na_fn = lib.launch_glint_htile_bf16_stream, lib.launch_glint_htile_bf16_stream_noalloc
     g = torch.Generator(device="cuda").manual_seed(7)
-    for M, N, K in [(512, 4096, 14336), (64, 4096, 4096), (2048, 384, 640), (1, 1024, 4096)]:
+    for M, N, K in [(1024, 4096, 14336), (512, 4096, 14336), (64, 4096, 4096), (2048, 384, 640), (1, 1024, 4096)]:
         print(f"noalloc M={M} N={N} K={K}", flush=True)
         pin = _pin(torch, N, K, 11 + N + K)
         x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
