@@ -281,7 +281,8 @@ def bench_host_abi(H, reps: int = 5):
 
 
 def bench_prefill(torch, H, steps: int, copies: int = 6):
-    """Prefill GEMMs at M = 64, 512, 2048 for the gate and down shapes. Each shape rotates
+    """Prefill GEMMs at M = 64, 512, 2048 for the gate and down shapes, and batched decode at
+    M = 2, 4, 8 (the small-M GEMV) on the same shapes. Each shape rotates
     `copies` pins (about 370 MB per shape) so the weights are not served from the
     256 MB last-level cache between calls."""
     out = {}
@@ -294,6 +295,18 @@ def bench_prefill(torch, H, steps: int, copies: int = 6):
         pins[name] = ([pin] + [tuple(t.clone() for t in pin) for _ in range(copies - 1)], N, K)
     gx = torch.Generator(device="cuda").manual_seed(3001)
     lib, st = H.encode_lib(), stream_handle(torch)
+    # batched decode: M = 2..8 rows run the small-M GEMV (each weight read once for all rows)
+    dec = {}
+    for M in (2, 4, 8):
+        for name, (cps, N, K) in pins.items():
+            x = torch.randn(M, K, device="cuda", generator=gx).to(torch.bfloat16)
+            y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+            calls = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, y, M, N, K, 64, st) for p in cps]
+            settle(torch, calls, 0.05)
+            ms = timed(torch, calls, steps * 3, copies)
+            byt = N * K * (1 + 4 / 64) + 2 * M * K + 2 * M * N
+            dec[f"M{M}_{name}"] = {"ms": ms, "eff_gbs": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS}
+    out["batched_decode"] = dec
     for M in (64, 512, 2048):
         for name, (cps, N, K) in pins.items():
             x = torch.randn(M, K, device="cuda", generator=gx).to(torch.bfloat16)
@@ -955,7 +968,9 @@ def main() -> int:
         if "prefill" in parts:
             extra["prefill"] = bench_prefill(torch, H, steps=12)
             log("prefill " + ", ".join(f"{k} {v['ms'] * 1e3:.1f} us (f32 out {v['f32_out']['ms'] * 1e3:.1f})"
-                                       for k, v in extra["prefill"].items()))
+                                       for k, v in extra["prefill"].items() if k != "batched_decode"))
+            log("batched decode " + ", ".join(f"{k} {v['ms'] * 1e3:.1f} us"
+                                              for k, v in extra["prefill"]["batched_decode"].items()))
         if "int8" in parts:
             extra["int8_gemm"] = bench_int8(torch, H, steps=10)
             log(f"int8 {extra['int8_gemm']['tops']:.0f} TOPS")

@@ -443,6 +443,154 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
     }
 }
 
+/* ------------------------------------------------- small-M decode GEMV (BF16 out) */
+/* k_htile_gemv_mr: M = 2 .. MR rows of x at once (batched decode), bs = 64, K % 2048 == 0,
+ * aligned. The layout and row walk of k_htile_gemv_xreg: wave (s, g) streams rows
+ * r0 + g, r0 + g + G, ... over K slice s, 32 elements per lane per row. Each weight is
+ * looked up once for all MR rows of x: the cells of a pair of elements are rounded to one
+ * BF16 pair, which v_dot2_f32_bf16 multiplies into the f32 partial of each row against the
+ * row's BF16 pair of x (x stays in registers as loaded, MR x 16 words per lane); the block
+ * absmax scales each partial once per row. So the weights are read once whatever M is,
+ * where the MFMA tiles cost the same at M = 2 as at M = 64. Numerics: the weights enter as
+ * BF16(cell) x absmax, the tiles' BF16(cell x absmax) up to one rounding of the scale;
+ * both within the BF16 API's 1e-2 relative Frobenius bound. Rows of x past M repeat row
+ * M - 1 and are not stored. */
+typedef __bf16 glint_bf16x2_t __attribute__((ext_vector_type(2)));
+template <int MR>
+__global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__restrict__ hole,
+                                                                  const void *__restrict__ plug,
+                                                                  const float *__restrict__ absmax,
+                                                                  const uint16_t *__restrict__ x,
+                                                                  uint16_t *__restrict__ y, int M, int N, int K,
+                                                                  int G, int rows_per_wg) {
+    __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS]; /* 64 KiB at LDS offset 0 */
+    extern __shared__ __attribute__((aligned(16))) float red[]; /* [rows_per_wg][S][4][MR] */
+    constexpr int EL = 32, Q = EL / 8;
+    const int lane = threadIdx.x & 63;
+    const uint32_t lane4 = (uint32_t)lane * 4u;
+    const int nch = K / EL, S = nch >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int s = w % S, g = w / S;
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int nrows = max(min(rows_per_wg, N - r0), 0);
+    const int my = g < nrows ? (nrows - g + G - 1) / G : 0;
+    auto row_of = [&](int i) -> int64_t { return (int64_t)min(r0 + g + min(i, max(my - 1, 0)) * G, N - 1); };
+    const uint32_t j = (uint32_t)(s * 64 + lane);
+
+    GlintCellFillS fill;
+    glint_cells_fill_sload(fill);
+    /* x: row m's 32 elements [32 j, 32 j + 32) as 16 words of BF16 pairs */
+    glint_u32x4 xv[MR][4];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const glint_u32x4 *xr = (const glint_u32x4 *)(x + (int64_t)min(m, M - 1) * K) + (size_t)j * 4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            xv[m][c] = xr[c];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    GemvRow<EL> buf[2];
+    gemv_x_load<EL>(hole, plug, absmax, row_of(0), nch, j, buf[0]);
+    gemv_x_load<EL>(hole, plug, absmax, row_of(1), nch, j, buf[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    glint_cells_fill_sstore(ltab, fill);
+    __syncthreads();
+
+    auto compute_row = [&](int i, const GemvRow<EL> &row) {
+        float part[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            part[m] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const uint32_t H = gemv_word<EL>(row.h, q), P = gemv_word<EL>(row.p, q);
+            const uint32_t E = glint_codes_even(H, P);
+            const uint32_t O = glint_codes_odd(H, P);
+            uint32_t wp[4];
+            wp[0] = glint_cvt_bf16x2(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)),
+                                     glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)));
+            wp[1] = glint_cvt_bf16x2(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)),
+                                     glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)));
+            wp[2] = glint_cvt_bf16x2(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)),
+                                     glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)));
+            wp[3] = glint_cvt_bf16x2(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)),
+                                     glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)));
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    /* the word as a value: this compiler bit-casts a vector element in place as
+                     * element 0 */
+                    const uint32_t xw = xv[m][q][b];
+                    part[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(glint_bf16x2_t, wp[b]),
+                                                              __builtin_bit_cast(glint_bf16x2_t, xw), part[m], false);
+                }
+        }
+        const int t = g + i * G;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float v = glint_row16_sum(row.a * part[m]);
+            if ((lane & 15) == 0)
+                red[((t * S + s) * 4 + (lane >> 4)) * MR + m] = v;
+        }
+    };
+    int i = 0;
+    for (; i + 4 <= my; i += 2) {
+        compute_row(i, buf[0]);
+        gemv_x_load<EL>(hole, plug, absmax, row_of(i + 2), nch, j, buf[0]);
+        compute_row(i + 1, buf[1]);
+        gemv_x_load<EL>(hole, plug, absmax, row_of(i + 3), nch, j, buf[1]);
+    }
+    for (int d = 0; d < 2; ++d)
+        if (i + d < my) {
+            compute_row(i + d, buf[d]);
+            if (i + d + 2 < my)
+                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + 2), nch, j, buf[d]);
+        }
+    for (int d = 0; d < 2; ++d)
+        if (i + 2 + d < my)
+            compute_row(i + 2 + d, buf[d]);
+    __syncthreads();
+
+    for (int e = threadIdx.x; e < nrows * MR; e += blockDim.x) {
+        const int t = e / MR, m = e % MR;
+        if (m >= M)
+            continue;
+        float sum = 0.0f;
+        for (int k = 0; k < S * 4; ++k)
+            sum += red[(t * S * 4 + k) * MR + m];
+        y[(int64_t)m * N + r0 + t] = glint_f32_to_bf16(sum);
+    }
+}
+
+#ifndef GEMV_MR_MAX
+#define GEMV_MR_MAX 8 /* largest M the small-M GEMV takes (templates for 2, 4 and 8 rows) */
+#endif
+/* k_htile_gemv_mr over 2 <= M <= GEMV_MR_MAX (bs 64, K % 2048 == 0, K / 2048 <= 8, aligned).
+ * Measured against the 64-row MFMA tile (k_tile_ss) on 14336 x 4096: M = 2 14.2-15.6 us
+ * against 35.0, M = 4 17.8-18.2 against 35.3, M = 5..8 24.7-24.9 against 34.3-34.6 (the
+ * 8-row template holds 128 VGPRs of x and runs at 2 waves per SIMD). */
+static int htile_launch_gemv_mr(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y,
+                                int M, int N, int K, hipStream_t st) {
+    const int S = K / 2048, G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
+    auto kern = M <= 2 ? k_htile_gemv_mr<2> : (M <= 4 ? k_htile_gemv_mr<4> : k_htile_gemv_mr<8>);
+    const int MR = M <= 2 ? 2 : (M <= 4 ? 4 : 8);
+    const int64_t resident =
+        std::max<int64_t>(glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4) / (G == 1 ? GEMV_G1_DIV : 1), 1);
+    const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
+    int64_t rows_per_wg = G * per_wave;
+    const int64_t cap = (GEMV_X_RED_MAX / (S * 4 * MR)) / G * G;
+    if (rows_per_wg > cap)
+        rows_per_wg = cap;
+    const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
+    const size_t lds = (size_t)rows_per_wg * S * 4 * MR * sizeof(float);
+    if (glint_set_lds_limit((const void *)kern, GEMV_X_RED_MAX * 4) != 0)
+        return -3;
+    kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K, G,
+                                     (int)rows_per_wg);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 /* ------------------------------------------------------------ generic f32 tiles */
 #define GT_N 64
 #define GT_M 32
@@ -585,6 +733,8 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
                          K <= GEMV_MAX_K;
     const bool mfma_ok = M > 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
                          glint_aligned(absmax, 4) && glint_aligned(x, 16);
+    if (OUT_BF16 && mfma_ok && M <= GEMV_MR_MAX && (K % 2048) == 0 && K / 2048 <= GEMV_X_THREADS / 64)
+        return htile_launch_gemv_mr(hole, plug, absmax, x, y, M, N, K, st);
     if (mfma_ok && OUT_BF16) {
         const GlintTileProducer p{(const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, N, K, nullptr};
         const uint16_t *xb = (const uint16_t *)x;

@@ -29,8 +29,9 @@ int launch_glint_htile_s3_f32(const uint8_t *d_hole, const uint8_t *d_plug, cons
                               const void *d_x_bf16, float *d_y, int M, int N, int K, int blocksize);
 
 /* ---- Additive (no reference counterpart). ----
- * BF16 output with f32 accumulation: the decode GEMV (small M, HBM-bound) and the
- * prefill GEMM (larger M: BF16 MFMA on LDS-dequantized weight tiles). Contract: within
+ * BF16 output with f32 accumulation: the decode GEMV (M = 1, and M = 2 .. 8 with each
+ * weight read once for all rows, as BF16(cell) x absmax) and the prefill GEMM (larger M:
+ * BF16 MFMA on LDS-dequantized weight tiles). Contract: within
  * 1e-2 relative Frobenius error of an f32 GEMM on the expanded weights; results are
  * deterministic (split K adds its partial tiles in a fixed order).
  * Split-K workspace (M > 1 on the MFMA routes, both outputs): one per (device, stream),

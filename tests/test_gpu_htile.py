@@ -115,6 +115,35 @@ def test_bf16_path_rel_frobenius(oracle, M):
     assert rel <= 4e-3  # BF16 rounding of the output alone is ~2^-9
 
 
+@pytest.mark.parametrize("M,N,K", [(2, 14336, 4096), (3, 4096, 14336), (4, 129, 2048), (5, 1000, 12288),
+                                   (8, 17, 16384), (6, 4097, 8192), (7, 7, 6144), (8, 3000, 6144)])
+def test_small_m_gemv_vs_float64(oracle, M, N, K):
+    """2 <= M <= 8 (batched decode) on the small-M GEMV: every weight looked up once for all
+    M rows, its cell rounded to BF16 and multiplied into each row by v_dot2_f32_bf16, the
+    block absmax applied once per row. Bound per output against float64 on the expanded
+    weights: the BF16 output rounding (2^-8 |ref|), the BF16 rounding of each cell
+    (2^-9 sum |w x|) and the f32 accumulation ((K + 2) 2^-23 sum |w x|). Also rel-Frobenius
+    <= 4e-3 and no write past row M - 1."""
+    torch = torch_cuda()
+    print(f"small-M gemv M={M} N={N} K={K}", flush=True)
+    hole, plug, am = _encoded_weight(oracle, N, K, 4002 + K)
+    g = torch.Generator(device="cuda").manual_seed(4001 + M)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.full((M + 1, N), 1234.0, dtype=torch.bfloat16, device="cuda")
+    rc = H.encode_lib().launch_glint_htile_bf16_stream(H._p(hole), H._p(plug), H._p(am), H._p(x), H._p(y), M, N, K,
+                                                       64, H._stream())
+    assert rc == 0
+    yh = host(y, np.uint16)
+    assert (yh[M] == np.uint16(0x449A)).all()  # 1234.0 in BF16: row M untouched
+    got = G.bf16_bits_to_f32(yh[:M].reshape(-1)).astype(np.float64).reshape(M, N)
+    ref, asum = oracle.htile_f64(host(hole), host(plug), host(am), host(x, np.uint16), M, N, K, 64)
+    ref, asum = ref.reshape(M, N), asum.reshape(M, N)
+    bound = np.abs(ref) * 2.0 ** -8 + asum * (2.0 ** -9 + (K + 2) * 2.0 ** -23) * 1.01
+    assert (np.abs(got - ref) <= bound).all(), float((np.abs(got - ref) / bound).max())
+    rel = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+    assert rel <= 4e-3, rel
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 1024, 4096), (300, 1000, 576), (513, 1100, 1024), (2048, 384, 640),
                                    (2000, 6100, 1088), (4096, 4096, 576)])
 def test_bf16_prefill_tiles_rel_frobenius(oracle, M, N, K):
@@ -146,8 +175,9 @@ SPLIT_SHAPES = [(64, 64, 2368), (40, 200, 1088), (64, 14336, 4096), (64, 4096, 1
 def test_bf16_split_k(oracle, M, N, K):
     """Shapes whose output tiles alone would leave most of the device idle split K over
     several workgroups per tile (K = 64 * 37 gives a ragged last split; K = 2304 and 768
-    give odd counts of 4-step super-steps with ragged M and N; M = 2 the smallest tile
-    M; M = 1024 and 1000 the 256 x 256 tiles split 4 ways, the latter with ragged tiles);
+    give odd counts of 4-step super-steps with ragged M and N; M = 1024 and 1000 the
+    256 x 256 tiles split 4 ways, the latter with ragged tiles; M = 2 on the gate shape runs
+    the small-M GEMV);
     the last workgroup of a tile adds the partial tiles in split order. Checked: relative Frobenius error
     against fp32 on the expanded weights (a lost or doubled partial fails it), every row
     bounded, bitwise-equal repeats, and bitwise-equal results from two streams running at
