@@ -306,6 +306,13 @@ def bench_prefill(torch, H, steps: int, copies: int = 6):
             ms = timed(torch, calls, steps * 3, copies)
             byt = N * K * (1 + 4 / 64) + 2 * M * K + 2 * M * N
             dec[f"M{M}_{name}"] = {"ms": ms, "eff_gbs": byt / ms / 1e6, "hbm_frac": byt / ms / 1e6 / HBM_PEAK_GBS}
+            # the reference ABI's f32 output (the f32 small-M GEMV up to M = 4, the 3-plane tile above)
+            yf = torch.empty(M, N, dtype=torch.float32, device="cuda")
+            calls32 = [bound(lib.launch_glint_htile_s3_f32_stream, p[0], p[1], p[2], x, yf, M, N, K, 64, st) for p in cps]
+            settle(torch, calls32, 0.05)
+            ms32 = timed(torch, calls32, steps * 3, copies)
+            dec[f"M{M}_{name}"]["f32_out"] = {"ms": ms32, "eff_gbs": (byt + 2 * M * N) / ms32 / 1e6}
+            del yf
     out["batched_decode"] = dec
     for M in (64, 512, 2048):
         for name, (cps, N, K) in pins.items():
@@ -969,7 +976,7 @@ def main() -> int:
             extra["prefill"] = bench_prefill(torch, H, steps=12)
             log("prefill " + ", ".join(f"{k} {v['ms'] * 1e3:.1f} us (f32 out {v['f32_out']['ms'] * 1e3:.1f})"
                                        for k, v in extra["prefill"].items() if k != "batched_decode"))
-            log("batched decode " + ", ".join(f"{k} {v['ms'] * 1e3:.1f} us"
+            log("batched decode " + ", ".join(f"{k} {v['ms'] * 1e3:.1f} us (f32 out {v['f32_out']['ms'] * 1e3:.1f})"
                                               for k, v in extra["prefill"]["batched_decode"].items()))
         if "int8" in parts:
             extra["int8_gemm"] = bench_int8(torch, H, steps=10)

@@ -295,6 +295,32 @@ __device__ __forceinline__ void glint_cells_fill_sstore(float *ltab, const Glint
     }
 }
 
+/* A lane's partial the way the reference forms it, w = cell * absmax per weight and then
+ * the FMA with x, for a block whose absmax is infinite, NaN or at least 2^126: there the
+ * factored form (sum of cell * x, times absmax) can give +-inf where products of mixed sign
+ * give NaN, or a finite value where a product overflows. Only the f32-out GEMVs take it;
+ * `xr` is the lane's 32 elements of x as f32. */
+template <int EL>
+__device__ __forceinline__ float gemv_exact_part(const float *ltab, const GemvRow<EL> &row, uint32_t lane4,
+                                                 const float (&xr)[EL]) {
+    float pe = 0.0f;
+#pragma unroll
+    for (int q = 0; q < EL / 8; ++q) {
+        const uint32_t H = gemv_word<EL>(row.h, q), P = gemv_word<EL>(row.p, q);
+        const uint32_t E = glint_codes_even(H, P);
+        const uint32_t O = glint_codes_odd(H, P);
+        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)) * row.a, xr[8 * q + 0], pe);
+        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)) * row.a, xr[8 * q + 1], pe);
+        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)) * row.a, xr[8 * q + 2], pe);
+        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)) * row.a, xr[8 * q + 3], pe);
+        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)) * row.a, xr[8 * q + 4], pe);
+        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)) * row.a, xr[8 * q + 5], pe);
+        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)) * row.a, xr[8 * q + 6], pe);
+        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)) * row.a, xr[8 * q + 7], pe);
+    }
+    return pe;
+}
+
 /* XC > 0: x goes through LDS. Thread t loads 16-B chunks t + c blockDim.x (c < XC, with
  * XC blockDim.x >= K / 8; threads past the last chunk load it again and store nothing), the
  * G waves of a slice then read it from LDS instead of each loading it from L2. XC == 0:
@@ -386,7 +412,11 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
             if ((q + 1) % GEMV_X_BATCH == 0)
                 __builtin_amdgcn_sched_barrier(0);
         }
-        const float v = glint_row16_sum(row.a * part);
+        float sc = row.a * part;
+        if constexpr (!OUT_BF16)
+            if (!(__builtin_fabsf(row.a) < 0x1p126f)) /* rare: the f32 ABI's per-weight products */
+                sc = gemv_exact_part<EL>(ltab, row, lane4, xr);
+        const float v = glint_row16_sum(sc);
         if ((lane & 15) == 0)
             red[((g + i * G) * S + s) * 4 + (lane >> 4)] = v;
     };
@@ -456,12 +486,16 @@ __global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(
  * both within the BF16 API's 1e-2 relative Frobenius bound. Rows of x past M repeat row
  * M - 1 and are not stored. */
 typedef __bf16 glint_bf16x2_t __attribute__((ext_vector_type(2)));
-template <int MR>
+/* F32: the f32-out form (the reference ABI's launch_glint_htile_s3_f32_stream at M = 2 .. 4):
+ * x held as f32 (MR x 32 registers) and one f32 FMA per weight and row in k order, the
+ * weights the exact f32 cells; the same arithmetic per row as the M = 1 f32 GEMV, so the
+ * same (K + 2) 2^-23 sum |w x| bound. */
+template <int MR, bool F32>
 __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__restrict__ hole,
                                                                   const void *__restrict__ plug,
                                                                   const float *__restrict__ absmax,
                                                                   const uint16_t *__restrict__ x,
-                                                                  uint16_t *__restrict__ y, int M, int N, int K,
+                                                                  void *__restrict__ y, int M, int N, int K,
                                                                   int G, int rows_per_wg) {
     __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS]; /* 64 KiB at LDS offset 0 */
     extern __shared__ __attribute__((aligned(16))) float red[]; /* [rows_per_wg][S][4][MR] */
@@ -495,6 +529,17 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__
     __builtin_amdgcn_sched_barrier(0);
     glint_cells_fill_sstore(ltab, fill);
     __syncthreads();
+    float xf[F32 ? MR : 1][F32 ? 32 : 1];
+    if constexpr (F32) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t xw = xv[m][e >> 2][e & 3];
+                xf[m][2 * e] = glint_bf16lo(xw);
+                xf[m][2 * e + 1] = glint_bf16hi(xw);
+            }
+    }
 
     auto compute_row = [&](int i, const GemvRow<EL> &row) {
         float part[MR];
@@ -506,30 +551,52 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__
             const uint32_t H = gemv_word<EL>(row.h, q), P = gemv_word<EL>(row.p, q);
             const uint32_t E = glint_codes_even(H, P);
             const uint32_t O = glint_codes_odd(H, P);
-            uint32_t wp[4];
-            wp[0] = glint_cvt_bf16x2(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)),
-                                     glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)));
-            wp[1] = glint_cvt_bf16x2(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)),
-                                     glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)));
-            wp[2] = glint_cvt_bf16x2(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)),
-                                     glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)));
-            wp[3] = glint_cvt_bf16x2(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)),
-                                     glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)));
+            float c[8];
+            c[0] = glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4));
+            c[1] = glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4));
+            c[2] = glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4));
+            c[3] = glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4));
+            c[4] = glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4));
+            c[5] = glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4));
+            c[6] = glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4));
+            c[7] = glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4));
+            if constexpr (F32) {
 #pragma unroll
-            for (int m = 0; m < MR; ++m)
+                for (int m = 0; m < MR; ++m)
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    /* the word as a value: this compiler bit-casts a vector element in place as
-                     * element 0 */
-                    const uint32_t xw = xv[m][q][b];
-                    part[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(glint_bf16x2_t, wp[b]),
-                                                              __builtin_bit_cast(glint_bf16x2_t, xw), part[m], false);
-                }
+                    for (int e = 0; e < 8; ++e)
+                        part[m] = fmaf(c[e], xf[m][8 * q + e], part[m]);
+            } else {
+                uint32_t wp[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    wp[b] = glint_cvt_bf16x2(c[2 * b], c[2 * b + 1]);
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        /* the word as a value: this compiler bit-casts a vector element in
+                         * place as element 0 */
+                        const uint32_t xw = xv[m][q][b];
+                        part[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(glint_bf16x2_t, wp[b]),
+                                                                  __builtin_bit_cast(glint_bf16x2_t, xw), part[m],
+                                                                  false);
+                    }
+            }
         }
         const int t = g + i * G;
+        float sc[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            sc[m] = row.a * part[m];
+        if constexpr (F32)
+            if (!(__builtin_fabsf(row.a) < 0x1p126f)) /* rare: the f32 ABI's per-weight products */
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+                    sc[m] = gemv_exact_part<EL>(ltab, row, lane4, xf[m]);
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            const float v = glint_row16_sum(row.a * part[m]);
+            const float v = glint_row16_sum(sc[m]);
             if ((lane & 15) == 0)
                 red[((t * S + s) * 4 + (lane >> 4)) * MR + m] = v;
         }
@@ -559,24 +626,41 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__
         float sum = 0.0f;
         for (int k = 0; k < S * 4; ++k)
             sum += red[(t * S * 4 + k) * MR + m];
-        y[(int64_t)m * N + r0 + t] = glint_f32_to_bf16(sum);
+        if (F32)
+            ((float *)y)[(int64_t)m * N + r0 + t] = sum;
+        else
+            ((uint16_t *)y)[(int64_t)m * N + r0 + t] = glint_f32_to_bf16(sum);
     }
 }
 
 #ifndef GEMV_MR_MAX
 #define GEMV_MR_MAX 8 /* largest M the small-M GEMV takes (templates for 2, 4 and 8 rows) */
 #endif
-/* k_htile_gemv_mr over 2 <= M <= GEMV_MR_MAX (bs 64, K % 2048 == 0, K / 2048 <= 8, aligned).
+/* k_htile_gemv_mr over 2 <= M <= GEMV_MR_MAX (bs 64, K % 2048 == 0, K / 2048 <= 8, aligned);
+ * the f32-out form up to GEMV_MR_MAX_F32 rows.
  * Measured against the 64-row MFMA tile (k_tile_ss) on 14336 x 4096: M = 2 14.2-15.6 us
  * against 35.0, M = 4 17.8-18.2 against 35.3, M = 5..8 24.7-24.9 against 34.3-34.6 (the
  * 8-row template holds 128 VGPRs of x and runs at 2 waves per SIMD). */
+#ifndef GEMV_MR_MAX_F32
+#define GEMV_MR_MAX_F32 4 /* largest M of the f32-out small-M GEMV (x as f32: MR x 32 registers) */
+#endif
+template <bool F32>
 static int htile_launch_gemv_mr(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y,
                                 int M, int N, int K, hipStream_t st) {
     const int S = K / 2048, G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
-    auto kern = M <= 2 ? k_htile_gemv_mr<2> : (M <= 4 ? k_htile_gemv_mr<4> : k_htile_gemv_mr<8>);
-    const int MR = M <= 2 ? 2 : (M <= 4 ? 4 : 8);
+    decltype(&k_htile_gemv_mr<2, F32>) kern;
+    int MR;
+    if constexpr (F32) { /* no 8-row f32 form: 256 registers of x */
+        kern = M <= 2 ? k_htile_gemv_mr<2, true> : k_htile_gemv_mr<4, true>;
+        MR = M <= 2 ? 2 : 4;
+    } else {
+        kern = M <= 2 ? k_htile_gemv_mr<2, false> : (M <= 4 ? k_htile_gemv_mr<4, false> : k_htile_gemv_mr<8, false>);
+        MR = M <= 2 ? 2 : (M <= 4 ? 4 : 8);
+    }
+    /* the whole resident grid: halving it where a workgroup holds one row group, as the M = 1
+     * kernel does, was slower here (4096 x 14336 f32 out at M = 4: 30.1 against 18.6 us) */
     const int64_t resident =
-        std::max<int64_t>(glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4) / (G == 1 ? GEMV_G1_DIV : 1), 1);
+        std::max<int64_t>(glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4), 1);
     const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
     int64_t rows_per_wg = G * per_wave;
     const int64_t cap = (GEMV_X_RED_MAX / (S * 4 * MR)) / G * G;
@@ -586,8 +670,7 @@ static int htile_launch_gemv_mr(const uint8_t *hole, const uint8_t *plug, const 
     const size_t lds = (size_t)rows_per_wg * S * 4 * MR * sizeof(float);
     if (glint_set_lds_limit((const void *)kern, GEMV_X_RED_MAX * 4) != 0)
         return -3;
-    kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const uint16_t *)x, (uint16_t *)y, M, N, K, G,
-                                     (int)rows_per_wg);
+    kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const uint16_t *)x, y, M, N, K, G, (int)rows_per_wg);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
@@ -733,8 +816,9 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
                          K <= GEMV_MAX_K;
     const bool mfma_ok = M > 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
                          glint_aligned(absmax, 4) && glint_aligned(x, 16);
-    if (OUT_BF16 && mfma_ok && M <= GEMV_MR_MAX && (K % 2048) == 0 && K / 2048 <= GEMV_X_THREADS / 64)
-        return htile_launch_gemv_mr(hole, plug, absmax, x, y, M, N, K, st);
+    if (mfma_ok && M <= (OUT_BF16 ? GEMV_MR_MAX : GEMV_MR_MAX_F32) && (K % 2048) == 0 &&
+        K / 2048 <= GEMV_X_THREADS / 64)
+        return htile_launch_gemv_mr<!OUT_BF16>(hole, plug, absmax, x, y, M, N, K, st);
     if (mfma_ok && OUT_BF16) {
         const GlintTileProducer p{(const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, N, K, nullptr};
         const uint16_t *xb = (const uint16_t *)x;

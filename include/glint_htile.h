@@ -30,7 +30,8 @@ int launch_glint_htile_s3_f32(const uint8_t *d_hole, const uint8_t *d_plug, cons
 
 /* ---- Additive (no reference counterpart). ----
  * BF16 output with f32 accumulation: the decode GEMV (M = 1, and M = 2 .. 8 with each
- * weight read once for all rows, as BF16(cell) x absmax) and the prefill GEMM (larger M:
+ * weight read once for all rows, as BF16(cell) x absmax; the f32-out entry above takes the
+ * same route at M = 2 .. 4 with exact f32 cells) and the prefill GEMM (larger M:
  * BF16 MFMA on LDS-dequantized weight tiles). Contract: within
  * 1e-2 relative Frobenius error of an f32 GEMM on the expanded weights; results are
  * deterministic (split K adds its partial tiles in a fixed order).

@@ -298,6 +298,59 @@ def test_f32_prefill_mfma_special_absmax(oracle):
     assert (err <= (K + 2) * 2.0 ** -23 * asum[fin] + 1e-30).all()
 
 
+@pytest.mark.parametrize("M,N,K", [(2, 14336, 4096), (3, 4096, 14336), (4, 1000, 2048), (4, 17, 16384),
+                                   (2, 4097, 8192)])
+def test_small_m_f32_gemv_vs_float64(oracle, M, N, K):
+    """The f32-out ABI at 2 <= M <= 4 (K % 2048 == 0) on the small-M GEMV: exact f32 cells,
+    one FMA per weight and row. Every output within the f32 summation bound
+    (K + 2) 2^-23 sum|t| and the reference's 1e-5 (1 + |ref|); repeats bit-equal."""
+    torch = torch_cuda()
+    print(f"small-M f32 gemv M={M} N={N} K={K}", flush=True)
+    hole, plug, am = _encoded_weight(oracle, N, K, 4100 + K)
+    g = torch.Generator(device="cuda").manual_seed(4101 + M)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    y = host(H.htile_f32(hole, plug, am, x, N, K, 64)).reshape(M, N).astype(np.float64)
+    ref, asum = oracle.htile_f64(host(hole), host(plug), host(am), host(x, np.uint16), M, N, K, 64)
+    err = np.abs(y - ref)
+    assert (err <= (K + 2) * 2.0 ** -23 * asum).all(), float((err / ((K + 2) * 2.0 ** -23 * asum)).max())
+    assert (err <= 1e-5 * (1 + np.abs(ref))).all(), float(err.max())
+    again = H.htile_f32(hole, plug, am, x, N, K, 64)
+    assert np.array_equal(host(again).reshape(M, N), y.astype(np.float32))
+
+
+@pytest.mark.parametrize("M,K", [(1, 2048), (1, 4096), (2, 2048), (4, 4096)])
+def test_f32_gemv_special_absmax(oracle, M, K):
+    """The f32-out GEMVs (M = 1 and the small-M form) on blocks with an infinite or NaN absmax,
+    one whose CELLS * absmax overflows f32 and one at 2^126: such a block takes the
+    reference's per-weight products (cell * absmax, then the FMA with x), so NaN and +-inf
+    land exactly where the f32 restatement puts them; the finite outputs agree within the
+    bound."""
+    torch = torch_cuda()
+    N = 64
+    nb = K // 64
+    rng = np.random.default_rng(78 + K + M)
+    i = np.arange(N * K // 2)
+    hole = ((i * 7 + 1) % 256).astype(np.uint8)
+    plug = ((i * 13 + 5) % 256).astype(np.uint8)
+    am = rng.uniform(0.5, 1.5, N * nb).astype(np.float32)
+    am[nb * 3 + 1] = np.inf          # row 3, block 1
+    am[nb * 10 + 0] = np.nan         # row 10, block 0
+    am[nb * 20 + 2] = np.finfo(np.float32).max  # row 20: CELLS * absmax overflows where |cells| > 1
+    am[nb * 30 + 3] = np.float32(2.0 ** 126)
+    am[nb * 40 + 5] = -np.inf        # row 40: a negative infinite absmax
+    x = bf16_bits(rng.normal(0, 1e-3, M * K).astype(np.float32))
+    x[64 + 5] = 0  # a zero x against row 3's infinite block (element 69 of x row 0)
+    y = host(H.htile_f32(dev(hole), dev(plug), dev(am), dev(x).reshape(M, K), N, K, 64)).reshape(M, N)
+    ref32 = oracle.htile_f32(hole, plug, am, x, M, N, K, 64).reshape(M, N)
+    assert np.isnan(ref32).any()  # mixed-sign infinite products; the factored form would give +-inf
+    assert np.array_equal(np.isnan(y), np.isnan(ref32))
+    assert np.array_equal(np.isinf(y), np.isinf(ref32)) and np.array_equal(y[np.isinf(y)], ref32[np.isinf(ref32)])
+    fin = np.isfinite(ref32)
+    ref, asum = oracle.htile_f64(hole, plug, am, x, M, N, K, 64)
+    err = np.abs(y[fin].astype(np.float64) - ref.reshape(M, N)[fin])
+    assert (err <= (K + 2) * 2.0 ** -23 * asum.reshape(M, N)[fin] + 1e-30).all()
+
+
 def test_split_workspace_under_graph_capture(oracle):
     """A split-K launch captured into a graph keeps the workspace it bound: after the
     capture, eager calls on the capture stream get a fresh workspace (they never share
