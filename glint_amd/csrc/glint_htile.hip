@@ -146,7 +146,33 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
                 /* at most 8 lookups in flight per wave: bounds live registers */
                 __builtin_amdgcn_sched_barrier(0);
             }
-            acc[r] = fmaf(jc < nch ? item[r].a : 0.0f, part, acc[r]);
+            const float a = jc < nch ? item[r].a : 0.0f;
+            if constexpr (!OUT_BF16) {
+                if (!(__builtin_fabsf(a) < 0x1p126f)) {
+                    /* rare: infinite, NaN or huge absmax take the f32 ABI's per-weight
+                     * products (cell * absmax, then the FMA), as the reference forms them */
+                    float pe = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const glint_f32x4 xa = xs[(2 * q) * xplane + jc];
+                        const glint_f32x4 xb = xs[(2 * q + 1) * xplane + jc];
+                        const uint32_t E = glint_codes_even(H[q], P[q]);
+                        const uint32_t O = glint_codes_odd(H[q], P[q]);
+                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)) * a, xa.x, pe);
+                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)) * a, xa.y, pe);
+                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)) * a, xa.z, pe);
+                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)) * a, xa.w, pe);
+                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)) * a, xb.x, pe);
+                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)) * a, xb.y, pe);
+                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)) * a, xb.z, pe);
+                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)) * a, xb.w, pe);
+                    }
+                    part = pe;
+                    acc[r] += part;
+                    continue;
+                }
+            }
+            acc[r] = fmaf(a, part, acc[r]);
         }
         if (step == steps - 1) { /* task done: reduce its rows and store */
             const int n0 = (g0 + (t / steps) * nwaves) * R;
@@ -766,16 +792,18 @@ static unsigned gemv_grid(const void *kern, int threads, size_t lds, int64_t tas
     return (unsigned)(needed < resident ? needed : resident);
 }
 
-/* k_htile_gemv_xreg over an M = 1 GEMV (bs 64, K % 2048 == 0, K / 2048 <= 8, aligned). */
-template <bool OUT_BF16>
+/* k_htile_gemv_xreg over an M = 1 GEMV (bs 64, K % (64 EL) == 0, K / (64 EL) <= 8, aligned).
+ * EL = 16 (8-B plane loads) for the K % 1024 == 0 shapes was timed slower than
+ * k_htile_gemv_b64 (13824 x 5120: 24.8 against 19.4 us), so only EL = 32 is dispatched. */
+template <bool OUT_BF16, int EL = GEMV_X_EL>
 static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x,
                                   void *y, int N, int K, hipStream_t st) {
-    const int S = K / (64 * GEMV_X_EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
+    const int S = K / (64 * EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
     /* K / 8 chunks of x over 64 S G threads: 4 / G per thread */
     /* S <= 2 (G >= 4): one row in flight per wave; more slices: GEMV_X_DEPTH */
-    auto kern = S <= 2 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 1, GEMV_X_DEPTH_S2>
-                       : (G >= 2 ? k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 2, GEMV_X_DEPTH>
-                                 : k_htile_gemv_xreg<GEMV_X_EL, OUT_BF16, 0, GEMV_X_DEPTH>);
+    auto kern = S <= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 1, GEMV_X_DEPTH_S2>
+                       : (G >= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 2, GEMV_X_DEPTH>
+                                 : k_htile_gemv_xreg<EL, OUT_BF16, 0, GEMV_X_DEPTH>);
     const int64_t resident =
         std::max<int64_t>(glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4) / (G == 1 ? GEMV_G1_DIV : 1), 1);
     const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
@@ -850,6 +878,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             return -5;
     } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS / 64) {
         return htile_launch_gemv_xreg<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);
+
     } else if (gemv_ok) {
         constexpr int R = GEMV_R, D = GEMV_D;
         const size_t lds = GEMV_LDS_BYTES(K);
