@@ -233,7 +233,13 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
  * registers; its partial sum is folded to 4 row-of-16 sums by DPP and parked in LDS, and
  * after one barrier the workgroup adds the 4 S partials of each row in a fixed order. */
 #ifndef GEMV_X_THREADS
-#define GEMV_X_THREADS 512 /* most threads per workgroup (whole waves of S slices are used) */
+#define GEMV_X_THREADS 512 /* most threads per workgroup at S <= 2 (whole waves of S slices are used) */
+#endif
+#ifndef GEMV_X_THREADS_WIDE
+#define GEMV_X_THREADS_WIDE 1024 /* most threads per workgroup at S > 2 */
+#endif
+#ifndef GEMV_X_WIDE_TARGET
+#define GEMV_X_WIDE_TARGET 768 /* S > 2: G = max(2, TARGET / (64 S)) row groups share x through LDS */
 #endif
 #ifndef GEMV_X_EL
 #define GEMV_X_EL 32 /* elements per lane per row: 32 (16-B plane loads) or 16 (8-B) */
@@ -245,7 +251,7 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #define GEMV_X_DEPTH_S2 1 /* rows of loads in flight per wave at S <= 2 slices (K <= 4096) */
 #endif
 #ifndef GEMV_X_DEPTH
-#define GEMV_X_DEPTH 2 /* rows of loads in flight per wave at S > 2 (3 and 4 measured 2% and 12% slower) */
+#define GEMV_X_DEPTH 1 /* rows of loads in flight per wave at S > 2 */
 #endif
 #ifndef GEMV_X_PRE
 #define GEMV_X_PRE 8 /* most rows issued before the table fill's barrier */
@@ -261,6 +267,8 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #define GEMV_X_WPE 1 /* minimum waves per SIMD the register allocation must allow */
 #endif
 #define GEMV_X_RED_MAX 4096 /* floats of per-row partials a workgroup may park in LDS */
+/* dynamic LDS of k_htile_gemv_xreg: the row partials, or x as BF16 while it is staged */
+#define GEMV_X_LDS_MAX (GEMV_X_RED_MAX * 4 > GEMV_MAX_K * 2 ? GEMV_X_RED_MAX * 4 : GEMV_MAX_K * 2)
 
 template <int EL> struct GemvVec;
 template <> struct GemvVec<32> { typedef glint_u32x4 T; };
@@ -351,8 +359,8 @@ __device__ __forceinline__ float gemv_exact_part(const float *ltab, const GemvRo
  * XC blockDim.x >= K / 8; threads past the last chunk load it again and store nothing), the
  * G waves of a slice then read it from LDS instead of each loading it from L2. XC == 0:
  * each wave loads its slice itself (G == 1, no repeats). */
-template <int EL, bool OUT_BF16, int XC, int DEPTH>
-__global__ __launch_bounds__(GEMV_X_THREADS) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE))) void k_htile_gemv_xreg(
+template <int EL, bool OUT_BF16, int XC, int DEPTH, int MAXT>
+__global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE))) void k_htile_gemv_xreg(
     const void *__restrict__ hole, const void *__restrict__ plug, const float *__restrict__ absmax,
     const glint_u32x4 *__restrict__ x, void *__restrict__ y, int N, int K, int G, int rows_per_wg) {
     __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS]; /* 64 KiB at LDS offset 0 */
@@ -794,18 +802,30 @@ static unsigned gemv_grid(const void *kern, int threads, size_t lds, int64_t tas
 
 /* k_htile_gemv_xreg over an M = 1 GEMV (bs 64, K % (64 EL) == 0, K / (64 EL) <= 8, aligned).
  * EL = 16 (8-B plane loads) for the K % 1024 == 0 shapes was timed slower than
- * k_htile_gemv_b64 (13824 x 5120: 24.8 against 19.4 us), so only EL = 32 is dispatched. */
+ * k_htile_gemv_b64 (13824 x 5120: 24.8 against 19.4 us), so only EL = 32 is dispatched.
+ * Workgroups: up to GEMV_X_THREADS threads at S <= 2 (two per CU); at S > 2 about
+ * GEMV_X_WIDE_TARGET threads and at least G = 2 row groups sharing one staged x, one
+ * row in flight per wave. Against at most 512 threads (G = 1 at S >= 5, on half the
+ * resident grid) with two rows in flight: 4096 x 6144 8.2 -> 7.8 us, 4096 x 10240
+ * 12.3 -> 10.5, 4096 x 12288 12.3 -> 11.3, 4096 x 14336 13.1 -> 12.8, 28672 x 8192
+ * 40.6 -> 39.4; 4096 x 16384 equal. */
 template <bool OUT_BF16, int EL = GEMV_X_EL>
 static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x,
                                   void *y, int N, int K, hipStream_t st) {
-    const int S = K / (64 * EL), G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
-    /* K / 8 chunks of x over 64 S G threads: 4 / G per thread */
-    /* S <= 2 (G >= 4): one row in flight per wave; more slices: GEMV_X_DEPTH */
-    auto kern = S <= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 1, GEMV_X_DEPTH_S2>
-                       : (G >= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 2, GEMV_X_DEPTH>
-                                 : k_htile_gemv_xreg<EL, OUT_BF16, 0, GEMV_X_DEPTH>);
+    const int S = K / (64 * EL);
+    const int G = S <= 2 ? (GEMV_X_THREADS / 64) / S
+                         : std::min(std::max(2, (GEMV_X_WIDE_TARGET / 64) / S), (GEMV_X_THREADS_WIDE / 64) / S);
+    const int threads = 64 * S * G;
+    if (G < 1)
+        return -3;
+    /* x staging (G >= 2): K / 8 chunks of 16 B over 64 S G threads, XC chunks per thread;
+     * S <= 2 (G >= 4): one chunk, one row in flight per wave; more slices: GEMV_X_DEPTH */
+    auto kern = S <= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 1, GEMV_X_DEPTH_S2, GEMV_X_THREADS>
+                       : (G >= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 2, GEMV_X_DEPTH, GEMV_X_THREADS_WIDE>
+                                 : k_htile_gemv_xreg<EL, OUT_BF16, 0, GEMV_X_DEPTH, GEMV_X_THREADS_WIDE>);
+    const size_t lds_max = G >= 2 ? std::max<size_t>(GEMV_X_RED_MAX * 4, (size_t)K * 2) : GEMV_X_RED_MAX * 4;
     const int64_t resident =
-        std::max<int64_t>(glint_resident_grid((const void *)kern, threads, GEMV_X_RED_MAX * 4) / (G == 1 ? GEMV_G1_DIV : 1), 1);
+        std::max<int64_t>(glint_resident_grid((const void *)kern, threads, lds_max) / (G == 1 ? GEMV_G1_DIV : 1), 1);
     const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
     int64_t rows_per_wg = G * per_wave;
     const int64_t cap = (GEMV_X_RED_MAX / (S * 4)) / G * G;
@@ -814,8 +834,8 @@ static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, cons
     const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
     size_t lds = (size_t)rows_per_wg * S * 4 * sizeof(float);
     if (G >= 2 && lds < (size_t)K * 2)
-        lds = (size_t)K * 2; /* x staging; K <= 8192 here, within GEMV_X_RED_MAX floats */
-    if (glint_set_lds_limit((const void *)kern, GEMV_X_RED_MAX * 4) != 0)
+        lds = (size_t)K * 2; /* x staging: K <= GEMV_MAX_K, within GEMV_X_LDS_MAX bytes */
+    if (glint_set_lds_limit((const void *)kern, GEMV_X_LDS_MAX) != 0)
         return -3;
     kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const glint_u32x4 *)x, y, N, K, G, (int)rows_per_wg);
     return hipGetLastError() == hipSuccess ? 0 : -3;
@@ -876,7 +896,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
                 : tile_mfma_launch<128, 128, 2, 4, 2, GlintTileProducer, TileOutF32, 3>(p, xb, yf, M, N, K, st, fixed);
         if (!planned)
             return -5;
-    } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS / 64) {
+    } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS_WIDE / 64) {
         return htile_launch_gemv_xreg<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);
 
     } else if (gemv_ok) {

@@ -83,7 +83,7 @@ def _encoded_weight(oracle, N, K, seed, bs=64):
 
 
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336), (100, 64), (3, 1088), (129, 2048), (1, 2048),
-                                 (7, 6144), (1000, 12288), (17, 16384), (4097, 8192),
+                                 (7, 6144), (1000, 12288), (17, 16384), (4097, 8192), (2000, 10240),
                                  (13824, 5120), (5, 1024), (300, 3072), (77, 7168)])
 def test_gemv_fast_path_vs_float64(oracle, N, K):
     torch = torch_cuda()
@@ -319,10 +319,11 @@ def test_small_m_f32_gemv_vs_float64(oracle, M, N, K):
     assert np.array_equal(host(again).reshape(M, N), y.astype(np.float32))
 
 
-@pytest.mark.parametrize("M,K", [(1, 2048), (1, 4096), (1, 1088), (1, 3072), (2, 2048), (4, 4096)])
+@pytest.mark.parametrize("M,K", [(1, 2048), (1, 4096), (1, 1088), (1, 3072), (1, 14336), (2, 2048), (4, 4096)])
 def test_f32_gemv_special_absmax(oracle, M, K):
-    """The f32-out GEMVs (M = 1: x in registers at K % 1024 == 0, x in LDS at K = 1088; and
-    the small-M form) on blocks with an infinite or NaN absmax,
+    """The f32-out GEMVs (M = 1: x in registers at K % 2048 == 0, in 512-thread workgroups
+    up to K = 4096 and wider ones above; x in LDS at K = 1088 and 3072; and the small-M
+    form) on blocks with an infinite or NaN absmax,
     one whose CELLS * absmax overflows f32 and one at 2^126: such a block takes the
     reference's per-weight products (cell * absmax, then the FMA with x), so NaN and +-inf
     land exactly where the f32 restatement puts them; the finite outputs agree within the
