@@ -245,7 +245,7 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #define GEMV_X_EL 32 /* elements per lane per row: 32 (16-B plane loads) or 16 (8-B) */
 #endif
 #ifndef GEMV_G1_DIV
-#define GEMV_G1_DIV 2 /* one row group per workgroup (G == 1: S = K / 2048 >= 5, K >= 10240): resident grid / this */
+#define GEMV_G1_DIV 2 /* one row group per workgroup (G == 1, only where GEMV_X_THREADS_WIDE < 128 S): resident grid / this */
 #endif
 #ifndef GEMV_X_DEPTH_S2
 #define GEMV_X_DEPTH_S2 1 /* rows of loads in flight per wave at S <= 2 slices (K <= 4096) */
