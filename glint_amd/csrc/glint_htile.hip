@@ -245,13 +245,16 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #define GEMV_X_EL 32 /* elements per lane per row: 32 (16-B plane loads) or 16 (8-B) */
 #endif
 #ifndef GEMV_G1_DIV
-#define GEMV_G1_DIV 2 /* one row group per workgroup (G == 1, only where GEMV_X_THREADS_WIDE < 128 S): resident grid / this */
+#define GEMV_G1_DIV 2 /* one row group per workgroup (G == 1: S > 8): resident grid / this where >= the CUs */
 #endif
 #ifndef GEMV_X_DEPTH_S2
 #define GEMV_X_DEPTH_S2 1 /* rows of loads in flight per wave at S <= 2 slices (K <= 4096) */
 #endif
 #ifndef GEMV_X_DEPTH
 #define GEMV_X_DEPTH 1 /* rows of loads in flight per wave at S > 2 */
+#endif
+#ifndef GEMV_X_DEPTH_G1
+#define GEMV_X_DEPTH_G1 1 /* rows of loads in flight per wave at G == 1 (S > 8: K > 16384; 8192 x 28672: 41.5 us, two rows 44.3, three 45.4) */
 #endif
 #ifndef GEMV_X_PRE
 #define GEMV_X_PRE 8 /* most rows issued before the table fill's barrier */
@@ -267,8 +270,9 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #define GEMV_X_WPE 1 /* minimum waves per SIMD the register allocation must allow */
 #endif
 #define GEMV_X_RED_MAX 4096 /* floats of per-row partials a workgroup may park in LDS */
+#define GEMV_X_S_MAX (GEMV_X_THREADS_WIDE / 64) /* most K slices: K <= 32768 at EL = 32 */
 /* dynamic LDS of k_htile_gemv_xreg: the row partials, or x as BF16 while it is staged */
-#define GEMV_X_LDS_MAX (GEMV_X_RED_MAX * 4 > GEMV_MAX_K * 2 ? GEMV_X_RED_MAX * 4 : GEMV_MAX_K * 2)
+#define GEMV_X_LDS_MAX (GEMV_X_RED_MAX * 4 > GEMV_MAX_K * 2 ? GEMV_X_RED_MAX * 4 : GEMV_MAX_K * 2) /* x staged at G >= 2: S <= 8 */
 
 template <int EL> struct GemvVec;
 template <> struct GemvVec<32> { typedef glint_u32x4 T; };
@@ -816,16 +820,17 @@ static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, cons
     const int G = S <= 2 ? (GEMV_X_THREADS / 64) / S
                          : std::min(std::max(2, (GEMV_X_WIDE_TARGET / 64) / S), (GEMV_X_THREADS_WIDE / 64) / S);
     const int threads = 64 * S * G;
-    if (G < 1)
+    if (G < 1 || (G >= 2 && (size_t)K * 2 > GEMV_X_LDS_MAX))
         return -3;
     /* x staging (G >= 2): K / 8 chunks of 16 B over 64 S G threads, XC chunks per thread;
      * S <= 2 (G >= 4): one chunk, one row in flight per wave; more slices: GEMV_X_DEPTH */
     auto kern = S <= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 1, GEMV_X_DEPTH_S2, GEMV_X_THREADS>
                        : (G >= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 2, GEMV_X_DEPTH, GEMV_X_THREADS_WIDE>
-                                 : k_htile_gemv_xreg<EL, OUT_BF16, 0, GEMV_X_DEPTH, GEMV_X_THREADS_WIDE>);
+                                 : k_htile_gemv_xreg<EL, OUT_BF16, 0, GEMV_X_DEPTH_G1, GEMV_X_THREADS_WIDE>);
     const size_t lds_max = G >= 2 ? std::max<size_t>(GEMV_X_RED_MAX * 4, (size_t)K * 2) : GEMV_X_RED_MAX * 4;
-    const int64_t resident =
-        std::max<int64_t>(glint_resident_grid((const void *)kern, threads, lds_max) / (G == 1 ? GEMV_G1_DIV : 1), 1);
+    int64_t resident = std::max<int64_t>(glint_resident_grid((const void *)kern, threads, lds_max), 1);
+    if (G == 1 && resident / GEMV_G1_DIV >= glint_cu_count())
+        resident /= GEMV_G1_DIV; /* only where two or more workgroups would share a CU */
     const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
     int64_t rows_per_wg = G * per_wave;
     const int64_t cap = (GEMV_X_RED_MAX / (S * 4)) / G * G;
@@ -859,14 +864,18 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         return -2;
     if (M <= 0 || N <= 0)
         return 0;
-    const bool gemv_ok = M == 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
-                         glint_aligned(absmax, 4) && glint_aligned(x, 16) &&
-                         K <= GEMV_MAX_K;
-    const bool mfma_ok = M > 1 && bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
+    const bool fast_ok = bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
                          glint_aligned(absmax, 4) && glint_aligned(x, 16);
-    if (mfma_ok && M <= (OUT_BF16 ? GEMV_MR_MAX : GEMV_MR_MAX_F32) && (K % 2048) == 0 &&
+    /* M = 1: the x-register GEMV (K % 2048 == 0, K <= 32768), else the x-in-LDS GEMV
+     * (K <= 16384), else the tiles; M > 1: the small-M GEMV or the tiles */
+    const bool gemv_x_ok = M == 1 && fast_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_S_MAX;
+    const bool gemv_ok = M == 1 && fast_ok && !gemv_x_ok && K <= GEMV_MAX_K;
+    const bool mfma_ok = fast_ok && !gemv_x_ok && !gemv_ok;
+    if (mfma_ok && M > 1 && M <= (OUT_BF16 ? GEMV_MR_MAX : GEMV_MR_MAX_F32) && (K % 2048) == 0 &&
         K / 2048 <= GEMV_X_THREADS / 64)
         return htile_launch_gemv_mr<!OUT_BF16>(hole, plug, absmax, x, y, M, N, K, st);
+    if (gemv_x_ok)
+        return htile_launch_gemv_xreg<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);
     if (mfma_ok && OUT_BF16) {
         const GlintTileProducer p{(const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, N, K, nullptr};
         const uint16_t *xb = (const uint16_t *)x;
@@ -896,9 +905,6 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
                 : tile_mfma_launch<128, 128, 2, 4, 2, GlintTileProducer, TileOutF32, 3>(p, xb, yf, M, N, K, st, fixed);
         if (!planned)
             return -5;
-    } else if (gemv_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_THREADS_WIDE / 64) {
-        return htile_launch_gemv_xreg<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);
-
     } else if (gemv_ok) {
         constexpr int R = GEMV_R, D = GEMV_D;
         const size_t lds = GEMV_LDS_BYTES(K);
