@@ -3,15 +3,14 @@
  * y[m, n] = sum_k CELLS[h][p] * absmax[(n*K + k) / bs] * x[m, k]
  * (reference cuda/glint_htile.cu:124-164 and glint_htile_sim.py:22-50; f32 arithmetic).
  *
- * k_htile_gemv_xreg — decode (M = 1), bs = 64, K % 2048 == 0 (the decode shapes): HBM-bound.
- *   Each wave keeps a 2048-wide slice of x in registers and streams weight rows past it:
+ * k_htile_gemv_xreg — decode (M = 1), bs = 64, K <= 32768: HBM-bound.
+ *   Each wave keeps a 2048-wide slice of x in registers (the last slice of a K that is not
+ *   a multiple of 2048 partly idle) and streams weight rows past it:
  *   per row, lane l reads 16 B of each nibble plane (32 consecutive k inside one absmax
  *   block), so a wave load is 1 KiB contiguous; rows are multi-buffered in registers. The
  *   cell table sits in LDS as 64 lane-private copies, so lookups never conflict and each
  *   lookup address is one v_perm_b32. Per element: 0.5 op to form code bytes, 1 perm, 1 LDS
  *   read, 1 f32 FMA; per row one FMA by the block absmax and 4 DPP adds.
- * k_htile_gemv_b64 — decode for the other K % 64 == 0: x staged in LDS as f32 planes,
- *   (task, step) items double-buffered in registers.
  * Prefill (M > 1, bf16 out, bs = 64; tile_mfma.h): BF16 MFMA on double-buffered
  *   LDS-dequantized weight tiles, f32 accumulation, K split across workgroups when the
  *   tiles alone would leave CUs idle (fixed-order reduction). k_tile_mfma: 256 x 128 tiles
@@ -22,211 +21,17 @@
  *   weights decoded to f32 in LDS per 32-wide K step, f32 FMAs in k order.
  */
 #include <algorithm>
+#include <type_traits>
 
 #include "glint_common.h"
 #include "glint_htile.h"
 #include "tile_mfma.h"
 
-/* ---------------------------------------------------------------- GEMV (M = 1) */
-#ifndef GEMV_R
-#define GEMV_R 1 /* weight rows per wave task */
-#endif
-#ifndef GEMV_D
-#define GEMV_D 1 /* groups of (task, step) items per register buffer (two buffers) */
-#endif
-#ifndef GEMV_T
-#define GEMV_T 1024 /* threads per workgroup */
-#endif
-#ifndef GEMV_WPE
-#define GEMV_WPE 4 /* minimum waves per SIMD the register allocation must allow */
-#endif
-/* x (K f32) + the 65 KiB of tables fit in the 160 KiB of LDS */
-#define GEMV_MAX_K 16384
-#define GEMV_LDS_BYTES(K) ((size_t)(K) * 4 + 128) /* dynamic part: x as f32 + one zero chunk */
-/* x is stored as 8 planes of (K/32 + 1) float4: plane q holds floats 4q..4q+3 of every
- * 32-element chunk, so the 64 lanes of one ds_read_b128 read 64 consecutive float4. */
-
-struct GemvItem {
-    glint_u32x4 h, p; /* 32 packed elements of each plane */
-    float a;
-};
-
-/* Loads of work item t of this wave: task g = g0 + (t / steps) * nwaves, step t % steps;
- * R rows per task. Lanes past the row end read the row's last chunk with absmax 0 and the
- * zero x chunk; rows past N reuse row N-1 (their sums are not stored). */
-template <int R>
-__device__ __forceinline__ void gemv_load_item(const glint_u32x4 *__restrict__ hole, const glint_u32x4 *__restrict__ plug,
-                                               const float *__restrict__ absmax, int N, int nch, int steps, int g0,
-                                               int nwaves, int nitems_max, int t, int lane, GemvItem (&it)[R]) {
-    t = min(t, nitems_max); /* past the end: reload the last item, whose result is unused */
-    const int task = g0 + (t / steps) * nwaves;
-    const int jr = (t % steps) * 64 + lane;
-    const uint32_t j = (uint32_t)min(jr, nch - 1);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int64_t n = min(task * R + r, N - 1);
-        it[r].h = __builtin_nontemporal_load(hole + n * nch + j);
-        it[r].p = __builtin_nontemporal_load(plug + n * nch + j);
-        it[r].a = absmax[n * (nch >> 1) + (j >> 1)]; /* lanes past the row end: masked at use */
-    }
-}
-
-/* One wave runs tasks g0, g0 + nwaves, ...; each task is `steps` items (lane l of step s
- * covers elements [32 (64 s + l), +32) of each of its R rows). Items are double-buffered
- * in groups of D across task boundaries; the first group goes out before the LDS fill. */
-template <int R, int D, int THREADS, bool OUT_BF16>
-__global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glint_u32x4 *__restrict__ hole,
-                                                                      const glint_u32x4 *__restrict__ plug,
-                                                                      const float *__restrict__ absmax,
-                                                                      const glint_u32x4 *__restrict__ x,
-                                                                      void *__restrict__ y, int N, int K) {
-    __shared__ __attribute__((aligned(16))) float ltab[GLINT_LDS_CELLS64_WORDS]; /* 64 KiB at LDS offset 0 */
-    __shared__ float stage[256];
-    extern __shared__ __attribute__((aligned(16))) glint_f32x4 xs[]; /* K f32, 8 planes */
-
-    const int lane = threadIdx.x & 63;
-    const uint32_t lane4 = (uint32_t)lane * 4u;
-    const int nch = K >> 5;                 /* 32-element chunks per row */
-    const int steps = (nch + 63) >> 6;
-    const int wpb = THREADS / 64;
-    const int nwaves = gridDim.x * wpb;
-    const int ntasks = (N + R - 1) / R;
-    /* wave-uniform, so task and row arithmetic stays in scalar registers */
-    const int g0 = blockIdx.x * wpb + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int my_tasks = g0 < ntasks ? (ntasks - g0 + nwaves - 1) / nwaves : 0;
-    const int nitems = my_tasks * steps;
-
-    /* two register buffers of D items: while one is computed, the other's loads are in
-     * flight; the loop is unrolled by 2 so the buffers never move (a loop-carried ring
-     * would make the compiler wait for every outstanding load at the loop head) */
-    GemvItem buf_a[D][R], buf_b[D][R];
-    const int tmax = max(nitems - 1, 0);
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-        gemv_load_item<R>(hole, plug, absmax, N, nch, steps, g0, nwaves, tmax, d, lane, buf_a[d]);
-
-    const int xplane = nch + 1;
-    for (int i = threadIdx.x; i < (K >> 3); i += THREADS) { /* i: 8 bf16 = a quarter chunk */
-        const glint_u32x4 v = x[i];
-        const int jj = i >> 2, q0 = (i & 3) * 2;
-        xs[q0 * xplane + jj] = glint_f32x4{glint_bf16lo(v.x), glint_bf16hi(v.x), glint_bf16lo(v.y), glint_bf16hi(v.y)};
-        xs[(q0 + 1) * xplane + jj] = glint_f32x4{glint_bf16lo(v.z), glint_bf16hi(v.z), glint_bf16lo(v.w), glint_bf16hi(v.w)};
-    }
-    if (threadIdx.x < 8)
-        xs[threadIdx.x * xplane + nch] = glint_f32x4{0.f, 0.f, 0.f, 0.f}; /* chunk nch: zeros */
-    glint_fill_cells_lds64(ltab, stage);
-
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-        acc[r] = 0.0f;
-
-    auto compute_item = [&](int t, const GemvItem (&item)[R]) {
-        const int step = t % steps;
-        const int jc = min(step * 64 + lane, nch);
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float part = 0.0f;
-            const uint32_t H[4] = {item[r].h.x, item[r].h.y, item[r].h.z, item[r].h.w};
-            const uint32_t P[4] = {item[r].p.x, item[r].p.y, item[r].p.z, item[r].p.w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const glint_f32x4 xa = xs[(2 * q) * xplane + jc];
-                const glint_f32x4 xb = xs[(2 * q + 1) * xplane + jc];
-                const uint32_t E = glint_codes_even(H[q], P[q]);
-                const uint32_t O = glint_codes_odd(H[q], P[q]);
-                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)), xa.x, part);
-                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)), xa.y, part);
-                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)), xa.z, part);
-                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)), xa.w, part);
-                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)), xb.x, part);
-                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)), xb.y, part);
-                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)), xb.z, part);
-                part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)), xb.w, part);
-                /* at most 8 lookups in flight per wave: bounds live registers */
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            const float a = jc < nch ? item[r].a : 0.0f;
-            if constexpr (!OUT_BF16) {
-                if (!(__builtin_fabsf(a) < 0x1p126f)) {
-                    /* rare: infinite, NaN or huge absmax take the f32 ABI's per-weight
-                     * products (cell * absmax, then the FMA), as the reference forms them */
-                    float pe = 0.0f;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const glint_f32x4 xa = xs[(2 * q) * xplane + jc];
-                        const glint_f32x4 xb = xs[(2 * q + 1) * xplane + jc];
-                        const uint32_t E = glint_codes_even(H[q], P[q]);
-                        const uint32_t O = glint_codes_odd(H[q], P[q]);
-                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)) * a, xa.x, pe);
-                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)) * a, xa.y, pe);
-                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)) * a, xa.z, pe);
-                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)) * a, xa.w, pe);
-                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)) * a, xb.x, pe);
-                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)) * a, xb.y, pe);
-                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)) * a, xb.z, pe);
-                        pe = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)) * a, xb.w, pe);
-                    }
-                    part = pe;
-                    acc[r] += part;
-                    continue;
-                }
-            }
-            acc[r] = fmaf(a, part, acc[r]);
-        }
-        if (step == steps - 1) { /* task done: reduce its rows and store */
-            const int n0 = (g0 + (t / steps) * nwaves) * R;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float sum = glint_wave_sum(acc[r]);
-                acc[r] = 0.0f;
-                if (lane == r && n0 + r < N) {
-                    if (OUT_BF16)
-                        ((uint16_t *)y)[n0 + r] = glint_f32_to_bf16(sum);
-                    else
-                        ((float *)y)[n0 + r] = sum;
-                }
-            }
-        }
-    };
-
-    /* full rounds: every compute is unconditional, so at the loop head the only loads in
-     * flight are the ones the next compute needs last (the wait counter can count them) */
-    int base = 0;
-    for (; base + 2 * D <= nitems; base += 2 * D) {
-        /* loads are unconditional (clamped): no branch hides them from the wait counter */
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-            gemv_load_item<R>(hole, plug, absmax, N, nch, steps, g0, nwaves, tmax, base + D + d, lane, buf_b[d]);
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-            compute_item(base + d, buf_a[d]);
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-            gemv_load_item<R>(hole, plug, absmax, N, nch, steps, g0, nwaves, tmax, base + 2 * D + d, lane, buf_a[d]);
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-            compute_item(base + D + d, buf_b[d]);
-    }
-    if (base < nitems) { /* fewer than 2 D items left; buf_a holds items base .. base + D - 1 */
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-            gemv_load_item<R>(hole, plug, absmax, N, nch, steps, g0, nwaves, tmax, base + D + d, lane, buf_b[d]);
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-            if (base + d < nitems)
-                compute_item(base + d, buf_a[d]);
-#pragma unroll
-        for (int d = 0; d < D; ++d)
-            if (base + D + d < nitems)
-                compute_item(base + D + d, buf_b[d]);
-    }
-}
-
 /* ------------------------------------------------ GEMV with x in registers */
-/* For K a multiple of 64 EL (EL = 32 or 16 elements per lane; every K of the decode shapes):
- * a row is cut into chunks of EL elements (EL/2 bytes of each plane, inside one absmax
- * block) and S = K / (64 EL) slices of 64 chunks. Wave (s, g) of a workgroup holds slice s
+/* For K a multiple of EL (EL = 32 elements per lane; every K with bs = 64): a row is cut
+ * into chunks of EL elements (EL/2 bytes of each plane, inside one absmax block) and
+ * S = ceil(K / (64 EL)) slices of 64 chunks, the last one partial where 64 EL does not
+ * divide K. Wave (s, g) of a workgroup holds slice s
  * of x in registers (lane l: the EL f32 of chunk 64 s + l) and runs rows r0 + g,
  * r0 + g + G, ... of the workgroup's row range; LDS then serves only the cell lookups. Per
  * row a wave loads 32 EL bytes of each plane plus its block scales, rows multi-buffered in
@@ -272,7 +77,8 @@ __global__ __launch_bounds__(THREADS, GEMV_WPE) void k_htile_gemv_b64(const glin
 #define GEMV_X_RED_MAX 4096 /* floats of per-row partials a workgroup may park in LDS */
 #define GEMV_X_S_MAX (GEMV_X_THREADS_WIDE / 64) /* most K slices: K <= 32768 at EL = 32 */
 /* dynamic LDS of k_htile_gemv_xreg: the row partials, or x as BF16 while it is staged */
-#define GEMV_X_LDS_MAX (GEMV_X_RED_MAX * 4 > GEMV_MAX_K * 2 ? GEMV_X_RED_MAX * 4 : GEMV_MAX_K * 2) /* x staged at G >= 2: S <= 8 */
+#define GEMV_X_STAGE_MAX_K 16384 /* x is staged in LDS at G >= 2, i.e. S <= 8 */
+#define GEMV_X_LDS_MAX (GEMV_X_RED_MAX * 4 > GEMV_X_STAGE_MAX_K * 2 ? GEMV_X_RED_MAX * 4 : GEMV_X_STAGE_MAX_K * 2)
 
 template <int EL> struct GemvVec;
 template <> struct GemvVec<32> { typedef glint_u32x4 T; };
@@ -362,8 +168,10 @@ __device__ __forceinline__ float gemv_exact_part(const float *ltab, const GemvRo
 /* XC > 0: x goes through LDS. Thread t loads 16-B chunks t + c blockDim.x (c < XC, with
  * XC blockDim.x >= K / 8; threads past the last chunk load it again and store nothing), the
  * G waves of a slice then read it from LDS instead of each loading it from L2. XC == 0:
- * each wave loads its slice itself (G == 1, no repeats). */
-template <int EL, bool OUT_BF16, int XC, int DEPTH, int MAXT>
+ * each wave loads its slice itself (G == 1, no repeats). PART: K % (64 EL) != 0, so the
+ * last slice holds fewer than 64 chunks; its idle lanes load the row's last chunk again
+ * and add nothing. */
+template <int EL, bool OUT_BF16, int XC, int DEPTH, int MAXT, bool PART>
 __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE))) void k_htile_gemv_xreg(
     const void *__restrict__ hole, const void *__restrict__ plug, const float *__restrict__ absmax,
     const glint_u32x4 *__restrict__ x, void *__restrict__ y, int N, int K, int G, int rows_per_wg) {
@@ -373,7 +181,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
 
     const int lane = threadIdx.x & 63;
     const uint32_t lane4 = (uint32_t)lane * 4u;
-    const int nch = K / EL, S = nch >> 6;
+    const int nch = K / EL, S = PART ? (nch + 63) >> 6 : nch >> 6;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = w % S, g = w / S;
     const int r0 = blockIdx.x * rows_per_wg;
@@ -382,6 +190,8 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
     /* row of item i, clamped into the matrix (a clamped reload is never used) */
     auto row_of = [&](int i) -> int64_t { return (int64_t)min(r0 + g + min(i, max(my - 1, 0)) * G, N - 1); };
     const uint32_t j = (uint32_t)(s * 64 + lane);
+    const bool act = !PART || j < (uint32_t)nch; /* lane holds a chunk of the row */
+    const uint32_t jl = act ? j : (uint32_t)nch - 1u;
 
     /* Loads go out in the order they are consumed (the wait counter is in order): the
      * cell table, x, then the first rows; the table's LDS writes follow. */
@@ -395,13 +205,13 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
     } else {
 #pragma unroll
         for (int q = 0; q < Q; ++q)
-            xv[q] = x[j * Q + q];
+            xv[q] = x[jl * Q + q];
     }
     __builtin_amdgcn_sched_barrier(0);
     GemvRow<EL> buf[DEPTH];
 #pragma unroll
     for (int d = 0; d < GEMV_X_PRE_OF(DEPTH); ++d)
-        gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, j, buf[d]);
+        gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, jl, buf[d]);
     __builtin_amdgcn_sched_barrier(0);
     glint_cells_fill_sstore(ltab, fill);
     if (XC > 0) {
@@ -414,7 +224,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
     if (XC > 0) {
 #pragma unroll
         for (int q = 0; q < Q; ++q)
-            xv[q] = ((const glint_u32x4 *)red)[j * Q + q];
+            xv[q] = ((const glint_u32x4 *)red)[jl * Q + q];
     }
     float xr[EL];
 #pragma unroll
@@ -429,7 +239,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
         __syncthreads(); /* x is read out before the row partials reuse its LDS */
 #pragma unroll
     for (int d = GEMV_X_PRE_OF(DEPTH); d < DEPTH; ++d)
-        gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, j, buf[d]);
+        gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, jl, buf[d]);
 
     auto compute_row = [&](int i, const GemvRow<EL> &row) {
         float part = 0.0f;
@@ -454,6 +264,8 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
         if constexpr (!OUT_BF16)
             if (!(__builtin_fabsf(row.a) < 0x1p126f)) /* rare: the f32 ABI's per-weight products */
                 sc = gemv_exact_part<EL>(ltab, row, lane4, xr);
+        if (PART && !act)
+            sc = 0.0f;
         const float v = glint_row16_sum(sc);
         if ((lane & 15) == 0)
             red[((g + i * G) * S + s) * 4 + (lane >> 4)] = v;
@@ -470,7 +282,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             compute_row(i + d, buf[d]);
-            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, j, buf[d]);
+            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, jl, buf[d]);
         }
     }
 #pragma unroll
@@ -478,7 +290,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
         if (i + d < my) {
             compute_row(i + d, buf[d]);
             if (i + d + DEPTH < my)
-                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, j, buf[d]);
+                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, jl, buf[d]);
         }
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
@@ -489,7 +301,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             compute_row(i + d, buf[d]);
-            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, j, buf[d]);
+            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, jl, buf[d]);
         }
     }
 #pragma unroll
@@ -796,17 +608,11 @@ __global__ __launch_bounds__(256) void k_htile_generic(const uint8_t *__restrict
 #endif
 
 /* ------------------------------------------------------------------ dispatch */
-/* One resident wave of workgroups (every CU filled to its occupancy limit), or fewer if
- * there are fewer wave tasks; the waves then loop over their tasks. */
-static unsigned gemv_grid(const void *kern, int threads, size_t lds, int64_t tasks) {
-    const int64_t resident = glint_resident_grid(kern, threads, lds);
-    const int64_t needed = (tasks + threads / 64 - 1) / (threads / 64);
-    return (unsigned)(needed < resident ? needed : resident);
-}
-
-/* k_htile_gemv_xreg over an M = 1 GEMV (bs 64, K % (64 EL) == 0, K / (64 EL) <= 8, aligned).
- * EL = 16 (8-B plane loads) for the K % 1024 == 0 shapes was timed slower than
- * k_htile_gemv_b64 (13824 x 5120: 24.8 against 19.4 us), so only EL = 32 is dispatched.
+/* k_htile_gemv_xreg over an M = 1 GEMV (bs 64, K % 64 == 0, K <= 64 EL GEMV_X_S_MAX, aligned).
+ * A partial last slice (K % 2048 != 0) replaced an x-in-LDS GEMV that ran those shapes at
+ * 45-49% of HBM: 13824 x 5120 19.5 -> 15.4 us, 5120 x 13824 20.7 -> 15.0, 5120 x 5120
+ * 11.6 -> 8.5, 8192 x 3072 9.8 -> 8.0. EL = 16 (8-B plane loads) was slower than both
+ * (13824 x 5120: 24.8 us).
  * Workgroups: up to GEMV_X_THREADS threads at S <= 2 (two per CU); at S > 2 about
  * GEMV_X_WIDE_TARGET threads and at least G = 2 row groups sharing one staged x, one
  * row in flight per wave. Against at most 512 threads (G = 1 at S >= 5, on half the
@@ -816,7 +622,8 @@ static unsigned gemv_grid(const void *kern, int threads, size_t lds, int64_t tas
 template <bool OUT_BF16, int EL = GEMV_X_EL>
 static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x,
                                   void *y, int N, int K, hipStream_t st) {
-    const int S = K / (64 * EL);
+    const int S = (K / EL + 63) / 64;
+    const bool part = (K % (64 * EL)) != 0;
     const int G = S <= 2 ? (GEMV_X_THREADS / 64) / S
                          : std::min(std::max(2, (GEMV_X_WIDE_TARGET / 64) / S), (GEMV_X_THREADS_WIDE / 64) / S);
     const int threads = 64 * S * G;
@@ -824,9 +631,13 @@ static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, cons
         return -3;
     /* x staging (G >= 2): K / 8 chunks of 16 B over 64 S G threads, XC chunks per thread;
      * S <= 2 (G >= 4): one chunk, one row in flight per wave; more slices: GEMV_X_DEPTH */
-    auto kern = S <= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 1, GEMV_X_DEPTH_S2, GEMV_X_THREADS>
-                       : (G >= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 2, GEMV_X_DEPTH, GEMV_X_THREADS_WIDE>
-                                 : k_htile_gemv_xreg<EL, OUT_BF16, 0, GEMV_X_DEPTH_G1, GEMV_X_THREADS_WIDE>);
+    auto pick = [&](auto part_c) {
+        constexpr bool P = decltype(part_c)::value;
+        return S <= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 1, GEMV_X_DEPTH_S2, GEMV_X_THREADS, P>
+                      : (G >= 2 ? k_htile_gemv_xreg<EL, OUT_BF16, 2, GEMV_X_DEPTH, GEMV_X_THREADS_WIDE, P>
+                                : k_htile_gemv_xreg<EL, OUT_BF16, 0, GEMV_X_DEPTH_G1, GEMV_X_THREADS_WIDE, P>);
+    };
+    auto kern = part ? pick(std::true_type{}) : pick(std::false_type{});
     const size_t lds_max = G >= 2 ? std::max<size_t>(GEMV_X_RED_MAX * 4, (size_t)K * 2) : GEMV_X_RED_MAX * 4;
     int64_t resident = std::max<int64_t>(glint_resident_grid((const void *)kern, threads, lds_max), 1);
     if (G == 1 && resident / GEMV_G1_DIV >= glint_cu_count())
@@ -839,7 +650,7 @@ static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, cons
     const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
     size_t lds = (size_t)rows_per_wg * S * 4 * sizeof(float);
     if (G >= 2 && lds < (size_t)K * 2)
-        lds = (size_t)K * 2; /* x staging: K <= GEMV_MAX_K, within GEMV_X_LDS_MAX bytes */
+        lds = (size_t)K * 2; /* x staging: K <= GEMV_X_STAGE_MAX_K, within GEMV_X_LDS_MAX bytes */
     if (glint_set_lds_limit((const void *)kern, GEMV_X_LDS_MAX) != 0)
         return -3;
     kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const glint_u32x4 *)x, y, N, K, G, (int)rows_per_wg);
@@ -866,11 +677,10 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         return 0;
     const bool fast_ok = bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
                          glint_aligned(absmax, 4) && glint_aligned(x, 16);
-    /* M = 1: the x-register GEMV (K % 2048 == 0, K <= 32768), else the x-in-LDS GEMV
-     * (K <= 16384), else the tiles; M > 1: the small-M GEMV or the tiles */
-    const bool gemv_x_ok = M == 1 && fast_ok && (K % (64 * GEMV_X_EL)) == 0 && K / (64 * GEMV_X_EL) <= GEMV_X_S_MAX;
-    const bool gemv_ok = M == 1 && fast_ok && !gemv_x_ok && K <= GEMV_MAX_K;
-    const bool mfma_ok = fast_ok && !gemv_x_ok && !gemv_ok;
+    /* M = 1: the x-register GEMV (K <= 32768), else the tiles; M > 1: the small-M GEMV or
+     * the tiles */
+    const bool gemv_x_ok = M == 1 && fast_ok && (K / GEMV_X_EL + 63) / 64 <= GEMV_X_S_MAX;
+    const bool mfma_ok = fast_ok && !gemv_x_ok;
     if (mfma_ok && M > 1 && M <= (OUT_BF16 ? GEMV_MR_MAX : GEMV_MR_MAX_F32) && (K % 2048) == 0 &&
         K / 2048 <= GEMV_X_THREADS / 64)
         return htile_launch_gemv_mr<!OUT_BF16>(hole, plug, absmax, x, y, M, N, K, st);
@@ -905,27 +715,6 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
                 : tile_mfma_launch<128, 128, 2, 4, 2, GlintTileProducer, TileOutF32, 3>(p, xb, yf, M, N, K, st, fixed);
         if (!planned)
             return -5;
-    } else if (gemv_ok) {
-        constexpr int R = GEMV_R, D = GEMV_D;
-        const size_t lds = GEMV_LDS_BYTES(K);
-        const int64_t tasks = ((int64_t)N + R - 1) / R;
-        if (K <= 8192) {
-            constexpr int T = GEMV_T;
-            auto kern = k_htile_gemv_b64<R, D, T, OUT_BF16>;
-            if (glint_set_lds_limit((const void *)kern, lds) != 0)
-                return -3;
-            const unsigned grid = gemv_grid((const void *)kern, T, lds, tasks);
-            kern<<<grid, T, lds, st>>>((const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax,
-                                      (const glint_u32x4 *)x, y, N, K);
-        } else {
-            constexpr int T = 1024;
-            auto kern = k_htile_gemv_b64<R, D, T, OUT_BF16>;
-            if (glint_set_lds_limit((const void *)kern, lds) != 0)
-                return -3;
-            const unsigned grid = gemv_grid((const void *)kern, T, lds, tasks);
-            kern<<<grid, T, lds, st>>>((const glint_u32x4 *)hole, (const glint_u32x4 *)plug, absmax,
-                                      (const glint_u32x4 *)x, y, N, K);
-        }
     } else {
         dim3 grid((N + GT_N - 1) / GT_N, (M + GT_M - 1) / GT_M);
         k_htile_generic<OUT_BF16><<<grid, 256, 0, st>>>(hole, plug, absmax, (const uint16_t *)x, y, M, N, K, bs);

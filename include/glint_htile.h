@@ -16,9 +16,8 @@ struct ihipStream_t;
 /* f32 output, f32 products and f32 sums (within 1e-5 * (1 + |ref|) of a float64 reference).
  * At M > 1 with blocksize 64, K % 64 == 0 and aligned pointers the products run on BF16
  * MFMA with each f32 weight split exactly into three BF16 planes (the sum differs from a
- * sequential f32 sum only in order); M = 1 is the f32 GEMV (K % 2048 == 0 up to
- * K = 32768, other K % 64 == 0 up to 16384; larger K takes the MFMA route), other shapes
- * a generic kernel. Enqueued on `stream`; y is overwritten. Returns 0, -1 for a null pointer,
+ * sequential f32 sum only in order); M = 1 is the f32 GEMV (K <= 32768; larger K takes
+ * the MFMA route), other shapes a generic kernel. Enqueued on `stream`; y is overwritten. Returns 0, -1 for a null pointer,
  * -2 for blocksize <= 0 (or K < 1), -3 for a launch error. The MFMA route uses the
  * stream's split-K workspace as launch_glint_htile_bf16_stream does.
  * Reference: include/glint_htile.h:11-14 (cuda/glint_htile.cu:165-180). */

@@ -85,7 +85,8 @@ def _encoded_weight(oracle, N, K, seed, bs=64):
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336), (100, 64), (3, 1088), (129, 2048), (1, 2048),
                                  (7, 6144), (1000, 12288), (17, 16384), (4097, 8192), (2000, 10240),
                                  (8, 18432), (100, 28672), (33, 32768),
-                                 (13824, 5120), (5, 1024), (300, 3072), (77, 7168)])
+                                 (13824, 5120), (5120, 13824), (5, 1024), (300, 3072), (77, 7168),
+                                 (300, 20544), (64, 30784)])
 def test_gemv_fast_path_vs_float64(oracle, N, K):
     torch = torch_cuda()
     hole, plug, am = _encoded_weight(oracle, N, K, 2002)
@@ -102,11 +103,11 @@ def test_gemv_fast_path_vs_float64(oracle, N, K):
     assert (np.abs(yb64 - ref) <= np.abs(ref) * 2.0 ** -8 + bound * 1.01).all()
 
 
-@pytest.mark.parametrize("N,K", [(300, 20544), (64, 34816)])
+@pytest.mark.parametrize("N,K", [(300, 32832), (64, 34816)])
 def test_m1_beyond_gemv_range(oracle, N, K):
-    """M = 1 past both GEMVs' K range (K % 2048 != 0 above 16384, or K above 32768) runs
-    on the MFMA tiles: f32 out within the f32 sum bound and the reference's 1e-5 gate,
-    BF16 out within 1e-2 relative Frobenius error of the float64 product."""
+    """M = 1 past the GEMV's K range (K above 32768) runs on the MFMA tiles: f32 out within
+    the f32 sum bound and the reference's 1e-5 gate, BF16 out within 1e-2 relative
+    Frobenius error of the float64 product."""
     torch = torch_cuda()
     hole, plug, am = _encoded_weight(oracle, N, K, 2302)
     g = torch.Generator(device="cuda").manual_seed(2301)
@@ -340,9 +341,9 @@ def test_small_m_f32_gemv_vs_float64(oracle, M, N, K):
 
 @pytest.mark.parametrize("M,K", [(1, 2048), (1, 4096), (1, 1088), (1, 3072), (1, 14336), (1, 28672), (2, 2048), (4, 4096)])
 def test_f32_gemv_special_absmax(oracle, M, K):
-    """The f32-out GEMVs (M = 1: x in registers at K % 2048 == 0, in 512-thread workgroups
-    up to K = 4096 and wider ones above; x in LDS at K = 1088 and 3072; and the small-M
-    form) on blocks with an infinite or NaN absmax,
+    """The f32-out GEMVs (M = 1: in 512-thread workgroups up to K = 4096 and wider ones
+    above, with a partial last K slice at K = 1088 and 3072; and the small-M form) on
+    blocks with an infinite or NaN absmax,
     one whose CELLS * absmax overflows f32 and one at 2^126: such a block takes the
     reference's per-weight products (cell * absmax, then the FMA with x), so NaN and +-inf
     land exactly where the f32 restatement puts them; the finite outputs agree within the
