@@ -340,8 +340,8 @@ typedef __bf16 glint_bf16x2_t __attribute__((ext_vector_type(2)));
  * x held as f32 (MR x 32 registers) and one f32 FMA per weight and row in k order, the
  * weights the exact f32 cells; the same arithmetic per row as the M = 1 f32 GEMV, so the
  * same (K + 2) 2^-23 sum |w x| bound. */
-template <int MR, bool F32>
-__global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__restrict__ hole,
+template <int MR, bool F32, bool PART, int MAXT>
+__global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__ hole,
                                                                   const void *__restrict__ plug,
                                                                   const float *__restrict__ absmax,
                                                                   const uint16_t *__restrict__ x,
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__
     constexpr int EL = 32, Q = EL / 8;
     const int lane = threadIdx.x & 63;
     const uint32_t lane4 = (uint32_t)lane * 4u;
-    const int nch = K / EL, S = nch >> 6;
+    const int nch = K / EL, S = PART ? (nch + 63) >> 6 : nch >> 6;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = w % S, g = w / S;
     const int r0 = blockIdx.x * rows_per_wg;
@@ -360,6 +360,8 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__
     const int my = g < nrows ? (nrows - g + G - 1) / G : 0;
     auto row_of = [&](int i) -> int64_t { return (int64_t)min(r0 + g + min(i, max(my - 1, 0)) * G, N - 1); };
     const uint32_t j = (uint32_t)(s * 64 + lane);
+    const bool act = !PART || j < (uint32_t)nch; /* PART: idle lanes of the last slice */
+    const uint32_t jl = act ? j : (uint32_t)nch - 1u;
 
     GlintCellFillS fill;
     glint_cells_fill_sload(fill);
@@ -367,15 +369,15 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__
     glint_u32x4 xv[MR][4];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-        const glint_u32x4 *xr = (const glint_u32x4 *)(x + (int64_t)min(m, M - 1) * K) + (size_t)j * 4;
+        const glint_u32x4 *xr = (const glint_u32x4 *)(x + (int64_t)min(m, M - 1) * K) + (size_t)jl * 4;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
             xv[m][c] = xr[c];
     }
     __builtin_amdgcn_sched_barrier(0);
     GemvRow<EL> buf[2];
-    gemv_x_load<EL>(hole, plug, absmax, row_of(0), nch, j, buf[0]);
-    gemv_x_load<EL>(hole, plug, absmax, row_of(1), nch, j, buf[1]);
+    gemv_x_load<EL>(hole, plug, absmax, row_of(0), nch, jl, buf[0]);
+    gemv_x_load<EL>(hole, plug, absmax, row_of(1), nch, jl, buf[1]);
     __builtin_amdgcn_sched_barrier(0);
     glint_cells_fill_sstore(ltab, fill);
     __syncthreads();
@@ -446,6 +448,8 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__
                     sc[m] = gemv_exact_part<EL>(ltab, row, lane4, xf[m]);
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
+            if (PART && !act)
+                sc[m] = 0.0f;
             const float v = glint_row16_sum(sc[m]);
             if ((lane & 15) == 0)
                 red[((t * S + s) * 4 + (lane >> 4)) * MR + m] = v;
@@ -454,15 +458,15 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__
     int i = 0;
     for (; i + 4 <= my; i += 2) {
         compute_row(i, buf[0]);
-        gemv_x_load<EL>(hole, plug, absmax, row_of(i + 2), nch, j, buf[0]);
+        gemv_x_load<EL>(hole, plug, absmax, row_of(i + 2), nch, jl, buf[0]);
         compute_row(i + 1, buf[1]);
-        gemv_x_load<EL>(hole, plug, absmax, row_of(i + 3), nch, j, buf[1]);
+        gemv_x_load<EL>(hole, plug, absmax, row_of(i + 3), nch, jl, buf[1]);
     }
     for (int d = 0; d < 2; ++d)
         if (i + d < my) {
             compute_row(i + d, buf[d]);
             if (i + d + 2 < my)
-                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + 2), nch, j, buf[d]);
+                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + 2), nch, jl, buf[d]);
         }
     for (int d = 0; d < 2; ++d)
         if (i + 2 + d < my)
@@ -483,30 +487,78 @@ __global__ __launch_bounds__(GEMV_X_THREADS) void k_htile_gemv_mr(const void *__
     }
 }
 
+#ifndef GEMV_MR_ON
+#define GEMV_MR_ON 1
+#endif
 #ifndef GEMV_MR_MAX
 #define GEMV_MR_MAX 8 /* largest M the small-M GEMV takes (templates for 2, 4 and 8 rows) */
 #endif
-/* k_htile_gemv_mr over 2 <= M <= GEMV_MR_MAX (bs 64, K % 2048 == 0, K / 2048 <= 8, aligned);
- * the f32-out form up to GEMV_MR_MAX_F32 rows.
+/* k_htile_gemv_mr over 2 <= M <= GEMV_MR_MAX (bs 64, K % 64 == 0, aligned; K <= 16384, and
+ * up to 32768 where x fits the wide workgroups), the f32-out form up to GEMV_MR_MAX_F32 rows.
  * Measured against the 64-row MFMA tile (k_tile_ss) on 14336 x 4096: M = 2 14.2-15.6 us
  * against 35.0, M = 4 17.8-18.2 against 35.3, M = 5..8 24.7-24.9 against 34.3-34.6 (the
  * 8-row template holds 128 VGPRs of x and runs at 2 waves per SIMD). */
 #ifndef GEMV_MR_MAX_F32
 #define GEMV_MR_MAX_F32 4 /* largest M of the f32-out small-M GEMV (x as f32: MR x 32 registers) */
 #endif
+#ifndef GEMV_MR_WIDE
+#define GEMV_MR_WIDE 1 /* S > 2: the M = 1 kernel's wider workgroups where x fits (see gemv_mr_wide_ok) */
+#endif
+/* rows of x per template for M rows */
+static inline int gemv_mr_rows(int M, bool f32) { return M <= 2 ? 2 : (M <= 4 || f32 ? 4 : 8); }
+/* Wider workgroups (up to 1024 threads: at most 128 VGPRs) only for BF16 out with up to
+ * 4 rows (x as 64 registers of BF16 words, 114 VGPRs); the f32 form of even 2 rows
+ * (x as 64 f32, 140 VGPRs) would spill. */
+static inline bool gemv_mr_wide_ok(int MR, bool f32) { return GEMV_MR_WIDE && !f32 && MR <= 4; }
+/* Workgroups over S slices: up to GEMV_X_THREADS threads (G = 8 / S row groups, S <= 8),
+ * or the M = 1 kernel's wider ones where those hold fewer than 7 waves (S = 3, 5, 6) or
+ * cannot hold S (S > 8). Measured (wide against narrow, M = 2 / 4): 4096 x 6144 8.3 / 11.0
+ * against 9.2 / 11.6 us, 4096 x 12288 12.6 / 15.7 against 13.5 / 17.6; narrow better at
+ * S = 4 (8192 x 8192 14.9 / 18.5 against 15.8 / 19.3) and S = 7 (4096 x 14336). */
+static inline bool gemv_mr_is_wide(int S, int MR, bool f32) {
+    return gemv_mr_wide_ok(MR, f32) && S > 2 && (S > 8 || S * ((GEMV_X_THREADS / 64) / S) < 7);
+}
+/* row groups per workgroup, 0 where the template cannot take S */
+static inline int gemv_mr_groups(int S, int MR, bool f32) {
+    if (!gemv_mr_is_wide(S, MR, f32))
+        return S <= 8 ? (GEMV_X_THREADS / 64) / S : 0;
+    return std::min(std::max(2, (GEMV_X_WIDE_TARGET / 64) / S), (GEMV_X_THREADS_WIDE / 64) / S);
+}
+/* whether k_htile_gemv_mr takes M rows at this K (bs 64, K % 64 == 0). The 8-row template is
+ * VALU-bound at 2 waves per SIMD; with a partial last slice it was slower than the tiles
+ * (13824 x 5120: 63.9 against 42.3 us), so it takes only K % 2048 == 0. */
+static inline bool gemv_mr_takes(int M, int K, bool f32) {
+    const int S = (K / 2048) + (K % 2048 != 0), MR = gemv_mr_rows(M, f32);
+    if (M < 2 || M > (f32 ? GEMV_MR_MAX_F32 : GEMV_MR_MAX) || S > GEMV_X_S_MAX)
+        return false;
+    if (MR == 8 && (K % 2048) != 0)
+        return false;
+    return gemv_mr_groups(S, MR, f32) >= 1;
+}
 template <bool F32>
 static int htile_launch_gemv_mr(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y,
                                 int M, int N, int K, hipStream_t st) {
-    const int S = K / 2048, G = (GEMV_X_THREADS / 64) / S, threads = 64 * S * G;
-    decltype(&k_htile_gemv_mr<2, F32>) kern;
-    int MR;
-    if constexpr (F32) { /* no 8-row f32 form: 256 registers of x */
-        kern = M <= 2 ? k_htile_gemv_mr<2, true> : k_htile_gemv_mr<4, true>;
-        MR = M <= 2 ? 2 : 4;
-    } else {
-        kern = M <= 2 ? k_htile_gemv_mr<2, false> : (M <= 4 ? k_htile_gemv_mr<4, false> : k_htile_gemv_mr<8, false>);
-        MR = M <= 2 ? 2 : (M <= 4 ? 4 : 8);
-    }
+    if (!gemv_mr_takes(M, K, F32))
+        return -3;
+    const int S = (K / 2048) + (K % 2048 != 0), MR = gemv_mr_rows(M, F32), G = gemv_mr_groups(S, MR, F32);
+    const int threads = 64 * S * G;
+    const bool part = (K % 2048) != 0, wide = gemv_mr_is_wide(S, MR, F32);
+    auto pick = [&](auto mr_c) {
+        constexpr int R = decltype(mr_c)::value;
+        constexpr bool W = !F32 && R <= 4; /* wide templates only where x fits (gemv_mr_wide_ok) */
+        constexpr int TW = W ? GEMV_X_THREADS_WIDE : GEMV_X_THREADS;
+        return part ? (wide ? k_htile_gemv_mr<R, F32, true, TW> : k_htile_gemv_mr<R, F32, true, GEMV_X_THREADS>)
+                    : (wide ? k_htile_gemv_mr<R, F32, false, TW> : k_htile_gemv_mr<R, F32, false, GEMV_X_THREADS>);
+    };
+    decltype(&k_htile_gemv_mr<2, F32, false, GEMV_X_THREADS>) kern;
+    if (MR == 2)
+        kern = pick(std::integral_constant<int, 2>{});
+    else if (MR == 4)
+        kern = pick(std::integral_constant<int, 4>{});
+    else if constexpr (!F32) /* no 8-row f32 form: 256 registers of x */
+        kern = pick(std::integral_constant<int, 8>{});
+    else
+        return -3;
     /* the whole resident grid: halving it where a workgroup holds one row group, as the M = 1
      * kernel does, was slower here (4096 x 14336 f32 out at M = 4: 30.1 against 18.6 us) */
     const int64_t resident =
@@ -516,6 +568,8 @@ static int htile_launch_gemv_mr(const uint8_t *hole, const uint8_t *plug, const 
     const int64_t cap = (GEMV_X_RED_MAX / (S * 4 * MR)) / G * G;
     if (rows_per_wg > cap)
         rows_per_wg = cap;
+    if (rows_per_wg < 1)
+        return -3;
     const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
     const size_t lds = (size_t)rows_per_wg * S * 4 * MR * sizeof(float);
     if (glint_set_lds_limit((const void *)kern, GEMV_X_RED_MAX * 4) != 0)
@@ -681,8 +735,7 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
      * the tiles */
     const bool gemv_x_ok = M == 1 && fast_ok && (K / GEMV_X_EL + 63) / 64 <= GEMV_X_S_MAX;
     const bool mfma_ok = fast_ok && !gemv_x_ok;
-    if (mfma_ok && M > 1 && M <= (OUT_BF16 ? GEMV_MR_MAX : GEMV_MR_MAX_F32) && (K % 2048) == 0 &&
-        K / 2048 <= GEMV_X_THREADS / 64)
+    if (mfma_ok && GEMV_MR_ON && gemv_mr_takes(M, K, !OUT_BF16))
         return htile_launch_gemv_mr<!OUT_BF16>(hole, plug, absmax, x, y, M, N, K, st);
     if (gemv_x_ok)
         return htile_launch_gemv_xreg<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);

@@ -137,7 +137,9 @@ def test_bf16_path_rel_frobenius(oracle, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(2, 14336, 4096), (3, 4096, 14336), (4, 129, 2048), (5, 1000, 12288),
-                                   (8, 17, 16384), (6, 4097, 8192), (7, 7, 6144), (8, 3000, 6144)])
+                                   (8, 17, 16384), (6, 4097, 8192), (7, 7, 6144), (8, 3000, 6144),
+                                   (2, 3000, 6144), (4, 300, 12288), (3, 1000, 5120), (4, 200, 13824),
+                                   (2, 100, 18432), (4, 300, 28672), (3, 33, 30784), (2, 50, 1088)])
 def test_small_m_gemv_vs_float64(oracle, M, N, K):
     """2 <= M <= 8 (batched decode) on the small-M GEMV: every weight looked up once for all
     M rows, its cell rounded to BF16 and multiplied into each row by v_dot2_f32_bf16, the
@@ -320,7 +322,7 @@ def test_f32_prefill_mfma_special_absmax(oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(2, 14336, 4096), (3, 4096, 14336), (4, 1000, 2048), (4, 17, 16384),
-                                   (2, 4097, 8192)])
+                                   (2, 4097, 8192), (2, 300, 5120), (4, 100, 13824), (3, 64, 3072)])
 def test_small_m_f32_gemv_vs_float64(oracle, M, N, K):
     """The f32-out ABI at 2 <= M <= 4 (K % 2048 == 0) on the small-M GEMV: exact f32 cells,
     one FMA per weight and row. Every output within the f32 summation bound
