@@ -8,7 +8,7 @@
  *   K is split across workgroups (fixed-order reduction) when the tiles leave CUs idle.
  *   Tiles: 256 x 128 over 8 waves for m >= 256 (k_tile_mfma), 128 x 64 for m > 64 and
  *   64 x 64 below (k_tile_ss: weight loads cover whole 128-B lines).
- * k_i8tile_gemv<MR> — m <= 4, k_in % 2048 == 0: the GEMV-shaped kernel, f32 FMAs.
+ * k_i8tile_gemv<MR> — m <= 4, k_in % 2048 == 0: the GEMV-shaped kernel, v_dot2_f32_bf16.
  * k_i8tile_generic — any k_in and alignment: 64 (n) x 32 (m) output tiles, weights
  *   dequantized to BF16 and widened to f32 in LDS per 32-wide K step, f32 FMAs in k order.
  *   A row's scale index is the flat (n * k_in + k) / 64, so a K step may span two blocks.
@@ -93,7 +93,12 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
  * activation rows in registers (32 f32 per lane per row) and streams weight rows
  * r0 + g, r0 + g + G, ... of its workgroup's row range: per row each lane reads 32 int8
  * (two 16-B loads, one 64-block, so one scale). Weights are rounded to BF16 exactly as the
- * tile kernels do (v_cvt_pk_bf16_f32 of q * scale); products accumulate with f32 FMAs.
+ * tile kernels do (v_cvt_pk_bf16_f32 of q * scale); each BF16 weight pair meets the BF16 x
+ * pair in one v_dot2_f32_bf16 (both products exact in f32, added into the f32 partial).
+ * Against unpacking the pair and two f32 FMAs, with the grid capped at 16 waves per CU
+ * (the dot form needs fewer registers, so more workgroups would fit): 14336 x 4096 m = 1
+ * 14.5 -> 14.1 us, m = 4 22.6 -> 19.4; 4096 x 14336 m = 1 15.6 -> 13.4, m = 4 25.2 -> 20.7;
+ * 8192 x 8192 m = 1 18.4 -> 16.0. Without the cap m = 2 was slower (16.1 -> 17.1).
  * Two rows are in flight per wave (four at m = 1, k_in <= 4096); loads are unconditional
  * (rows clamped at the end).
  * A row's S slice sums (DPP within the wave) meet in LDS and are added in slice order. */
@@ -107,6 +112,9 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
 #define I8V_DEPTH_M1 4
 #endif
 #define I8V_RED_MAX 8192 /* floats of row partials a workgroup may park in LDS */
+#ifndef I8V_WAVES_CU
+#define I8V_WAVES_CU 16 /* most waves per CU the grid is sized for (4 per SIMD) */
+#endif
 #ifndef I8V_GRID_DIV
 #define I8V_GRID_DIV 2 /* m = 1, one row group per workgroup (k_in >= 10240): launch the resident grid / this */
 #endif
@@ -115,6 +123,10 @@ struct I8Row {
     glint_u32x4 q0, q1;
     float s;
 };
+#ifndef I8V_DOT2
+#define I8V_DOT2 1 /* products of the BF16 weight pair and the BF16 x pair by v_dot2_f32_bf16 */
+#endif
+typedef __bf16 i8v_bf16x2_t __attribute__((ext_vector_type(2)));
 
 template <int MR, int DEPTH>
 __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *__restrict__ q,
@@ -138,8 +150,9 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
         r.q1 = __builtin_nontemporal_load(&q[n * kv + j + 1]);
         r.s = scale[n * (K >> 6) + (j >> 2)];
     };
-    /* x: this lane's 32 activations of each of the MR rows, as f32 */
-    float xr[MR][32];
+    /* x: this lane's 32 activations of each of the MR rows: as BF16 pairs (I8V_DOT2) or f32 */
+    uint32_t xw[MR][16];
+    float xr[I8V_DOT2 ? 1 : MR][I8V_DOT2 ? 1 : 32];
 #pragma unroll
     for (int mr = 0; mr < MR; ++mr)
 #pragma unroll
@@ -148,8 +161,11 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
             const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                xr[mr][8 * h + 2 * e] = glint_bf16lo(d[e]);
-                xr[mr][8 * h + 2 * e + 1] = glint_bf16hi(d[e]);
+                xw[mr][4 * h + e] = d[e];
+                if constexpr (!I8V_DOT2) {
+                    xr[mr][8 * h + 2 * e] = glint_bf16lo(d[e]);
+                    xr[mr][8 * h + 2 * e + 1] = glint_bf16hi(d[e]);
+                }
             }
         }
     I8Row buf[DEPTH];
@@ -170,11 +186,20 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
                     float lo, hi;
                     weights(W[e], b, lo, hi);
                     const uint32_t pk = glint_cvt_bf16x2(lo, hi);
-                    const float wl = glint_bf16lo(pk), wh = glint_bf16hi(pk);
+                    if constexpr (I8V_DOT2) {
+                        /* both BF16 products are exact in f32; one instruction adds them */
 #pragma unroll
-                    for (int mr = 0; mr < MR; ++mr) {
-                        part[mr] = fmaf(wl, xr[mr][4 * e + 2 * b], part[mr]);
-                        part[mr] = fmaf(wh, xr[mr][4 * e + 2 * b + 1], part[mr]);
+                        for (int mr = 0; mr < MR; ++mr)
+                            part[mr] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(i8v_bf16x2_t, pk),
+                                                                       __builtin_bit_cast(i8v_bf16x2_t, xw[mr][2 * e + b]),
+                                                                       part[mr], false);
+                    } else {
+                        const float wl = glint_bf16lo(pk), wh = glint_bf16hi(pk);
+#pragma unroll
+                        for (int mr = 0; mr < MR; ++mr) {
+                            part[mr] = fmaf(wl, xr[mr][4 * e + 2 * b], part[mr]);
+                            part[mr] = fmaf(wh, xr[mr][4 * e + 2 * b + 1], part[mr]);
+                        }
                     }
                 }
         };
@@ -237,8 +262,9 @@ static void i8tile_launch_gemv(const uint16_t *x, const Int8PinLinear &w, float 
      * 4096 x 14336; at k_in = 4096 or m = 4 it was slower, and k_in = 6144 / 8192 (G = 2)
      * were not measured, so they keep the full grid */
     const int div = (MR == 1 && G == 1) ? I8V_GRID_DIV : 1;
-    const int64_t resident =
-        std::max<int64_t>(glint_resident_grid((const void *)kern, threads, I8V_RED_MAX * 4) / div, 1);
+    int64_t resident = glint_resident_grid((const void *)kern, threads, I8V_RED_MAX * 4);
+    resident = std::min<int64_t>(resident, (int64_t)glint_cu_count() * std::max(I8V_WAVES_CU / (threads / 64), 1));
+    resident = std::max<int64_t>(resident / div, 1);
     const int64_t per_wave = ((int64_t)w.n_out + G * resident - 1) / (G * resident);
     int64_t rows_per_wg = G * per_wave;
     const int64_t cap = (I8V_RED_MAX / (S * MR)) / G * G;
