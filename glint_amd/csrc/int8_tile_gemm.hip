@@ -99,17 +99,20 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
  * (the dot form needs fewer registers, so more workgroups would fit): 14336 x 4096 m = 1
  * 14.5 -> 14.1 us, m = 4 22.6 -> 19.4; 4096 x 14336 m = 1 15.6 -> 13.4, m = 4 25.2 -> 20.7;
  * 8192 x 8192 m = 1 18.4 -> 16.0. Without the cap m = 2 was slower (16.1 -> 17.1).
- * Two rows are in flight per wave (four at m = 1, k_in <= 4096); loads are unconditional
- * (rows clamped at the end).
+ * Two rows are in flight per wave (one at m = 2); loads are unconditional (rows clamped at
+ * the end).
  * A row's S slice sums (DPP within the wave) meet in LDS and are added in slice order. */
 #ifndef I8V_THREADS
 #define I8V_THREADS 512
 #endif
 #ifndef I8V_DEPTH
-#define I8V_DEPTH 2 /* rows of loads in flight per wave (I8V_DEPTH_M1 for m = 1, k_in <= 4096) */
+#define I8V_DEPTH 2 /* rows of loads in flight per wave (I8V_DEPTH_M1 for m = 1, k_in <= 4096; I8V_DEPTH_M2 at m = 2) */
 #endif
 #ifndef I8V_DEPTH_M1
-#define I8V_DEPTH_M1 4
+#define I8V_DEPTH_M1 2
+#endif
+#ifndef I8V_DEPTH_M2
+#define I8V_DEPTH_M2 1 /* rows in flight at m = 2 */
 #endif
 #define I8V_RED_MAX 8192 /* floats of row partials a workgroup may park in LDS */
 #ifndef I8V_WAVES_CU
@@ -254,9 +257,12 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
 template <int MR>
 static void i8tile_launch_gemv(const uint16_t *x, const Int8PinLinear &w, float *y, hipStream_t st) {
     const int S = w.k_in / 2048, G = (I8V_THREADS / 64) / S, threads = 64 * S * G;
-    /* 4 rows in flight measured 14% faster at m = 1, k_in = 4096 (14.6 against 17.0 us on
-     * 14336 x 4096) and 2-5% slower at k_in = 14336 or m = 4 */
-    auto kern = (MR == 1 && S <= 2) ? k_i8tile_gemv<MR, I8V_DEPTH_M1> : k_i8tile_gemv<MR, I8V_DEPTH>;
+    /* rows in flight (with the dot form and the 16-wave cap): m = 1 at k_in <= 4096 two
+     * (14336 x 4096: 13.6 us, four 14.0, three 14.3); m = 2 one (14336 x 4096 15.4 against
+     * 15.6, 4096 x 14336 16.4 against 16.9, 8192 x 8192 17.3 against 17.9); otherwise two
+     * (one was 8-35% slower at m = 1, k_in > 4096 and at m = 4, three 1-7% slower) */
+    auto kern = (MR == 1 && S <= 2) ? k_i8tile_gemv<MR, I8V_DEPTH_M1>
+                                    : (MR == 2 ? k_i8tile_gemv<MR, I8V_DEPTH_M2> : k_i8tile_gemv<MR, I8V_DEPTH>);
     /* m = 1 with one row group per workgroup (G == 1: S = k_in / 2048 >= 5, k_in >= 10240):
      * half the resident grid (twice the rows per wave) measured 16.5 -> 15.4 us on
      * 4096 x 14336; at k_in = 4096 or m = 4 it was slower, and k_in = 6144 / 8192 (G = 2)
