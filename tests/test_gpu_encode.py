@@ -110,6 +110,31 @@ def test_ragged_sizes_blocksizes_alignment(oracle, bs, pad):
         assert_same(gpu_encode(u16, bs, pad), oracle.encode_bf16(u16, bs), f"n={n} bs={bs} pad={pad}")
 
 
+def test_encode_in_pieces(oracle):
+    """A tensor above 2^17 wave chunks (67 M elements) is encoded as equal consecutive
+    launches: n = 2 * 2^17 * 512 + 5 * 512 + 100 gives three pieces of 87383 chunks and a
+    100-element tail for the generic kernels. The bytes around every piece boundary and the
+    tail match the oracle, and every absmax equals the block's largest magnitude."""
+    torch = torch_cuda()
+    n = 2 * (1 << 17) * 512 + 5 * 512 + 100
+    print(f"encode in pieces n={n}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(515)
+    w = (torch.randn(n, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    hole, plug, am = H.encode_bf16(w, 64)
+    nch = (n // 512)
+    per = (nch + 2) // 3
+    edges = [0, per * 512, 2 * per * 512, (n // 512) * 512, n]
+    for e in edges:
+        lo, hi = max(0, (e - 4096) // 64 * 64), min(n, e + 4096)
+        u16 = host(w[lo:hi].view(torch.int16), np.uint16)
+        want = oracle.encode_bf16(u16, 64)
+        got = (host(hole[lo // 2:(hi + 1) // 2]), host(plug[lo // 2:(hi + 1) // 2]), host(am[lo // 64:(hi + 63) // 64]))
+        assert_same(got, want, f"edge {e}")
+    full = n // 64 * 64
+    amx = w[:full].float().abs().reshape(-1, 64).amax(dim=1)
+    assert bool(torch.equal(amx, am[:full // 64])), "absmax"
+
+
 def test_special_blocks(oracle):
     blocks = []
     z = np.zeros(64, np.float32)
