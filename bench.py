@@ -693,6 +693,15 @@ COUNTER_PASSES = {
 }
 
 
+ENCODE_PIECE_CHUNKS = 1 << 17  # the library's most 512-element chunks per encode launch
+
+
+def encode_launches(n: int) -> int:
+    """k_encode_bf16_b64 dispatches of one BF16 bs-64 encode of n elements (n % 512 == 0):
+    the library launches tensors above ENCODE_PIECE_CHUNKS chunks in equal pieces."""
+    return max(1, -(-(n // 512) // ENCODE_PIECE_CHUNKS))
+
+
 def counter_workload(torch, H, manifest_path):
     """The hot kernels at their BASELINE shapes, a fixed number of dispatches each, on one
     stream, phases fenced by synchronize. Writes the phase manifest (kernel-name key, how many
@@ -731,14 +740,15 @@ def counter_workload(torch, H, manifest_path):
           lambda: [bound(lib.glint_encode_bf16_device, w, N * K, 64, *o, st)() for w, o in zip(ws, outs)],
           nbytes=6 * 3.0625 * N * K, elements=6 * N * K)
     del ws, outs
-    # encode over the Llama-3-8B tensor set (one dispatch per tensor, every size a multiple of 512)
+    # encode over the Llama-3-8B tensor set (every size a multiple of 512; one dispatch per
+    # tensor, the two embedding tensors in ENCODE_PIECE_CHUNKS pieces)
     shapes = llama3_8b_shapes()
     total = sum(a * b for a, b in shapes)
     ws = [(torch.randn(a * b, device="cuda", generator=g) * 0.02).to(torch.bfloat16) for a, b in shapes]
     outs = [(torch.empty(w.numel() // 2, dtype=torch.uint8, device="cuda"),
              torch.empty(w.numel() // 2, dtype=torch.uint8, device="cuda"),
              torch.empty(w.numel() // 64, dtype=torch.float32, device="cuda")) for w in ws]
-    phase("encode_model_set", "k_encode_bf16_b64", len(shapes),
+    phase("encode_model_set", "k_encode_bf16_b64", sum(encode_launches(a * b) for a, b in shapes),
           lambda: [bound(lib.glint_encode_bf16_device, w, w.numel(), 64, *o, st)() for w, o in zip(ws, outs)],
           nbytes=3.0625 * total, elements=total, note="226 Llama-3-8B tensors, 8.03e9 weights")
     del ws, outs
