@@ -501,7 +501,7 @@ __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__
 #ifndef GEMV_MR_MAX_F32
 #define GEMV_MR_MAX_F32 4 /* largest M of the f32-out small-M GEMV (x as f32: MR x 32 registers) */
 #endif
-#define GEMV_MR_RED_WIDE 16384 /* floats of row partials a wide small-M workgroup may park in LDS (64 KiB) */
+#define GEMV_MR_RED_ONE 22528 /* floats of row partials a small-M workgroup alone on its CU may park in LDS (88 KiB) */
 #ifndef GEMV_MR_WIDE
 #define GEMV_MR_WIDE 1 /* S > 2: the M = 1 kernel's wider workgroups where x fits (see gemv_mr_wide_ok) */
 #endif
@@ -562,11 +562,16 @@ static int htile_launch_gemv_mr(const uint8_t *hole, const uint8_t *plug, const 
         return -3;
     /* the whole resident grid: halving it where a workgroup holds one row group, as the M = 1
      * kernel does, was slower here (4096 x 14336 f32 out at M = 4: 30.1 against 18.6 us).
-     * Wide workgroups run one per CU, so their row partials may take GEMV_MR_RED_WIDE floats
-     * (with 16 KiB, 8192 x 28672 at M = 4 held 18 rows per workgroup: two generations) */
-    const int red_max = wide ? GEMV_MR_RED_WIDE : GEMV_X_RED_MAX;
-    const int64_t resident =
-        std::max<int64_t>(glint_resident_grid((const void *)kern, threads, (size_t)red_max * 4), 1);
+     * Where only one workgroup fits a CU anyway (the wide ones, and the narrow ones whose
+     * registers allow 2 or 3 waves per SIMD), its row partials may take GEMV_MR_RED_ONE
+     * floats of LDS beside the 64 KiB table: with 16 KiB, 8192 x 28672 at M = 4 held 18 rows
+     * per workgroup (two generations of workgroups) */
+    int red_max = GEMV_X_RED_MAX;
+    int64_t resident = std::max<int64_t>(glint_resident_grid((const void *)kern, threads, (size_t)red_max * 4), 1);
+    if (resident <= glint_cu_count()) {
+        red_max = GEMV_MR_RED_ONE;
+        resident = std::max<int64_t>(glint_resident_grid((const void *)kern, threads, (size_t)red_max * 4), 1);
+    }
     const int64_t per_wave = ((int64_t)N + G * resident - 1) / (G * resident);
     int64_t rows_per_wg = G * per_wave;
     const int64_t cap = (red_max / (S * 4 * MR)) / G * G;
