@@ -501,6 +501,9 @@ __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__
 #ifndef GEMV_MR_MAX_F32
 #define GEMV_MR_MAX_F32 4 /* largest M of the f32-out small-M GEMV (x as f32: MR x 32 registers) */
 #endif
+#ifndef GEMV_MR_F32_TWICE
+#define GEMV_MR_F32_TWICE 1 /* f32 out at M = 5 .. 8 as two small-M launches */
+#endif
 #define GEMV_MR_RED_ONE 22528 /* floats of row partials a small-M workgroup alone on its CU may park in LDS (88 KiB) */
 #ifndef GEMV_MR_WIDE
 #define GEMV_MR_WIDE 1 /* S > 2: the M = 1 kernel's wider workgroups where x fits (see gemv_mr_wide_ok) */
@@ -746,6 +749,20 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
     const bool mfma_ok = fast_ok && !gemv_x_ok;
     if (mfma_ok && GEMV_MR_ON && gemv_mr_takes(M, K, !OUT_BF16))
         return htile_launch_gemv_mr<!OUT_BF16>(hole, plug, absmax, x, y, M, N, K, st);
+    if (!OUT_BF16 && mfma_ok && GEMV_MR_ON && GEMV_MR_F32_TWICE && M > GEMV_MR_MAX_F32 && M <= 2 * GEMV_MR_MAX_F32 &&
+        gemv_mr_takes(GEMV_MR_MAX_F32, K, true)) {
+        /* f32 out at M = 5 .. 8: the 4-row form twice (the weights are read twice), rows 4 ..
+         * M - 1 by the small-M form or, for one row, the M = 1 GEMV; the same f32 arithmetic
+         * per row as one launch would have */
+        const int rc = htile_launch_gemv_mr<true>(hole, plug, absmax, x, y, GEMV_MR_MAX_F32, N, K, st);
+        if (rc != 0)
+            return rc;
+        const int M2 = M - GEMV_MR_MAX_F32;
+        const uint16_t *x2 = (const uint16_t *)x + (int64_t)GEMV_MR_MAX_F32 * K;
+        float *y2 = (float *)y + (int64_t)GEMV_MR_MAX_F32 * N;
+        return M2 >= 2 ? htile_launch_gemv_mr<true>(hole, plug, absmax, x2, y2, M2, N, K, st)
+                       : htile_launch_gemv_xreg<false>(hole, plug, absmax, x2, y2, N, K, st);
+    }
     if (gemv_x_ok)
         return htile_launch_gemv_xreg<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);
     if (mfma_ok && OUT_BF16) {

@@ -322,11 +322,14 @@ def test_f32_prefill_mfma_special_absmax(oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(2, 14336, 4096), (3, 4096, 14336), (4, 1000, 2048), (4, 17, 16384),
-                                   (2, 4097, 8192), (2, 300, 5120), (4, 100, 13824), (3, 64, 3072)])
+                                   (2, 4097, 8192), (2, 300, 5120), (4, 100, 13824), (3, 64, 3072),
+                                   (5, 1000, 4096), (6, 129, 5120), (7, 64, 2048), (8, 300, 14336)])
 def test_small_m_f32_gemv_vs_float64(oracle, M, N, K):
-    """The f32-out ABI at 2 <= M <= 4 (K % 2048 == 0) on the small-M GEMV: exact f32 cells,
-    one FMA per weight and row. Every output within the f32 summation bound
-    (K + 2) 2^-23 sum|t| and the reference's 1e-5 (1 + |ref|); repeats bit-equal."""
+    """The f32-out ABI on the small-M GEMV: 2 <= M <= 4 in one launch, 5 <= M <= 8 as the
+    4-row launch and a second one for the rest (the M = 1 GEMV for one row; M = 5 here),
+    any K % 64 == 0 (a partial last slice at K = 5120, 13824, 3072). Exact f32 cells, one
+    FMA per weight and row. Every output within the f32 summation bound (K + 2) 2^-23
+    sum|t| and the reference's 1e-5 (1 + |ref|); repeats bit-equal."""
     torch = torch_cuda()
     print(f"small-M f32 gemv M={M} N={N} K={K}", flush=True)
     hole, plug, am = _encoded_weight(oracle, N, K, 4100 + K)
@@ -341,7 +344,8 @@ def test_small_m_f32_gemv_vs_float64(oracle, M, N, K):
     assert np.array_equal(host(again).reshape(M, N), y.astype(np.float32))
 
 
-@pytest.mark.parametrize("M,K", [(1, 2048), (1, 4096), (1, 1088), (1, 3072), (1, 14336), (1, 28672), (2, 2048), (4, 4096)])
+@pytest.mark.parametrize("M,K", [(1, 2048), (1, 4096), (1, 1088), (1, 3072), (1, 14336), (1, 28672), (2, 2048), (4, 4096),
+                                 (5, 2048), (8, 4096)])
 def test_f32_gemv_special_absmax(oracle, M, K):
     """The f32-out GEMVs (M = 1: in 512-thread workgroups up to K = 4096 and wider ones
     above, with a partial last K slice at K = 1088 and 3072; and the small-M form) on
