@@ -726,8 +726,12 @@ static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, cons
 /* f32 output at M > 1 (the reference ABI's prefill use): 3-plane k_tile_mfma, whose
  * products are exact and whose sums are f32. 128 x 128 tiles over 8 waves (2 x 4, wave tile
  * 64 x 32) fill the 160 KiB of LDS: x 32 KiB, three W planes 96 KiB, cell table 32 KiB;
- * below 128 rows 64 x 128 tiles (8 waves in a row, wave tile 64 x 16). */
+ * below 128 rows 64 x 128 tiles (8 waves in a row, wave tile 64 x 16), or 64 x 64 over 4
+ * waves where those would leave CUs idle (4096 x 14336 at M = 64: 78.5 -> 61.6 us). */
 #define F32_TILE_MIN_M 128
+#ifndef F32_BN64
+#define F32_BN64 1
+#endif
 
 /* `fixed`: the caller's split-K workspace (the no-allocation entry point); null for the
  * stream's own. Returns 0, -1 null pointer, -2 bs <= 0 or K < 1, -3 launch error, -5 the
@@ -788,9 +792,15 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         const GlintTileProducer p{(const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, N, K, nullptr};
         const uint16_t *xb = (const uint16_t *)x;
         float *yf = (float *)y;
+        /* below 128 rows, 64 x 64 tiles (4 waves) where the 64 x 128 ones, split K ways at most
+         * TILE_SPLIT_MAX, would leave CUs idle (the 4096-row down projection) */
+        const int64_t tiles128 = (int64_t)((N + 127) / 128) * ((M + 63) / 64);
+        const bool narrow = F32_BN64 && tiles128 * TILE_SPLIT_MAX < glint_cu_count();
         const bool planned =
             M < F32_TILE_MIN_M
-                ? tile_mfma_launch<64, 128, 1, 8, 2, GlintTileProducer, TileOutF32, 3>(p, xb, yf, M, N, K, st, fixed)
+                ? (narrow ? tile_mfma_launch<64, 64, 1, 4, 2, GlintTileProducer, TileOutF32, 3>(p, xb, yf, M, N, K, st, fixed)
+                          : tile_mfma_launch<64, 128, 1, 8, 2, GlintTileProducer, TileOutF32, 3>(p, xb, yf, M, N, K, st,
+                                                                                                  fixed))
                 : tile_mfma_launch<128, 128, 2, 4, 2, GlintTileProducer, TileOutF32, 3>(p, xb, yf, M, N, K, st, fixed);
         if (!planned)
             return -5;
