@@ -130,10 +130,31 @@ def bench_gemv(torch, H, steps, warmup, headline_only=False):
     fnsd = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], xd, yd, 1, 4096, 14336, 64, st) for p in pins_d]
     msd = timed(torch, fnsd, steps, warmup)
     del pins_d
+    # Beside the headline, not instead of it: a decode step's gate and up projections are two
+    # independent GEMVs on the same x. On two streams (16 GEMVs a pass, alternating) one's
+    # tail overlaps the other's start; stacked as one 28672-row pin they are one launch.
+    ys = [torch.empty(N, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    pair = lambda i, s: bound(lib.launch_glint_htile_bf16_stream, pins[i % copies][0], pins[i % copies][1],
+                              pins[i % copies][2], x, ys[i % 2], 1, N, K, 64, s)
+    ms_pair = timed(torch, [spread_over_streams(torch, pair, 16, 2)], max(steps // 16, 20), 3) / 16
+    gs = torch.Generator(device="cuda").manual_seed(2004)
+    pins_s = []
+    for _ in range(max(5, int(1.05 * 2 ** 30 / (2 * per)) + 1)):
+        w = (torch.randn(2 * N * K, device="cuda", generator=gs) * 0.02).to(torch.bfloat16)
+        pins_s.append(H.encode_bf16(w, 64))
+        del w
+    ys2 = torch.empty(2 * N, dtype=torch.bfloat16, device="cuda")
+    fnss = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, ys2, 1, 2 * N, K, 64, st) for p in pins_s]
+    ms_stack = timed(torch, fnss, max(steps // 2, 50), warmup)
+    del pins_s
     return {
         "ms": ms, "bytes": per, "gbs": per / ms / 1e6, "copies": copies, "rotation_bytes": copies * per,
         "f32_out_ms": ms32, "f32_out_gbs": gemv_bytes(N, K, 4) / ms32 / 1e6,
         "down_4096x14336_ms": msd, "down_4096x14336_gbs": gemv_bytes(4096, 14336) / msd / 1e6,
+        "gate_up_two_streams": {"ms_per_gemv": ms_pair, "gbs": per / ms_pair / 1e6,
+                                "frac": per / ms_pair / 1e6 / HBM_PEAK_GBS},
+        "gate_up_stacked_28672x4096": {"ms": ms_stack, "gbs": 2 * per / ms_stack / 1e6,
+                                       "frac": 2 * per / ms_stack / 1e6 / HBM_PEAK_GBS},
     }, pins, x
 
 
@@ -967,6 +988,10 @@ def main() -> int:
         del src, dst
     gemv, pins, x = bench_gemv(torch, H, args.steps, args.warmup, args.headline_only)
     log(f"gemv {gemv['ms'] * 1e3:.2f} us {gemv['gbs']:.0f} GB/s")
+    if "gate_up_two_streams" in gemv:
+        log(f"gate/up pair on two streams {gemv['gate_up_two_streams']['ms_per_gemv'] * 1e3:.2f} us per GEMV "
+            f"({gemv['gate_up_two_streams']['frac']:.3f}); stacked 28672x4096 "
+            f"{gemv['gate_up_stacked_28672x4096']['ms'] * 1e3:.2f} us ({gemv['gate_up_stacked_28672x4096']['frac']:.3f})")
     del pins
     torch.cuda.empty_cache()
     extra = {}
