@@ -713,6 +713,9 @@ __global__ __launch_bounds__(512) void k_int8_mma_dma(const int8_t *__restrict__
 #ifndef Q_NBUF
 #define Q_NBUF 8
 #endif
+#ifndef Q_PER_STEP
+#define Q_PER_STEP 2 /* K slices per barrier (1 or 2) */
+#endif
 template <bool ACCUM>
 __global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
                                                        const float *__restrict__ sx, const float *__restrict__ sw,
@@ -773,13 +776,7 @@ __global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict_
                                                  4, svo, kc * 4u, 0, 0);
     };
     const int fr_ofs = g2_lds_ofs(lane & 15, lane >> 4);
-    auto step = [&](int kb, int u) {
-        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(3 * (Q_NBUF - 2)));
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
-        dma(kb + Q_NBUF - 1, (u + Q_NBUF - 1) % Q_NBUF);
-        __builtin_amdgcn_sched_barrier(0);
+    auto slice = [&](int u) {
         const int8_t *ta = slotA(u), *tb = slotB(u);
         const float *ts = slotS(u);
         glint_i32x4 af[2], bf[2];
@@ -804,17 +801,33 @@ __global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict_
             }
         }
     };
+    /* Q_PER_STEP slices per barrier; Q_NBUF - Q_PER_STEP slices in flight ahead */
+    constexpr int PS = Q_PER_STEP, AHEAD = Q_NBUF - PS;
+    auto step = [&](int kb, int u) {
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(3 * (AHEAD - PS)));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
 #pragma unroll
-    for (int i = 0; i < Q_NBUF - 1; ++i)
+        for (int v = 0; v < PS; ++v)
+            dma(kb + AHEAD + v, (u + AHEAD + v) % Q_NBUF);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int v = 0; v < PS; ++v)
+            if (v == 0 || kb + v < nkb) /* the last step of an odd count has one slice */
+                slice((u + v) % Q_NBUF);
+    };
+#pragma unroll
+    for (int i = 0; i < AHEAD; ++i)
         dma(i, i);
     int kb = 0;
     for (; kb + Q_NBUF <= nkb; kb += Q_NBUF) {
 #pragma unroll
-        for (int u = 0; u < Q_NBUF; ++u)
+        for (int u = 0; u < Q_NBUF; u += PS)
             step(kb + u, u);
     }
 #pragma unroll
-    for (int u = 0; u + 1 < Q_NBUF; ++u)
+    for (int u = 0; u < Q_NBUF; u += PS)
         if (kb + u < nkb)
             step(kb + u, u);
     __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0); /* the ring's last (clamped) loads land first */

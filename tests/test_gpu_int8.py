@@ -15,7 +15,8 @@ from tests.gpu_util import dev, host, bf16_bits, first_diff, torch_cuda
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("m,n,k", [(70, 192, 256), (37, 100, 1536), (1, 64, 64), (130, 257, 512)])
+@pytest.mark.parametrize("m,n,k", [(70, 192, 256), (37, 100, 1536), (1, 64, 64), (130, 257, 512), (70, 4096, 3072),
+                                   (33, 200, 3136)])
 def test_int8_mma_gemm_matches_emulation(oracle, m, n, k):
     rng = np.random.default_rng(m * 1000 + n)
     x = bf16_bits(rng.normal(0, 1, m * k).astype(np.float32))
