@@ -713,10 +713,13 @@ __global__ __launch_bounds__(512) void k_int8_mma_dma(const int8_t *__restrict__
 #ifndef Q_NBUF
 #define Q_NBUF 8
 #endif
+#ifndef Q_NARROW
+#define Q_NARROW 1
+#endif
 #ifndef Q_PER_STEP
 #define Q_PER_STEP 2 /* K slices per barrier (1 or 2) */
 #endif
-template <bool ACCUM>
+template <bool ACCUM, int NB>
 __global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
                                                        const float *__restrict__ sx, const float *__restrict__ sw,
                                                        float *__restrict__ y, int M, int N, int K) {
@@ -742,13 +745,13 @@ __global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict_
     };
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * Q_BM, n0 = blockIdx.x * Q_BN;
+    const int m0 = blockIdx.y * Q_BM, n0 = blockIdx.x * (32 * NB); /* NB 16-column blocks per wave */
     const int nkb = K / 64;
-    float acc[2][2][4];
+    float acc[2][NB][4];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 acc[a][b][i] = 0.0f;
@@ -779,21 +782,21 @@ __global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict_
     auto slice = [&](int u) {
         const int8_t *ta = slotA(u), *tb = slotB(u);
         const float *ts = slotS(u);
-        glint_i32x4 af[2], bf[2];
-        float swv[2];
+        glint_i32x4 af[2], bf[NB];
+        float swv[NB];
 #pragma unroll
         for (int a = 0; a < 2; ++a)
             af[a] = *(const glint_i32x4 *)(ta + (wm * 32 + a * 16) * G2_LDS_ROW + fr_ofs);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            bf[b] = *(const glint_i32x4 *)(tb + (wn * 32 + b * 16) * G2_LDS_ROW + fr_ofs);
-            swv[b] = ts[64 + wn * 32 + b * 16 + (lane & 15)];
+        for (int b = 0; b < NB; ++b) {
+            bf[b] = *(const glint_i32x4 *)(tb + (wn * 16 * NB + b * 16) * G2_LDS_ROW + fr_ofs);
+            swv[b] = ts[64 + wn * 16 * NB + b * 16 + (lane & 15)];
         }
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
             const glint_f32x4 sxv = *(const glint_f32x4 *)(ts + wm * 32 + a * 16 + (lane >> 4) * 4);
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
+            for (int b = 0; b < NB; ++b) {
                 const glint_i32x4 ic = glint_mfma_i8(af[a], bf[b], glint_i32x4{0, 0, 0, 0});
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
@@ -834,11 +837,11 @@ __global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict_
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int rr = m0 + wm * 32 + a * 16 + (lane >> 4) * 4 + i;
-                const int cc = n0 + wn * 32 + b * 16 + (lane & 15);
+                const int cc = n0 + wn * 16 * NB + b * 16 + (lane & 15);
                 if (rr < M && cc < N) {
                     float *dst = y + (int64_t)rr * N + cc;
                     *dst = ACCUM ? *dst + acc[a][b][i] : acc[a][b][i];
@@ -891,8 +894,15 @@ static void q_launch_gemm(const int8_t *xq, const float *sx, const int8_t *wq, c
         return;
     }
     if (!PLUG && g3_fits(m, n, k_in)) {
-        k_int8_mma_ring<ACCUM><<<dim3((n + Q_BN - 1) / Q_BN, (m + Q_BM - 1) / Q_BM), 256, 0, st>>>(xq, wq, sx, sw, y, m,
-                                                                                                 n, k_in);
+        /* 64 x 32 output tiles (each wave one 16-column block; the loader still stages 64 W
+         * rows, half of them unused) where 64 x 64 tiles would leave CUs idle */
+        const int64_t tiles64 = (int64_t)((n + Q_BN - 1) / Q_BN) * ((m + Q_BM - 1) / Q_BM);
+        if (Q_NARROW && tiles64 < glint_cu_count())
+            k_int8_mma_ring<ACCUM, 1><<<dim3((n + 31) / 32, (m + Q_BM - 1) / Q_BM), 256, 0, st>>>(xq, wq, sx, sw, y, m,
+                                                                                                  n, k_in);
+        else
+            k_int8_mma_ring<ACCUM, 2><<<dim3((n + Q_BN - 1) / Q_BN, (m + Q_BM - 1) / Q_BM), 256, 0, st>>>(xq, wq, sx, sw,
+                                                                                                          y, m, n, k_in);
         return;
     }
     dim3 g((n + Q_BN - 1) / Q_BN, (m + Q_BM - 1) / Q_BM);
