@@ -64,6 +64,8 @@ __device__ __forceinline__ glint_i16x2 glint_mag_key(uint32_t d) {
 #ifndef ENC_COPIES
 #define ENC_COPIES 8
 #endif
+static_assert(ENC_COPIES >= 1 && ENC_COPIES <= 64 && (ENC_COPIES & (ENC_COPIES - 1)) == 0, "power-of-two table copies");
+#define ENC_ENTRY_SHIFT (4 + __builtin_ctz(ENC_COPIES)) /* log2 of the byte stride of one entry's copies */
 #ifndef ENC_THREADS
 #define ENC_THREADS 1024
 #endif
@@ -159,7 +161,9 @@ __device__ __forceinline__ void glint_encode_chunk(const glint_u32x4 d, const gl
     /* element 4h + i contributes its hole nibble at bit 4i and plug nibble at 16 + 4i */
     uint32_t acc[2];
     if (sbits - 0x12800000u < 0x6C800000u - 0x12800000u) { /* 2^-90 <= s < 2^90, so no NaN or inf */
-        const uint32_t rw = *(const uint32_t *)((const char *)tab + ((sbits >> 9) & (127u << 7)) + lane_r);
+        /* entry m (the mantissa of s, bits 16..22) at byte m * ENC_COPIES * 16 */
+        const uint32_t rw =
+            *(const uint32_t *)((const char *)tab + ((sbits >> (16 - ENC_ENTRY_SHIFT)) & (127u << ENC_ENTRY_SHIFT)) + lane_r);
         const float y = __uint_as_float(rw - sbits); /* RN(1/s) */
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
