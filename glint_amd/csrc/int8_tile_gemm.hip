@@ -91,8 +91,9 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
 /* m <= 4, k_in % 2048 == 0, k_in / 2048 <= 8 (the decode shapes). Like the GLINT decode
  * GEMV: the row is cut into S = k_in / 2048 slices, wave (s, g) keeps slice s of the m
  * activation rows in registers (32 f32 per lane per row) and streams weight rows
- * r0 + g, r0 + g + G, ... of its workgroup's row range: per row each lane reads 32 int8
- * (two 16-B loads, one 64-block, so one scale). Weights are rounded to BF16 exactly as the
+ * r0 + g, r0 + g + G, ... of its workgroup's row range: per row each lane reads 32 int8,
+ * vectors l and 64 + l of the slice (two 16-B loads, each instruction 1 KiB contiguous;
+ * two 64-blocks, so two scales). Weights are rounded to BF16 exactly as the
  * tile kernels do (v_cvt_pk_bf16_f32 of q * scale); each BF16 weight pair meets the BF16 x
  * pair in one v_dot2_f32_bf16 (both products exact in f32, added into the f32 partial).
  * Against unpacking the pair and two f32 FMAs, with the grid capped at 16 waves per CU
@@ -124,8 +125,11 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
 
 struct I8Row {
     glint_u32x4 q0, q1;
-    float s;
+    float s, s1; /* the scales of q0's and q1's 64-blocks */
 };
+#ifndef I8V_LINE
+#define I8V_LINE 1 /* lane l loads vectors l and 64 + l of its slice (1 KiB contiguous per load) */
+#endif
 #ifndef I8V_DOT2
 #define I8V_DOT2 1 /* products of the BF16 weight pair and the BF16 x pair by v_dot2_f32_bf16 */
 #endif
@@ -145,13 +149,17 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
     const int nrows = max(min(rows_per_wg, N - r0), 0);
     const int my = g < nrows ? (nrows - g + G - 1) / G : 0;
     const int64_t kv = K >> 4;                     /* 16-B vectors per weight row */
-    const int64_t j = (int64_t)(s * 64 + lane) * 2; /* this lane's two vectors in a row */
+    /* this lane's two 16-B vectors in a row: 1 KiB contiguous per load instruction
+     * (I8V_LINE), or two adjacent vectors */
+    const int64_t v0 = I8V_LINE ? (int64_t)s * 128 + lane : (int64_t)(s * 64 + lane) * 2;
+    const int64_t v1 = I8V_LINE ? v0 + 64 : v0 + 1;
     auto row_of = [&](int i) -> int64_t { return (int64_t)min(r0 + g + min(i, max(my - 1, 0)) * G, N - 1); };
     auto load = [&](int i, I8Row &r) {
         const int64_t n = row_of(i);
-        r.q0 = __builtin_nontemporal_load(&q[n * kv + j]);
-        r.q1 = __builtin_nontemporal_load(&q[n * kv + j + 1]);
-        r.s = scale[n * (K >> 6) + (j >> 2)];
+        r.q0 = __builtin_nontemporal_load(&q[n * kv + v0]);
+        r.q1 = __builtin_nontemporal_load(&q[n * kv + v1]);
+        r.s = scale[n * (K >> 6) + (v0 >> 2)];
+        r.s1 = scale[n * (K >> 6) + (v1 >> 2)];
     };
     /* x: this lane's 32 activations of each of the MR rows: as BF16 pairs (I8V_DOT2) or f32 */
     uint32_t xw[MR][16];
@@ -160,7 +168,7 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
     for (int mr = 0; mr < MR; ++mr)
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-            const glint_u32x4 v = x[(int64_t)mr * (K >> 3) + (s * 64 + lane) * 4 + h];
+            const glint_u32x4 v = x[(int64_t)mr * (K >> 3) + (h < 2 ? 2 * v0 + h : 2 * v1 + h - 2)];
             const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -187,7 +195,7 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
 #pragma unroll
                 for (int b = 0; b < 2; ++b) {
                     float lo, hi;
-                    weights(W[e], b, lo, hi);
+                    weights(W[e], e >> 2, b, lo, hi);
                     const uint32_t pk = glint_cvt_bf16x2(lo, hi);
                     if constexpr (I8V_DOT2) {
                         /* both BF16 products are exact in f32; one instruction adds them */
@@ -210,17 +218,17 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
          * then v_cvt_f32_ubyte) and -128 s is exact, so the one rounding gives the f32
          * product q s exactly as a multiply would. When -128 s is not finite (s infinite,
          * NaN or above 2^120) the lane multiplies instead. */
-        const float ns = -128.0f * r.s;
-        if (__builtin_isfinite(ns)) {
-            accumulate([&](uint32_t w, int b, float &lo, float &hi) {
+        const float sv[2] = {r.s, r.s1}, ns[2] = {-128.0f * r.s, -128.0f * r.s1};
+        if (__builtin_isfinite(ns[0]) && __builtin_isfinite(ns[1])) {
+            accumulate([&](uint32_t w, int hv, int b, float &lo, float &hi) {
                 const uint32_t u = w ^ 0x80808080u;
-                lo = fmaf((float)((u >> (16 * b)) & 0xFFu), r.s, ns);
-                hi = fmaf((float)((u >> (16 * b + 8)) & 0xFFu), r.s, ns);
+                lo = fmaf((float)((u >> (16 * b)) & 0xFFu), sv[hv], ns[hv]);
+                hi = fmaf((float)((u >> (16 * b + 8)) & 0xFFu), sv[hv], ns[hv]);
             });
         } else {
-            accumulate([&](uint32_t w, int b, float &lo, float &hi) {
-                lo = (float)(int8_t)(w >> (16 * b)) * r.s;
-                hi = (float)(int8_t)(w >> (16 * b + 8)) * r.s;
+            accumulate([&](uint32_t w, int hv, int b, float &lo, float &hi) {
+                lo = (float)(int8_t)(w >> (16 * b)) * sv[hv];
+                hi = (float)(int8_t)(w >> (16 * b + 8)) * sv[hv];
             });
         }
 #pragma unroll
