@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void k_i8tile_generic(const uint16_t *__restri
 #define I8V_DEPTH 2 /* rows of loads in flight per wave (I8V_DEPTH_M1 for m = 1, k_in <= 4096; I8V_DEPTH_M2 at m = 2) */
 #endif
 #ifndef I8V_DEPTH_M1
-#define I8V_DEPTH_M1 2
+#define I8V_DEPTH_M1 1
 #endif
 #ifndef I8V_DEPTH_M2
 #define I8V_DEPTH_M2 1 /* rows in flight at m = 2 */
@@ -265,8 +265,9 @@ __global__ __launch_bounds__(I8V_THREADS) void k_i8tile_gemv(const glint_u32x4 *
 template <int MR>
 static void i8tile_launch_gemv(const uint16_t *x, const Int8PinLinear &w, float *y, hipStream_t st) {
     const int S = w.k_in / 2048, G = (I8V_THREADS / 64) / S, threads = 64 * S * G;
-    /* rows in flight (with the dot form and the 16-wave cap): m = 1 at k_in <= 4096 two
-     * (14336 x 4096: 13.6 us, four 14.0, three 14.3); m = 2 one (14336 x 4096 15.4 against
+    /* rows in flight (with the dot form and the 16-wave cap): m = 1 at k_in <= 4096 one
+     * with the 1-KiB loads (14336 x 4096 12.5 against 13.5 us with two; with adjacent vectors
+     * per lane two had been best, 13.6 against 14.0 for four); m = 2 one (14336 x 4096 15.4 against
      * 15.6, 4096 x 14336 16.4 against 16.9, 8192 x 8192 17.3 against 17.9); otherwise two
      * (one was 8-35% slower at m = 1, k_in > 4096 and at m = 4, three 1-7% slower) */
     auto kern = (MR == 1 && S <= 2) ? k_i8tile_gemv<MR, I8V_DEPTH_M1>
