@@ -340,7 +340,7 @@ typedef __bf16 glint_bf16x2_t __attribute__((ext_vector_type(2)));
  * x held as f32 (MR x 32 registers) and one f32 FMA per weight and row in k order, the
  * weights the exact f32 cells; the same arithmetic per row as the M = 1 f32 GEMV, so the
  * same (K + 2) 2^-23 sum |w x| bound. */
-template <int MR, bool F32, bool PART, int MAXT>
+template <int MR, bool F32, bool PART, int MAXT, int DEPTH>
 __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__ hole,
                                                                   const void *__restrict__ plug,
                                                                   const float *__restrict__ absmax,
@@ -375,9 +375,10 @@ __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__
             xv[m][c] = xr[c];
     }
     __builtin_amdgcn_sched_barrier(0);
-    GemvRow<EL> buf[2];
-    gemv_x_load<EL>(hole, plug, absmax, row_of(0), nch, jl, buf[0]);
-    gemv_x_load<EL>(hole, plug, absmax, row_of(1), nch, jl, buf[1]);
+    GemvRow<EL> buf[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+        gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, jl, buf[d]);
     __builtin_amdgcn_sched_barrier(0);
     glint_cells_fill_sstore(ltab, fill);
     __syncthreads();
@@ -455,22 +456,27 @@ __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__
                 red[((t * S + s) * 4 + (lane >> 4)) * MR + m] = v;
         }
     };
+    /* DEPTH rows in flight, full rounds while every load is of a real row (as in
+     * k_htile_gemv_xreg) */
     int i = 0;
-    for (; i + 4 <= my; i += 2) {
-        compute_row(i, buf[0]);
-        gemv_x_load<EL>(hole, plug, absmax, row_of(i + 2), nch, jl, buf[0]);
-        compute_row(i + 1, buf[1]);
-        gemv_x_load<EL>(hole, plug, absmax, row_of(i + 3), nch, jl, buf[1]);
+    for (; i + 2 * DEPTH <= my; i += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            compute_row(i + d, buf[d]);
+            gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, jl, buf[d]);
+        }
     }
-    for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
         if (i + d < my) {
             compute_row(i + d, buf[d]);
-            if (i + d + 2 < my)
-                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + 2), nch, jl, buf[d]);
+            if (i + d + DEPTH < my)
+                gemv_x_load<EL>(hole, plug, absmax, row_of(i + d + DEPTH), nch, jl, buf[d]);
         }
-    for (int d = 0; d < 2; ++d)
-        if (i + 2 + d < my)
-            compute_row(i + 2 + d, buf[d]);
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+        if (i + DEPTH + d < my)
+            compute_row(i + DEPTH + d, buf[d]);
     __syncthreads();
 
     for (int e = threadIdx.x; e < nrows * MR; e += blockDim.x) {
@@ -500,6 +506,15 @@ __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__
  * 8-row template holds 128 VGPRs of x and runs at 2 waves per SIMD). */
 #ifndef GEMV_MR_MAX_F32
 #define GEMV_MR_MAX_F32 4 /* largest M of the f32-out small-M GEMV (x as f32: MR x 32 registers) */
+#endif
+/* Rows in flight per wave: one for BF16 out (against two: 14336 x 4096 M = 2 14.1 -> 13.4 us,
+ * M = 4 17.1 -> 16.4, M = 8 24.4 -> 23.7; 4096 x 14336 M = 2 14.4 -> 13.9; three slower), two
+ * for f32 out (one: 14336 x 4096 M = 4 16.4 -> 22.0 us) */
+#ifndef GEMV_MR_DEPTH_BF16
+#define GEMV_MR_DEPTH_BF16 1
+#endif
+#ifndef GEMV_MR_DEPTH_F32
+#define GEMV_MR_DEPTH_F32 2
 #endif
 #ifndef GEMV_MR_F32_TWICE
 #define GEMV_MR_F32_TWICE 1 /* f32 out at M = 5 .. 8 as two small-M launches */
@@ -551,10 +566,11 @@ static int htile_launch_gemv_mr(const uint8_t *hole, const uint8_t *plug, const 
         constexpr int R = decltype(mr_c)::value;
         constexpr bool W = !F32 && R <= 4; /* wide templates only where x fits (gemv_mr_wide_ok) */
         constexpr int TW = W ? GEMV_X_THREADS_WIDE : GEMV_X_THREADS;
-        return part ? (wide ? k_htile_gemv_mr<R, F32, true, TW> : k_htile_gemv_mr<R, F32, true, GEMV_X_THREADS>)
-                    : (wide ? k_htile_gemv_mr<R, F32, false, TW> : k_htile_gemv_mr<R, F32, false, GEMV_X_THREADS>);
+        constexpr int D = F32 ? GEMV_MR_DEPTH_F32 : GEMV_MR_DEPTH_BF16;
+        return part ? (wide ? k_htile_gemv_mr<R, F32, true, TW, D> : k_htile_gemv_mr<R, F32, true, GEMV_X_THREADS, D>)
+                    : (wide ? k_htile_gemv_mr<R, F32, false, TW, D> : k_htile_gemv_mr<R, F32, false, GEMV_X_THREADS, D>);
     };
-    decltype(&k_htile_gemv_mr<2, F32, false, GEMV_X_THREADS>) kern;
+    decltype(&k_htile_gemv_mr<2, F32, false, GEMV_X_THREADS, 2>) kern;
     if (MR == 2)
         kern = pick(std::integral_constant<int, 2>{});
     else if (MR == 4)
