@@ -280,7 +280,9 @@ static inline int glint_cu_count() {
  * 64 KiB); remembered per (kernel, device). Returns 0 or -1. */
 static inline int glint_set_lds_limit(const void *kernel, size_t bytes) {
     static std::mutex mu;
-    static struct { const void *k; int dev; size_t bytes; } seen[64];
+    /* (kernel, device) pairs already raised; past the last slot the attribute is set on every
+     * call, which is correct but costs a runtime call per launch */
+    static struct { const void *k; int dev; size_t bytes; } seen[256];
     static int nseen = 0;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess)
@@ -291,7 +293,7 @@ static inline int glint_set_lds_limit(const void *kernel, size_t bytes) {
             return 0;
     if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess)
         return -1;
-    if (nseen < 64)
+    if (nseen < 256)
         seen[nseen++] = {kernel, dev, bytes};
     return 0;
 }
