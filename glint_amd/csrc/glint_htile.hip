@@ -139,6 +139,60 @@ __device__ __forceinline__ void glint_cells_fill_sstore(float *ltab, const Glint
     }
 }
 
+/* Half fill (GEMV_HALF_TABLE): lanes l and l + 32 share copy l % 32, so only copies 0 .. 31
+ * of each cell are written: 2048 runs of 16 B instead of 4096 (the fill's LDS writes were
+ * 0.5-0.8 us of the 14336 x 4096 launch). A lookup address stays one v_perm (lane4 =
+ * (lane % 32) * 4); two lanes of a ds_read then share a bank. Run u (0 .. 2047) is run
+ * (u / 8) * 16 + u % 8 of the 64-copy layout; thread t takes u = t + k blockDim.x, so a
+ * wave's 64 runs of step k hold 8 consecutive cells: two s_load_dwordx4 per step.
+ * 14336 x 4096: 12.30-12.59 -> 11.87-11.95 us. A 16-copy form was slower (12.8 us), and so
+ * was a generic form of this fill (12.3 us): keep the prologue's code as it is. */
+#ifndef GEMV_HALF_TABLE
+#define GEMV_HALF_TABLE 1
+#endif
+#define GLINT_FILLH_STEPS 5 /* covers 2048 runs for blockDim.x >= 410 */
+struct GlintCellFillH {
+    glint_f32x4 c[GLINT_FILLH_STEPS][2];
+};
+__device__ __forceinline__ void glint_cells_fillh_sload(GlintCellFillH &f) {
+    const int wbase = __builtin_amdgcn_readfirstlane((int)threadIdx.x & ~63);
+#pragma unroll
+    for (int k = 0; k < GLINT_FILLH_STEPS; ++k) {
+        const int c0 = min((wbase + k * (int)blockDim.x) >> 3, 248);
+        f.c[k][0] = *(const glint_f32x4 *)(&kCells[0][0] + c0);
+        f.c[k][1] = *(const glint_f32x4 *)(&kCells[0][0] + c0 + 4);
+    }
+}
+__device__ __forceinline__ void glint_cells_fillh_sstore(float *ltab, const GlintCellFillH &f) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63, ci = lane >> 3; /* cell c0 + ci (blockDim.x % 64 == 0) */
+#pragma unroll
+    for (int k = 0; k < GLINT_FILLH_STEPS; ++k) {
+        const int u = (int)threadIdx.x + k * (int)blockDim.x;
+        const glint_f32x4 lo = f.c[k][0], hi = f.c[k][1];
+        const float vl = (ci & 2) ? ((ci & 1) ? lo.w : lo.z) : ((ci & 1) ? lo.y : lo.x);
+        const float vh = (ci & 2) ? ((ci & 1) ? hi.w : hi.z) : ((ci & 1) ? hi.y : hi.x);
+        const float v = (ci & 4) ? vh : vl;
+        if (u < 2048)
+            ((f32x4 *)ltab)[(u >> 3) * 16 + (u & 7)] = f32x4{v, v, v, v};
+    }
+    for (int u = threadIdx.x + GLINT_FILLH_STEPS * blockDim.x; u < 2048; u += blockDim.x) {
+        const float v = (&kCells[0][0])[u >> 3];
+        ((f32x4 *)ltab)[(u >> 3) * 16 + (u & 7)] = f32x4{v, v, v, v};
+    }
+}
+#if GEMV_HALF_TABLE
+typedef GlintCellFillH GemvFill;
+#define gemv_fill_sload glint_cells_fillh_sload
+#define gemv_fill_sstore glint_cells_fillh_sstore
+#define GEMV_LANE4(lane) ((uint32_t)((lane) & 31) * 4u)
+#else
+typedef GlintCellFillS GemvFill;
+#define gemv_fill_sload glint_cells_fill_sload
+#define gemv_fill_sstore glint_cells_fill_sstore
+#define GEMV_LANE4(lane) ((uint32_t)(lane) * 4u)
+#endif
+
 /* A lane's partial the way the reference forms it, w = cell * absmax per weight and then
  * the FMA with x, for a block whose absmax is infinite, NaN or at least 2^126: there the
  * factored form (sum of cell * x, times absmax) can give +-inf where products of mixed sign
@@ -180,7 +234,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
     constexpr int Q = EL / 8; /* 8-element groups per chunk = packed words per plane */
 
     const int lane = threadIdx.x & 63;
-    const uint32_t lane4 = (uint32_t)lane * 4u;
+    const uint32_t lane4 = GEMV_LANE4(lane);
     const int nch = K / EL, S = PART ? (nch + 63) >> 6 : nch >> 6;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = w % S, g = w / S;
@@ -195,8 +249,8 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
 
     /* Loads go out in the order they are consumed (the wait counter is in order): the
      * cell table, x, then the first rows; the table's LDS writes follow. */
-    GlintCellFillS fill;
-    glint_cells_fill_sload(fill);
+    GemvFill fill;
+    gemv_fill_sload(fill);
     glint_u32x4 xv[XC > Q ? XC : Q];
     if (XC > 0) {
 #pragma unroll
@@ -213,7 +267,7 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
     for (int d = 0; d < GEMV_X_PRE_OF(DEPTH); ++d)
         gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, jl, buf[d]);
     __builtin_amdgcn_sched_barrier(0);
-    glint_cells_fill_sstore(ltab, fill);
+    gemv_fill_sstore(ltab, fill);
     if (XC > 0) {
 #pragma unroll
         for (int c = 0; c < XC; ++c)
@@ -351,7 +405,7 @@ __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__
     extern __shared__ __attribute__((aligned(16))) float red[]; /* [rows_per_wg][S][4][MR] */
     constexpr int EL = 32, Q = EL / 8;
     const int lane = threadIdx.x & 63;
-    const uint32_t lane4 = (uint32_t)lane * 4u;
+    const uint32_t lane4 = GEMV_LANE4(lane);
     const int nch = K / EL, S = PART ? (nch + 63) >> 6 : nch >> 6;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = w % S, g = w / S;
@@ -363,8 +417,8 @@ __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__
     const bool act = !PART || j < (uint32_t)nch; /* PART: idle lanes of the last slice */
     const uint32_t jl = act ? j : (uint32_t)nch - 1u;
 
-    GlintCellFillS fill;
-    glint_cells_fill_sload(fill);
+    GemvFill fill;
+    gemv_fill_sload(fill);
     /* x: row m's 32 elements [32 j, 32 j + 32) as 16 words of BF16 pairs */
     glint_u32x4 xv[MR][4];
 #pragma unroll
@@ -380,7 +434,7 @@ __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__
     for (int d = 0; d < DEPTH; ++d)
         gemv_x_load<EL>(hole, plug, absmax, row_of(d), nch, jl, buf[d]);
     __builtin_amdgcn_sched_barrier(0);
-    glint_cells_fill_sstore(ltab, fill);
+    gemv_fill_sstore(ltab, fill);
     __syncthreads();
     float xf[F32 ? MR : 1][F32 ? 32 : 1];
     if constexpr (F32) {
