@@ -33,6 +33,8 @@ struct GlintCodeEntry {
 #define GLINT_LDS_CELLS_WORDS (256 * 32)
 
 #include "glint_cells.h"
+
+typedef float glint_f32x4 __attribute__((ext_vector_type(4)));
 /* Device copy of GLINT_CELLS (one per translation unit). */
 static __constant__ float kCells[16][16] = GLINT_CELLS_INIT;
 
@@ -125,6 +127,45 @@ __device__ __forceinline__ void glint_cells_fill_store(float *ltab, const GlintC
     }
 }
 
+/* Half fill: lanes l and l + 32 share copy l % 32, so only copies 0 .. 31
+ * of each cell are written: 2048 runs of 16 B instead of 4096 (the fill's LDS writes were
+ * 0.5-0.8 us of the 14336 x 4096 launch). A lookup address stays one v_perm (lane4 =
+ * (lane % 32) * 4); two lanes of a ds_read then share a bank. Run u (0 .. 2047) is run
+ * (u / 8) * 16 + u % 8 of the 64-copy layout; thread t takes u = t + k blockDim.x, so a
+ * wave's 64 runs of step k hold 8 consecutive cells: two s_load_dwordx4 per step.
+ * 14336 x 4096: 12.30-12.59 -> 11.87-11.95 us. A 16-copy form was slower (12.8 us), and so
+ * was a generic form of this fill (12.3 us): keep the prologue's code as it is. */
+#define GLINT_FILLH_STEPS 5 /* covers 2048 runs for blockDim.x >= 410 */
+struct GlintCellFillH {
+    glint_f32x4 c[GLINT_FILLH_STEPS][2];
+};
+__device__ __forceinline__ void glint_cells_fillh_sload(GlintCellFillH &f) {
+    const int wbase = __builtin_amdgcn_readfirstlane((int)threadIdx.x & ~63);
+#pragma unroll
+    for (int k = 0; k < GLINT_FILLH_STEPS; ++k) {
+        const int c0 = min((wbase + k * (int)blockDim.x) >> 3, 248);
+        f.c[k][0] = *(const glint_f32x4 *)(&kCells[0][0] + c0);
+        f.c[k][1] = *(const glint_f32x4 *)(&kCells[0][0] + c0 + 4);
+    }
+}
+__device__ __forceinline__ void glint_cells_fillh_sstore(float *ltab, const GlintCellFillH &f) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63, ci = lane >> 3; /* cell c0 + ci (blockDim.x % 64 == 0) */
+#pragma unroll
+    for (int k = 0; k < GLINT_FILLH_STEPS; ++k) {
+        const int u = (int)threadIdx.x + k * (int)blockDim.x;
+        const glint_f32x4 lo = f.c[k][0], hi = f.c[k][1];
+        const float vl = (ci & 2) ? ((ci & 1) ? lo.w : lo.z) : ((ci & 1) ? lo.y : lo.x);
+        const float vh = (ci & 2) ? ((ci & 1) ? hi.w : hi.z) : ((ci & 1) ? hi.y : hi.x);
+        const float v = (ci & 4) ? vh : vl;
+        if (u < 2048)
+            ((f32x4 *)ltab)[(u >> 3) * 16 + (u & 7)] = f32x4{v, v, v, v};
+    }
+    for (int u = threadIdx.x + GLINT_FILLH_STEPS * blockDim.x; u < 2048; u += blockDim.x) {
+        const float v = (&kCells[0][0])[u >> 3];
+        ((f32x4 *)ltab)[(u >> 3) * 16 + (u & 7)] = f32x4{v, v, v, v};
+    }
+}
 /* Byte address of code byte K of E for the lane whose lane*4 is `lane4` (in byte 0). */
 template <int K>
 __device__ __forceinline__ uint32_t glint_cell_addr(uint32_t E, uint32_t lane4) {
@@ -154,7 +195,6 @@ struct GlintSplitWs {
 /* ------------------------------------------------------------- device helpers */
 typedef uint32_t glint_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t glint_u32x2 __attribute__((ext_vector_type(2)));
-typedef float glint_f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float glint_bf16lo(uint32_t d) { return __uint_as_float(d << 16); }
 __device__ __forceinline__ float glint_bf16hi(uint32_t d) { return __uint_as_float(d & 0xFFFF0000u); }
