@@ -505,6 +505,9 @@ __global__ __launch_bounds__(256) void k_expand_generic(const uint8_t *__restric
 #ifndef EXPANDR_THREADS
 #define EXPANDR_THREADS 512 /* two per CU (the table's LDS): 14336 x 4096 BF16 32.8 -> 30.8 us against 1024 */
 #endif
+#ifndef EXPANDR_GRID_DIV
+#define EXPANDR_GRID_DIV 2 /* launch the resident grid / this: one workgroup (8 waves) per CU streams best */
+#endif
 #ifndef EXPANDR_HWCVT
 #define EXPANDR_HWCVT 1 /* BF16 by v_cvt_pk_bf16_f32 (RNE); NaN absmax takes the scalar rule */
 #endif
@@ -623,7 +626,7 @@ static int expand_device(const uint8_t *d_hole, const uint8_t *d_plug, const flo
     if (aligned && bs >= 8 && bs <= 2048 && (bs & (bs - 1)) == 0 && n >= 2048 && n / 2048 < (1LL << 30)) {
         n_fast = (n / 2048) * 2048;
         const int64_t nchunks = n_fast / 2048;
-        const int64_t resident = glint_resident_grid((const void *)k_expand_runs<BF16>, EXPANDR_THREADS, 0);
+        const int64_t resident = std::max<int64_t>(1, glint_resident_grid((const void *)k_expand_runs<BF16>, EXPANDR_THREADS, 0) / EXPANDR_GRID_DIV);
         const int64_t wanted = (nchunks + EXPANDR_THREADS / 64 - 1) / (EXPANDR_THREADS / 64);
         const unsigned grid = (unsigned)(wanted < resident ? wanted : resident);
         /* one launch: split into pieces as the encode is, the 525 M-element embedding
