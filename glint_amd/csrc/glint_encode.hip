@@ -503,7 +503,7 @@ __global__ __launch_bounds__(256) void k_expand_generic(const uint8_t *__restric
  * contiguous (f32: two 16-B stores, 2 KiB). Chunks are double-buffered in registers with
  * unconditional (clamped) loads in full rounds. */
 #ifndef EXPANDR_THREADS
-#define EXPANDR_THREADS 512 /* two per CU (the table's LDS): 14336 x 4096 BF16 32.8 -> 30.8 us against 1024 */
+#define EXPANDR_THREADS 512 /* 14336 x 4096 BF16 32.8 -> 30.8 us against 1024 (both two per CU, the table's LDS) */
 #endif
 #ifndef EXPANDR_GRID_DIV
 #define EXPANDR_GRID_DIV 2 /* launch the resident grid / this: one workgroup (8 waves) per CU streams best */
