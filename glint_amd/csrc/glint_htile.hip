@@ -338,6 +338,203 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
     }
 }
 
+/* ------------------------------------- decode GEMV, claimed items, one item in flight */
+/* k_htile_gemv_cu: M = 1, bs = 64, K % 2048 == 0, K <= 32768, aligned. The per-element
+ * work of k_htile_gemv_xreg (x slice in registers, 64-copy cell table, 16 B per lane per
+ * plane per item), with a different split and schedule:
+ *   - an item is (row, K slice of 2048). A workgroup holds G waves per slice (64 S G
+ *     threads) and a contiguous band of rows. Wave (s, g) takes items g and g + G of slice
+ *     s, then claims the slice's next items from an LDS counter. The SIMD arbiter issues for
+ *     the oldest waves first, so waves with equal static shares end far apart; claimed items
+ *     let the favoured waves take more of the band.
+ *   - one item in flight per wave: wait for the item, issue the next item's loads, then
+ *     look up and multiply. A plain read of these bytes streams faster with one 1 KiB piece
+ *     per wave in flight than with two. The next item's byte offsets are formed before the
+ *     wait, so once an item lands the wave's next instructions are its loads, not VALU work
+ *     queued behind older waves' lookups.
+ *   - loads are raw buffer loads over the band: an item past the band's end reads beyond the
+ *     buffer's range, which the hardware drops (no memory request, zeros back), so no load
+ *     sits under a branch and the wait counter tracks exactly one item in flight.
+ *   - each (row, slice) partial has its own LDS slot and the workgroup adds a row's slots in
+ *     a fixed order, so results do not depend on which wave took which item (bit-identical
+ *     to k_htile_gemv_xreg).
+ * Two shapes of launch (template NT):
+ *   - S <= 2 (K <= 4096, the gate/up shape): 512-thread workgroups, two per CU; x and the
+ *     first two items go out together.
+ *   - S > 2 (the down shape): one workgroup of 64 S G <= 1024 threads per CU (the 64 KiB x
+ *     stage keeps a second one off the CU); each wave's x chunk lands before its weight
+ *     loads go out (then its first two items), since x issued together with them is served
+ *     behind the weights of every wave that started earlier (x 1.6 us median into a launch,
+ *     2.6 us at worst).
+ * Measured against k_htile_gemv_xreg in one process (rotated pins): 14336 x 4096 11.68
+ * against 11.94 us, 4096 x 14336 12.00 against 12.75 us. */
+#define GEMV_CU_SMAX 16 /* K <= 32768 */
+#define GEMV_CU_DYN_MAX (28 * 1024) /* bytes of dynamic LDS: the partials, 16 S per row */
+
+template <bool OUT_BF16, int XC, int NT, int XS, bool XFIRST>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_htile_gemv_cu(
+    const uint8_t *__restrict__ hole, const uint8_t *__restrict__ plug, const float *__restrict__ absmax,
+    const glint_u32x4 *__restrict__ x, void *__restrict__ y, int N, int K, int G, int rows_per_wg) {
+    /* One block, so the table sits at LDS offset 0 (a lookup address is then one v_perm). */
+    __shared__ struct __attribute__((aligned(16))) {
+        float ltab[GLINT_LDS_CELLS64_WORDS];
+        glint_u32x4 xs[XS]; /* x as BF16, XS >= K / 8 chunks of 16 B */
+        int claim[GEMV_CU_SMAX];
+    } sh;
+    float *const ltab = sh.ltab;
+    glint_u32x4 *const xs = sh.xs;
+    int *const claim = sh.claim;
+    extern __shared__ __attribute__((aligned(16))) float red[]; /* [rows_per_wg][S][4] */
+    constexpr int EL = 32, Q = EL / 8;
+    const int lane = threadIdx.x & 63;
+    const uint32_t lane4 = GEMV_LANE4(lane);
+    const int S = K >> 11;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int s = w % S, g = w / S;
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int nrows = max(min(rows_per_wg, N - r0), 0);
+
+    /* the band's rows of each plane and of absmax; offsets at or past num_records load zeros */
+    const uint32_t rowb = (uint32_t)K >> 1; /* bytes of a row in each plane */
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(hole + (int64_t)r0 * rowb), (short)0, (int)((uint32_t)nrows * rowb), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(plug + (int64_t)r0 * rowb), (short)0, (int)((uint32_t)nrows * rowb), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(absmax + (int64_t)r0 * (K >> 6)), (short)0, (int)((uint32_t)nrows * (rowb >> 3)), GLINT_BUF_DWORD3);
+    const uint32_t lofs = (uint32_t)(s * 1024 + lane * 16), aofs = (uint32_t)(s * 128 + (lane >> 1) * 4);
+    /* an item's two byte offsets, formed ahead of the wait that precedes its loads */
+    struct Ofs {
+        uint32_t w, a;
+    };
+    auto ofs = [&](int i) -> Ofs { return {(uint32_t)i * rowb + lofs, (uint32_t)i * (rowb >> 3) + aofs}; };
+    auto load_at = [&](Ofs o, GemvRow<EL> &row) {
+        row.h = __builtin_amdgcn_raw_buffer_load_b128(rh, o.w, 0, 2 /* nt */);
+        row.p = __builtin_amdgcn_raw_buffer_load_b128(rp, o.w, 0, 2);
+        row.a = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, o.a, 0, 0));
+    };
+    auto load = [&](int i, GemvRow<EL> &row) { load_at(ofs(i), row); };
+
+    /* loads in the order they are consumed: the cell table (scalar), x, the first items */
+    GemvFill fill;
+    gemv_fill_sload(fill);
+    glint_u32x4 xv[XC];
+#pragma unroll
+    for (int c = 0; c < XC; ++c)
+        xv[c] = x[min((int)threadIdx.x + c * (int)blockDim.x, (K >> 3) - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    if (XFIRST) /* x lands before this wave's weight loads go out */
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0);
+    __builtin_amdgcn_sched_barrier(0);
+    /* items g and g + G of slice s are static and both go out before the barrier that waits
+     * for the table and x, so the stream does not pause while the prologue finishes (the
+     * steady state then keeps one item in flight) */
+    int cur = g, nxt = g + G;
+    GemvRow<EL> bufA, bufB;
+    load(cur, bufA);
+    __builtin_amdgcn_sched_barrier(0);
+    load(nxt, bufB);
+    __builtin_amdgcn_sched_barrier(0);
+    gemv_fill_sstore(ltab, fill);
+#pragma unroll
+    for (int c = 0; c < XC; ++c)
+        if ((int)threadIdx.x + c * (int)blockDim.x < (K >> 3))
+            xs[threadIdx.x + c * blockDim.x] = xv[c];
+    if ((int)threadIdx.x < S)
+        claim[threadIdx.x] = 2 * G;
+    __syncthreads();
+    float xr[EL];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const glint_u32x4 v = xs[(s * 64 + lane) * Q + q];
+        xr[8 * q + 0] = glint_bf16lo(v.x); xr[8 * q + 1] = glint_bf16hi(v.x);
+        xr[8 * q + 2] = glint_bf16lo(v.y); xr[8 * q + 3] = glint_bf16hi(v.y);
+        xr[8 * q + 4] = glint_bf16lo(v.z); xr[8 * q + 5] = glint_bf16hi(v.z);
+        xr[8 * q + 6] = glint_bf16lo(v.w); xr[8 * q + 7] = glint_bf16hi(v.w);
+    }
+    /* The counter's address goes through an empty asm, so the compiler does not see it as
+     * wave-uniform: its atomic optimizer would otherwise rewrite the add into a form that
+     * waits for the result right away. Only lane 0 adds; the result is read one item later,
+     * so its LDS round trip is hidden and no atomic sits among the lookups. */
+    typedef __attribute__((address_space(3))) int lds_int;
+    lds_int *claim_s = (lds_int *)&claim[s];
+    asm volatile("" : "+v"(claim_s));
+    auto claim_one = [&]() -> int {
+        int v = 0;
+        if (lane == 0)
+            v = __hip_atomic_fetch_add(claim_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return v;
+    };
+    int pend = claim_one();
+
+    auto compute = [&](const GemvRow<EL> &row, int item) {
+        float part = 0.0f;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const uint32_t H = gemv_word<EL>(row.h, q), P = gemv_word<EL>(row.p, q);
+            const uint32_t E = glint_codes_even(H, P);
+            const uint32_t O = glint_codes_odd(H, P);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4)), xr[8 * q + 0], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4)), xr[8 * q + 1], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4)), xr[8 * q + 2], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4)), xr[8 * q + 3], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4)), xr[8 * q + 4], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4)), xr[8 * q + 5], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4)), xr[8 * q + 6], part);
+            part = fmaf(glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4)), xr[8 * q + 7], part);
+            if ((q + 1) % GEMV_X_BATCH == 0)
+                __builtin_amdgcn_sched_barrier(0);
+        }
+        float sc = row.a * part;
+        if constexpr (!OUT_BF16)
+            if (!(__builtin_fabsf(row.a) < 0x1p126f)) /* rare: the f32 ABI's per-weight products */
+                sc = gemv_exact_part<EL>(ltab, row, lane4, xr);
+        const float v = glint_row16_sum(sc);
+        if ((lane & 15) == 0)
+            red[(item * S + s) * 4 + (lane >> 4)] = v;
+    };
+    /* first item (landed before the barrier) */
+    if (cur < nrows)
+        compute(bufA, cur);
+    /* steady state: wait for the item in `row` (the only one in flight), send the next
+     * claimed item's loads into `other` (past the band they are dropped by the buffer range
+     * check), compute. Items are claimed in increasing order, so once `nxt` is past the band
+     * every later one is. The loads sit outside any branch and the loop runs in pairs, so the
+     * wait counter tracks exactly one item in flight. */
+    auto step = [&](GemvRow<EL> &row, GemvRow<EL> &other) {
+        cur = nxt;
+        nxt = __builtin_amdgcn_readfirstlane(pend);
+        pend = claim_one();
+        /* the next item's offsets go ahead of the wait, so once `row` lands the wave's next
+         * instructions are the loads themselves, not VALU work queued behind older waves'
+         * lookups */
+        const Ofs o = ofs(nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_at(o, other);
+        __builtin_amdgcn_sched_barrier(0);
+        if (cur < nrows)
+            compute(row, cur);
+    };
+    while (nxt < nrows) {
+        step(bufB, bufA);
+        step(bufA, bufB);
+    }
+    __syncthreads();
+
+    for (int t = threadIdx.x; t < nrows; t += blockDim.x) {
+        const int row = r0 + t;
+        float sum = 0.0f;
+        for (int k = 0; k < S * 4; ++k)
+            sum += red[t * S * 4 + k];
+        if (OUT_BF16)
+            ((uint16_t *)y)[row] = glint_f32_to_bf16(sum);
+        else
+            ((float *)y)[row] = sum;
+    }
+}
+
 /* ------------------------------------------------- small-M decode GEMV (BF16 out) */
 /* k_htile_gemv_mr: M = 2 .. MR rows of x at once (batched decode), bs = 64, K % 2048 == 0,
  * aligned. The layout and row walk of k_htile_gemv_xreg: wave (s, g) streams rows
@@ -754,6 +951,42 @@ static int htile_launch_gemv_xreg(const uint8_t *hole, const uint8_t *plug, cons
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
+/* k_htile_gemv_cu over an M = 1 GEMV (bs 64, K % 2048 == 0, aligned): at S <= 2 slices two
+ * 512-thread workgroups per CU, at S > 2 one of up to 1024 threads; a band of
+ * ceil(N / workgroups) rows each. Returns 1 where the shape does not fit its plan (the caller
+ * then takes k_htile_gemv_xreg), else 0 or -3. */
+#ifndef GEMV_CU_ON
+#define GEMV_CU_ON 1
+#endif
+#define GEMV_CU_NARROW_DYN_MAX (7 * 1024) /* two 512-thread workgroups (72 KiB static each) per CU */
+template <bool OUT_BF16>
+static int htile_launch_gemv_cu(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x,
+                                void *y, int N, int K, hipStream_t st) {
+    if (!GEMV_CU_ON || K % 2048 != 0)
+        return 1;
+    const int S = K / 2048;
+    if (S > GEMV_CU_SMAX)
+        return 1;
+    const bool narrow = S <= 2;
+    const int G = (narrow ? 8 : 16) / S; /* waves per slice */
+    const int wgs = glint_cu_count() * (narrow ? 2 : 1);
+    const int64_t rows = ((int64_t)N + wgs - 1) / wgs;
+    const size_t lds = (size_t)rows * S * 16; /* the row partials */
+    if (lds > (narrow ? GEMV_CU_NARROW_DYN_MAX : GEMV_CU_DYN_MAX) || rows * (K / 2) >= ((int64_t)1 << 31))
+        return 1;
+    const unsigned grid = (unsigned)(((int64_t)N + rows - 1) / rows);
+    const int threads = 64 * S * G;
+    /* x staging: K / 8 chunks of 16 B over `threads` threads, XC chunks each */
+    auto kern = narrow ? k_htile_gemv_cu<OUT_BF16, 1, 512, 512, false>
+                       : (G >= 4 ? k_htile_gemv_cu<OUT_BF16, 1, 1024, GEMV_CU_SMAX * 256, true>
+                                 : (G >= 2 ? k_htile_gemv_cu<OUT_BF16, 2, 1024, GEMV_CU_SMAX * 256, true>
+                                           : k_htile_gemv_cu<OUT_BF16, 4, 1024, GEMV_CU_SMAX * 256, true>));
+    if (glint_set_lds_limit((const void *)kern, GEMV_CU_DYN_MAX) != 0)
+        return -3;
+    kern<<<grid, threads, lds, st>>>(hole, plug, absmax, (const glint_u32x4 *)x, y, N, K, G, (int)rows);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
 /* f32 output at M > 1 (the reference ABI's prefill use): 3-plane k_tile_mfma, whose
  * products are exact and whose sums are f32. 128 x 128 tiles over 8 waves (2 x 4, wave tile
  * 64 x 32) fill the 160 KiB of LDS: x 32 KiB, three W planes 96 KiB, cell table 32 KiB;
@@ -798,8 +1031,10 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         return M2 >= 2 ? htile_launch_gemv_mr<true>(hole, plug, absmax, x2, y2, M2, N, K, st)
                        : htile_launch_gemv_xreg<false>(hole, plug, absmax, x2, y2, N, K, st);
     }
-    if (gemv_x_ok)
-        return htile_launch_gemv_xreg<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);
+    if (gemv_x_ok) {
+        const int rc = htile_launch_gemv_cu<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);
+        return rc != 1 ? rc : htile_launch_gemv_xreg<OUT_BF16>(hole, plug, absmax, x, y, N, K, st);
+    }
     if (mfma_ok && OUT_BF16) {
         const GlintTileProducer p{(const glint_u32x2 *)hole, (const glint_u32x2 *)plug, absmax, N, K, nullptr};
         const uint16_t *xb = (const uint16_t *)x;
