@@ -37,9 +37,35 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def timed(torch, fns, steps: int, warmup: int) -> float:
-    """Average ms per call over `steps` calls (cycling through fns), HIP events on the
-    current stream bracketing the whole timed loop."""
+def timed(torch, fns, steps: int, warmup: int, lead: int = 4) -> float:
+    """Average ms per call over exactly `steps` calls (cycling through fns), HIP events on
+    the current stream bracketing them, the device synchronized before and after.
+
+    The warmup calls (at least `lead`) are queued after the first synchronize and the start
+    event is recorded behind them, so the timed window opens when the GPU finishes the last
+    warmup call and holds the `steps` calls back to back, with the host already ahead of
+    the GPU. Recording the start event on an idle GPU instead puts the host's latency for
+    the first timed call (a few microseconds of Python, ctypes and launch) inside the
+    window, which at 20 steps of a 12 us kernel is 2-4% of the figure."""
+    torch.cuda.synchronize()
+    n = len(fns)
+    w = max(warmup, lead)
+    for i in range(w):
+        fns[i % n]()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        fns[(w + i) % n]()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def timed_sync_first(torch, fns, steps: int, warmup: int) -> float:
+    """The same loop with the start event recorded on an idle GPU (synchronize, then
+    record, then launch): the host's first-launch latency falls inside the window. Kept
+    beside `timed` so both figures are on the line."""
     for i in range(warmup):
         fns[i % len(fns)]()
     torch.cuda.synchronize()
@@ -113,8 +139,10 @@ def bench_gemv(torch, H, steps, warmup, headline_only=False):
     fns = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, y, 1, N, K, 64, st) for p in pins]
     settle(torch, fns, 0.2)
     ms = timed(torch, fns, steps, warmup)
+    ms_sync_first = timed_sync_first(torch, fns, steps, warmup)
     if headline_only:
-        return {"ms": ms, "bytes": per, "gbs": per / ms / 1e6, "copies": copies, "rotation_bytes": copies * per}, pins, x
+        return {"ms": ms, "bytes": per, "gbs": per / ms / 1e6, "copies": copies, "rotation_bytes": copies * per,
+                "ms_sync_first": ms_sync_first}, pins, x
     yf = torch.empty(N, dtype=torch.float32, device="cuda")
     fns32 = [bound(lib.launch_glint_htile_s3_f32_stream, p[0], p[1], p[2], x, yf, 1, N, K, 64, st) for p in pins]
     ms32 = timed(torch, fns32, steps, warmup)
@@ -132,7 +160,7 @@ def bench_gemv(torch, H, steps, warmup, headline_only=False):
     del pins_d
     return {
         "ms": ms, "bytes": per, "gbs": per / ms / 1e6, "copies": copies, "rotation_bytes": copies * per,
-        "f32_out_ms": ms32, "f32_out_gbs": gemv_bytes(N, K, 4) / ms32 / 1e6,
+        "ms_sync_first": ms_sync_first, "f32_out_ms": ms32, "f32_out_gbs": gemv_bytes(N, K, 4) / ms32 / 1e6,
         "down_4096x14336_ms": msd, "down_4096x14336_gbs": gemv_bytes(4096, 14336) / msd / 1e6,
     }, pins, x
 
@@ -514,6 +542,35 @@ def bench_copy_ceiling(torch, mib: int = 1024):
     ms = timed(torch, [lambda: dst.copy_(src)], 20, 3)
     del src, dst
     return {"bytes_moved": 2 * n, "ms": ms, "gbs": 2 * n / ms / 1e6, "frac": 2 * n / ms / 1e6 / HBM_PEAK_GBS}
+
+
+def bench_read_ceiling(torch, H, steps: int):
+    """Read-only HBM ceilings from libglint_probe's grid-stride read (no writes):
+    - `stream_1gib`: one 1 GiB buffer per launch, the steady streaming rate;
+    - `gemv_sized`: 62.43 MB buffers (the 14336 x 4096 GEMV's bytes) rotated over more than
+      1 GiB, the same launch size and rotation as the headline, so launch cost and ramp are
+      in it: the practical floor for the headline GEMV, which also computes and writes y."""
+    import ctypes
+    lib = H.probe_lib().glint_probe_read
+    st = stream_handle(torch)
+    grid = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.empty(grid * 1024, dtype=torch.int32, device="cuda")
+    big = torch.ones(1 << 30, dtype=torch.uint8, device="cuda")
+    ms_big = timed(torch, [bound(lib, big, ctypes.c_int64(big.numel()), sink, grid, st)], 20, 3)
+    del big
+    per = int(gemv_bytes(GEMV_N, GEMV_K)) // 16 * 16
+    copies = max(17, int(1.05 * 2 ** 30 / per) + 1)
+    bufs = [torch.ones(per, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    fns = [bound(lib, b, ctypes.c_int64(per), sink, grid, st) for b in bufs]
+    settle(torch, fns, 0.1)
+    ms = timed(torch, fns, steps, 10)
+    del bufs
+    torch.cuda.empty_cache()
+    return {"stream_1gib": {"bytes": 1 << 30, "ms": ms_big, "gbs": (1 << 30) / ms_big / 1e6,
+                            "frac": (1 << 30) / ms_big / 1e6 / HBM_PEAK_GBS},
+            "gemv_sized": {"bytes": per, "copies": copies, "ms": ms, "gbs": per / ms / 1e6,
+                           "frac": per / ms / 1e6 / HBM_PEAK_GBS},
+            "grid": f"{grid} x 1024 threads, grid-stride 16-B nontemporal loads"}
 
 
 def bench_pin_tools(tensors: int = 16):
@@ -1013,6 +1070,9 @@ def main() -> int:
         if "copy" in parts:
             extra["hbm_copy_1gib"] = bench_copy_ceiling(torch)
             log(f"device copy 1 GiB {extra['hbm_copy_1gib']['gbs']:.0f} GB/s (read + write)")
+            extra["hbm_read"] = bench_read_ceiling(torch, H, args.steps)
+            log(f"read ceiling: 1 GiB {extra['hbm_read']['stream_1gib']['gbs']:.0f} GB/s, GEMV-sized "
+                f"{extra['hbm_read']['gemv_sized']['ms'] * 1e3:.2f} us ({extra['hbm_read']['gemv_sized']['frac']:.3f})")
         if "encode4096" in parts:
             extra["encode_4096x4096"] = bench_encode_4096(torch, H)
             log(f"encode 4096^2 {extra['encode_4096x4096']['encode_bf16_in_gbs']:.0f} GB/s bf16-in")

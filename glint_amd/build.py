@@ -6,6 +6,7 @@
 Outputs (git-ignored, shipped with the tree):
     glint_amd/lib/libglint_encode.so   encode / expand / H-TILE (include/glint_encode.h, glint_htile.h)
     glint_amd/lib/libp7_kernels.so     attach ABI: INT8 GEMM (include/int8_mma_gemm.h, p7_attach.h)
+    glint_amd/lib/libglint_probe.so    bench.py's HBM read ceiling (measurement only)
     oracle/liboracle.so                CPU oracle (tests only)
     tests/native/bin/abi_caller        C++ caller of the C ABI, linked with -lglint_encode (tests only)
 """
@@ -38,6 +39,8 @@ HIP_FLAGS = [
 LIBS = {
     "libglint_encode.so": ["glint_encode.hip", "glint_htile.hip", "glint_select.hip", "glint_noalloc.hip"],
     "libp7_kernels.so": ["int8_mma_gemm.hip", "int8_tile_gemm.hip", "p7_abi.cpp", "glint_plug_streamer.cpp", "p7_selftest.cpp"],
+    # measurement only (bench.py's read ceiling), not part of the GLINT ABI
+    "libglint_probe.so": ["hbm_probe.hip"],
 }
 
 

@@ -236,15 +236,23 @@ __device__ __forceinline__ int glint_max8(int v) {
     return v;
 }
 
-/* Sum over the 64 lanes of a wave; every lane gets the total. */
+/* v + (v of the lane CTRL names), as one v_add_f32 with a DPP source: every lane these
+ * controls name is inside the row, so the old value 0 is never used */
+template <int CTRL>
+__device__ __forceinline__ float glint_add_dpp(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 /* Sum over each row of 16 lanes, left in every lane of the row (DPP only, no LDS). */
 __device__ __forceinline__ float glint_row16_sum(float v) {
-    v += __int_as_float(glint_dpp<GLINT_DPP_QUAD_1032>(__float_as_int(v)));
-    v += __int_as_float(glint_dpp<GLINT_DPP_QUAD_2301>(__float_as_int(v)));
-    v += __int_as_float(glint_dpp<GLINT_DPP_ROW_HALF_MIRROR>(__float_as_int(v)));
-    v += __int_as_float(glint_dpp<GLINT_DPP_ROW_MIRROR>(__float_as_int(v)));
+    v = glint_add_dpp<GLINT_DPP_QUAD_1032>(v);
+    v = glint_add_dpp<GLINT_DPP_QUAD_2301>(v);
+    v = glint_add_dpp<GLINT_DPP_ROW_HALF_MIRROR>(v);
+    v = glint_add_dpp<GLINT_DPP_ROW_MIRROR>(v);
     return v;
 }
+
+/* Sum over the 64 lanes of a wave; every lane gets the total. */
 
 __device__ __forceinline__ float glint_wave_sum(float v) {
 #pragma unroll

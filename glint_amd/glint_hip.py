@@ -139,6 +139,20 @@ def encode_lib() -> ctypes.CDLL:
     return _ENC
 
 
+_PROBE: Optional[ctypes.CDLL] = None
+
+
+def probe_lib() -> ctypes.CDLL:
+    """glint_amd/lib/libglint_probe.so: bench.py's HBM read ceiling (not part of the ABI)."""
+    global _PROBE
+    if _PROBE is None:
+        p = LIB_DIR / "libglint_probe.so"
+        if not p.is_file():
+            raise RuntimeError("libglint_probe.so not built: run `python -m glint_amd.build`")
+        _PROBE = _bind(p, {"glint_probe_read": ([VP, I64, VP, I32, VP], I32)})
+    return _PROBE
+
+
 def p7_lib() -> ctypes.CDLL:
     global _P7
     if _P7 is None:
