@@ -488,6 +488,10 @@ def bench_kmajor(torch, H, steps: int = 200, copies: int = 20):
     idx = torch.empty(K, dtype=torch.int32, device="cuda")
     cnt = torch.empty(1, dtype=torch.int32, device="cuda")
     lib, st = H.encode_lib(), stream_handle(torch)
+    # the fold and the correction add their K slices through the stream's split-K counters
+    # when the stream has a workspace (they never allocate one themselves)
+    if lib.glint_htile_workspace_reserve(st) != 0:
+        raise RuntimeError("glint_htile_workspace_reserve failed")
     ksg, ks, nsel = 16, 8, K // 10
     fold_bytes = N * K / 2 + N * K / 16 + 2 * K + 4 * N
     folds = [bound(lib.glint_gemv_km_fold, pk[0], pk[2], x, y, N, K, ksg, part, st) for pk in pins]

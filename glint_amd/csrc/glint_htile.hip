@@ -998,17 +998,36 @@ static int htile_launch_gemv_cu(const uint8_t *hole, const uint8_t *plug, const 
 #endif
 
 /* `fixed`: the caller's split-K workspace (the no-allocation entry point); null for the
- * stream's own. Returns 0, -1 null pointer, -2 bs <= 0 or K < 1, -3 launch error, -5 the
- * split plan needs more than the fixed workspace holds. */
+ * stream's own. Returns 0, -1 null pointer, -2 bs <= 0, -3 launch error, -5 the split plan
+ * needs more than the fixed workspace holds. K < 1 writes zeros (the empty sum). */
+/* y[0 .. n) = 0 (words of 16 or 32 bits): the K <= 0 result. A kernel, not a memset, so
+ * it can be recorded into a graph. */
+template <typename T>
+__global__ __launch_bounds__(256) void k_htile_zero(T *__restrict__ y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        y[i] = (T)0;
+}
+
 template <bool OUT_BF16>
 static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y, int M,
                         int N, int K, int bs, hipStream_t st, const GlintSplitWs *fixed = nullptr) {
     if (!hole || !plug || !absmax || !x || !y)
         return -1;
-    if (bs <= 0 || K < 1)
+    if (bs <= 0)
         return -2;
     if (M <= 0 || N <= 0)
         return 0;
+    if (K < 1) {
+        /* no k term: every output is the empty sum, 0, as the reference's k loop runs no
+         * iteration and stores its zero accumulators (cuda/glint_htile.cu:141-163) */
+        const int64_t n = (int64_t)M * N;
+        const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
+        if (OUT_BF16)
+            k_htile_zero<uint16_t><<<grid, 256, 0, st>>>((uint16_t *)y, n);
+        else
+            k_htile_zero<float><<<grid, 256, 0, st>>>((float *)y, n);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     const bool fast_ok = bs == 64 && (K % 64) == 0 && glint_aligned(hole, 16) && glint_aligned(plug, 16) &&
                          glint_aligned(absmax, 4) && glint_aligned(x, 16);
     /* M = 1: the x-register GEMV (K <= 32768), else the tiles; M > 1: the small-M GEMV or
@@ -1102,9 +1121,14 @@ GLINT_API int glint_htile_workspace_reserve(struct ihipStream_t *stream) {
     return glint_split_ws_stream((hipStream_t)stream, ws) ? 0 : -1;
 }
 
-/* Library-internal (not exported): the stream's split-K workspace, for the K-major
- * kernels' slice reductions (one workspace cache per library). */
-bool glint_stream_workspace(hipStream_t st, GlintSplitWs *ws) { return glint_split_ws_stream(st, *ws); }
+GLINT_API int glint_htile_workspace_release(struct ihipStream_t *stream) {
+    return glint_split_ws_release((hipStream_t)stream);
+}
+
+/* Library-internal (not exported): the stream's split-K workspace if it already has one,
+ * for the K-major kernels' slice reductions; never allocates (one workspace cache per
+ * library). */
+bool glint_stream_workspace(hipStream_t st, GlintSplitWs *ws) { return glint_split_ws_stream(st, *ws, false); }
 
 /* Library-internal (not exported): the BF16-out launch with the caller's split-K
  * workspace in place of the stream's own. Used by the no-allocation entry point. */

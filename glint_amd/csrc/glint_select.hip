@@ -572,9 +572,10 @@ static int km_launched() { return hipGetLastError() == hipSuccess ? 0 : -3; }
 
 bool glint_stream_workspace(hipStream_t st, GlintSplitWs *ws); /* glint_htile.hip */
 
-/* Arrival counters for `blocks` row blocks: the stream's split-K workspace counters (zero
- * between launches), or null when the stream has none (a capture on a stream that never
- * ran a split launch) or too few: the slices then meet in k_km_combine. */
+/* Arrival counters for `blocks` row blocks: the split-K workspace counters (zero between
+ * launches) of a stream that already has a workspace, or null when it has none (these
+ * calls never allocate one: glint_htile_workspace_reserve or an earlier split launch
+ * provides it) or too few: the slices then meet in k_km_combine. */
 static unsigned *km_counters(hipStream_t st, unsigned blocks) {
     GlintSplitWs ws;
     if (!glint_stream_workspace(st, &ws) || ws.nctr < blocks)

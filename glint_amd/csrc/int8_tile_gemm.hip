@@ -370,3 +370,5 @@ GLINT_API int int8_tile_gemm_bf16(const void *x_bf16, Int8PinLinear w, float *y,
     }
     return (int)hipGetLastError();
 }
+
+GLINT_API int int8_tile_gemm_workspace_release(hipStream_t stream) { return glint_split_ws_release(stream); }

@@ -854,55 +854,115 @@ static __global__ void k_glint_zero_u32(unsigned *p, size_t n) {
         p[i] = 0u;
 }
 
-/* The split-K workspace of a stream on the current device, allocated once at full
- * capacity (hipMalloc; its counters zeroed by a kernel on `st`) and never grown or freed,
- * so a pointer a graph captured stays valid. A launch that is being captured binds the
- * stream's existing workspace and marks it as owned by the graph: the next eager launch on
- * that stream allocates a fresh one, so graph replays and eager calls never share counters.
- * A capture on a stream that has no workspace yet cannot allocate one (the launch then
- * runs unsplit): make one eager call, or call the library's workspace reserve, first.
+/* The split-K workspaces of a stream on the current device: at most two, each allocated
+ * once at full capacity (hipMalloc; its counters zeroed by a kernel on `st`) and never
+ * grown:
+ *   - the eager one, used by launches that are not being captured;
+ *   - the graph one, bound by every launch captured on the stream. The first capture takes
+ *     the stream's eager workspace over as the graph one (the next eager launch allocates a
+ *     fresh eager one), later captures bind the same graph workspace. So replays and eager
+ *     calls never share counters, graphs captured on one stream share theirs (their replays
+ *     must not overlap one another), and capture -> eager cycles allocate nothing after the
+ *     first.
+ * A capture on a stream that has neither cannot allocate (the launch then runs unsplit):
+ * make one eager call, or call the library's workspace reserve, first. `may_alloc` false:
+ * return a workspace only if the stream already has one (never allocates).
  * hipStreamPerThread is keyed by host thread, since each thread's per-thread stream is a
- * different queue behind the same handle. Returns false if no workspace can be had. */
-static inline bool glint_split_ws_stream(hipStream_t st, GlintSplitWs &ws) {
-    struct Entry {
-        char *base;
-        bool captured;
-    };
+ * different queue behind the same handle. glint_split_ws_release frees both. Returns false
+ * if no workspace can be had. */
+struct GlintSplitWsEntry {
+    char *eager = nullptr, *graph = nullptr;
+};
+static inline std::mutex &glint_split_ws_mu() {
     static std::mutex mu;
-    static std::unordered_map<uint64_t, Entry> cache;
+    return mu;
+}
+static inline std::unordered_map<uint64_t, GlintSplitWsEntry> &glint_split_ws_cache() {
+    static std::unordered_map<uint64_t, GlintSplitWsEntry> cache;
+    return cache;
+}
+static inline bool glint_split_ws_key(hipStream_t st, uint64_t &key) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess)
         return false;
-    uint64_t key = (uint64_t)(uintptr_t)st;
+    key = (uint64_t)(uintptr_t)st;
     if (st == hipStreamPerThread)
         key = (uint64_t)std::hash<std::thread::id>{}(std::this_thread::get_id()) | 1u; /* handles are even */
     key = key * 131u + (uint64_t)dev;
+    return true;
+}
+static inline size_t glint_split_ws_bytes(size_t &cb, size_t &nctr, size_t &part_floats) {
+    const size_t cus = (size_t)glint_cu_count();
+    nctr = 2 * cus;
+    part_floats = cus * GLINT_SPLIT_TILE_FLOATS_MAX;
+    cb = glint_split_ctr_bytes(nctr);
+    return cb + part_floats * sizeof(float);
+}
+static inline bool glint_split_ws_stream(hipStream_t st, GlintSplitWs &ws, bool may_alloc = true) {
+    uint64_t key = 0;
+    if (!glint_split_ws_key(st, key))
+        return false;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cap) != hipSuccess)
         return false;
-    const size_t cus = (size_t)glint_cu_count();
-    const size_t nctr = 2 * cus, part_floats = cus * GLINT_SPLIT_TILE_FLOATS_MAX;
-    const size_t cb = glint_split_ctr_bytes(nctr);
-    std::lock_guard<std::mutex> lock(mu);
-    Entry &e = cache[key];
+    size_t cb = 0, nctr = 0, part_floats = 0;
+    const size_t bytes = glint_split_ws_bytes(cb, nctr, part_floats);
+    std::lock_guard<std::mutex> lock(glint_split_ws_mu());
+    GlintSplitWsEntry &e = glint_split_ws_cache()[key];
+    char *base = nullptr;
     if (cap != hipStreamCaptureStatusNone) {
-        if (e.base == nullptr)
-            return false;
-        e.captured = true;
-    } else if (e.base == nullptr || e.captured) {
-        /* a captured workspace stays allocated: the graph that bound it may be replayed */
-        char *b = nullptr;
-        if (hipMalloc((void **)&b, cb + part_floats * sizeof(float)) != hipSuccess)
-            return false;
-        k_glint_zero_u32<<<1, 256, 0, st>>>((unsigned *)b, cb / sizeof(unsigned));
-        if (hipGetLastError() != hipSuccess) {
-            (void)hipFree(b); /* nothing was enqueued on it */
-            return false;
+        if (e.graph == nullptr) {
+            e.graph = e.eager; /* may be null: then the capture runs unsplit */
+            e.eager = nullptr;
         }
-        e = Entry{b, false};
+        base = e.graph;
+    } else {
+        if (e.eager == nullptr && may_alloc) {
+            char *b = nullptr;
+            if (hipMalloc((void **)&b, bytes) != hipSuccess)
+                return false;
+            k_glint_zero_u32<<<1, 256, 0, st>>>((unsigned *)b, cb / sizeof(unsigned));
+            if (hipGetLastError() != hipSuccess) {
+                (void)hipFree(b); /* nothing was enqueued on it */
+                return false;
+            }
+            e.eager = b;
+        }
+        base = e.eager;
     }
-    ws = GlintSplitWs{(float *)(e.base + cb), (unsigned *)e.base, part_floats, nctr};
+    if (base == nullptr)
+        return false;
+    ws = GlintSplitWs{(float *)(base + cb), (unsigned *)base, part_floats, nctr};
     return true;
+}
+
+/* Frees the stream's workspaces (after waiting for the stream). Graphs captured on the
+ * stream before the call must not be replayed after it. Not during capture. Returns 0, -1
+ * if the stream is capturing or the runtime fails. */
+static inline int glint_split_ws_release(hipStream_t st) {
+    uint64_t key = 0;
+    if (!glint_split_ws_key(st, key))
+        return -1;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+        return -1;
+    if (hipStreamSynchronize(st) != hipSuccess)
+        return -1;
+    GlintSplitWsEntry e;
+    {
+        std::lock_guard<std::mutex> lock(glint_split_ws_mu());
+        auto it = glint_split_ws_cache().find(key);
+        if (it == glint_split_ws_cache().end())
+            return 0;
+        e = it->second;
+        glint_split_ws_cache().erase(it);
+    }
+    int rc = 0;
+    if (e.eager && hipFree(e.eager) != hipSuccess)
+        rc = -1;
+    if (e.graph && hipFree(e.graph) != hipSuccess)
+        rc = -1;
+    return rc;
 }
 
 /* Splits of K for a grid of `tiles` output tiles when `slots` workgroups should run at

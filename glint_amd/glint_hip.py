@@ -58,6 +58,7 @@ _ENCODE_SIGS = {
     "launch_glint_htile_s3_f32": ([VP, VP, VP, VP, VP, I32, I32, I32, I32], I32),
     "launch_glint_htile_bf16_stream": ([VP, VP, VP, VP, VP, I32, I32, I32, I32, VP], I32),
     "glint_htile_workspace_reserve": ([VP], I32),
+    "glint_htile_workspace_release": ([VP], I32),
     "launch_glint_htile_bf16_stream_noalloc": ([VP, VP, VP, VP, VP, I32, I32, I32, I32, VP], I32),
     "glint_kmajor_pack": ([VP, VP, VP, I32, I32, VP, VP, VP, VP], I32),
     "glint_gemv_km_fold": ([VP, VP, VP, VP, I32, I32, I32, VP, VP], I32),
@@ -93,6 +94,7 @@ _P7_SIGS = {
     "p7_int8_gemm_flat": ([VP, VP, VP, I32, I32, VP, I32, VP, VP, VP], I32),
     "p7_int8_gemm_plug_flat": ([VP, VP, VP, VP, VP, I32, I32, VP, I32, VP, VP, VP], I32),
     "int8_tile_gemm_bf16": ([VP, Int8PinLinear, VP, I32, VP], I32),
+    "int8_tile_gemm_workspace_release": ([VP], I32),
     "glint_int8_gemm_i32": ([VP, VP, VP, I32, I32, I32, VP], I32),
     "glint_int8_gemm_scaled_bf16": ([VP, VP, VP, VP, VP, I32, I32, I32, VP], I32),
     "glint_plug_streamer_create": ([_c.POINTER(VP), I32, _c.POINTER(_c.c_uint64), VP, VP], I32),

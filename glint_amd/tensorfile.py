@@ -121,6 +121,20 @@ class TensorFile:
         self.close()
 
 
+def _umask() -> int:
+    """The process umask, read without changing it (Linux /proc); elsewhere set and restored."""
+    try:
+        with open("/proc/self/status") as fh:
+            for line in fh:
+                if line.startswith("Umask:"):
+                    return int(line.split()[1], 8)
+    except OSError:
+        pass
+    mask = os.umask(0o022)
+    os.umask(mask)
+    return mask
+
+
 def save(path: str | os.PathLike, items: Sequence[Tuple[str, str, Sequence[int], object]],
          meta: Optional[Mapping[str, str]] = None) -> int:
     """Write (name, dtype, shape, bytes-like) items in order; returns the data bytes
@@ -147,6 +161,9 @@ def save(path: str | os.PathLike, items: Sequence[Tuple[str, str, Sequence[int],
     dest.parent.mkdir(parents=True, exist_ok=True)
     fd, tmp = tempfile.mkstemp(prefix=dest.name + ".", suffix=".part", dir=dest.parent)
     try:
+        # mkstemp creates the file 0600; give it the mode open(path, "wb") would (0666 less
+        # the umask), so a pin converted by one user stays readable by the serving user
+        os.fchmod(fd, 0o666 & ~_umask())
         with os.fdopen(fd, "wb") as fh:
             fh.write(len(head).to_bytes(8, "little"))
             fh.write(head)

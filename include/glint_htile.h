@@ -17,9 +17,11 @@ struct ihipStream_t;
  * At M > 1 with blocksize 64, K % 64 == 0 and aligned pointers the products run on BF16
  * MFMA with each f32 weight split exactly into three BF16 planes (the sum differs from a
  * sequential f32 sum only in order); M = 1 is the f32 GEMV (K <= 32768; larger K takes
- * the MFMA route), other shapes a generic kernel. Enqueued on `stream`; y is overwritten. Returns 0, -1 for a null pointer,
- * -2 for blocksize <= 0 (or K < 1), -3 for a launch error. The MFMA route uses the
- * stream's split-K workspace as launch_glint_htile_bf16_stream does.
+ * the MFMA route), other shapes a generic kernel. Enqueued on `stream`; y is overwritten
+ * (with zeros when K <= 0: the empty sum, as in the reference). Returns 0, -1 for a null
+ * pointer, -2 for blocksize <= 0, -3 for a launch error; M <= 0 or N <= 0 launches nothing
+ * and returns 0. The MFMA route uses the stream's split-K workspace as
+ * launch_glint_htile_bf16_stream does.
  * Reference: include/glint_htile.h:11-14 (cuda/glint_htile.cu:165-180). */
 int launch_glint_htile_s3_f32_stream(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax,
                                      const void *d_x_bf16, float *d_y,
@@ -35,14 +37,16 @@ int launch_glint_htile_s3_f32(const uint8_t *d_hole, const uint8_t *d_plug, cons
  * BF16 MFMA on LDS-dequantized weight tiles). Contract: within
  * 1e-2 relative Frobenius error of an f32 GEMM on the expanded weights; results are
  * deterministic (split K adds its partial tiles in a fixed order).
- * Split-K workspace (M > 1 on the MFMA routes, both outputs): one per (device, stream),
- * allocated at full size (CUs x 256 KiB of partials plus counters, 64 MiB on MI355X) by
- * the first call that splits, its counters zeroed by a kernel on the stream, never grown
- * or freed. hipStreamPerThread gets one per host thread. A launch captured into a graph
- * keeps the workspace it bound for the graph; the next eager call on that stream gets a
- * fresh one, so replays and eager calls never share counters. Replays of graphs captured
- * on one stream share that workspace and must not overlap one another. A capture on a
- * stream with no workspace yet runs unsplit. Same return codes. */
+ * Split-K workspace (M > 1 on the MFMA routes, both outputs): at most two per (device,
+ * stream), each allocated once at full size (CUs x 256 KiB of partials plus counters,
+ * 64 MiB on MI355X), its counters zeroed by a kernel on the stream, never grown; freed by
+ * glint_htile_workspace_release. The eager one is allocated by the first call that
+ * splits. The first launch captured into a graph takes it over as the stream's graph
+ * workspace, which every later capture on that stream binds too; the next eager call gets
+ * a fresh eager one. So replays and eager calls never share counters, replays of graphs
+ * captured on one stream share theirs and must not overlap one another, and capture ->
+ * eager cycles allocate nothing after the first. hipStreamPerThread gets its own per host
+ * thread. A capture on a stream with no workspace yet runs unsplit. Same return codes. */
 int launch_glint_htile_bf16_stream(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax,
                                    const void *d_x_bf16, uint16_t *d_y_bf16,
                                    int M, int N, int K, int blocksize, struct ihipStream_t *stream);
@@ -50,6 +54,11 @@ int launch_glint_htile_bf16_stream(const uint8_t *d_hole, const uint8_t *d_plug,
  * capture on the stream can split K and no later call allocates. Not during capture.
  * Returns 0, or -1 if it cannot (allocation failed, or the stream is capturing). */
 int glint_htile_workspace_reserve(struct ihipStream_t *stream);
+/* No reference counterpart. Free `stream`'s split-K workspaces (eager and graph), after
+ * waiting for the stream. Graphs captured on the stream before the call must not be
+ * replayed after it; a later call allocates afresh. Not during capture. Returns 0, or -1
+ * if the stream is capturing or the runtime fails. */
+int glint_htile_workspace_release(struct ihipStream_t *stream);
 
 /* No reference counterpart. For callers that cannot allocate (code under graph capture,
  * tight serving loops, harnesses that forbid hipMalloc): launch_glint_htile_bf16_stream

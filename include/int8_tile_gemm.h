@@ -31,11 +31,16 @@ typedef struct {
  * n_out >= 1, k_in >= 1 and any alignment; m == 0 launches nothing.
  * Before checking its arguments it returns, and clears, an error already pending on the
  * calling thread (hipGetLastError), without launching.
- * At m > 4 the first call on a stream at a given size may allocate the stream's split-K
- * workspace (hipMalloc, at most 64 MiB, kept until exit); during graph capture it is not
- * grown and the GEMM runs unsplit. Results are deterministic.
+ * At m > 4 the first call on a stream may allocate the stream's split-K workspace
+ * (hipMalloc, 64 MiB; at most two per stream, the second bound by graph captures, as in
+ * glint_htile.h), kept until int8_tile_gemm_workspace_release; a capture on a stream with
+ * no workspace runs unsplit. Results are deterministic.
  * Reference: include/int8_tile_gemm.h:20-27 (cuda/int8_tile_gemm.cu:169-180). */
 int int8_tile_gemm_bf16(const void *x_bf16, Int8PinLinear w, float *y, int m, struct ihipStream_t *stream);
+/* No reference counterpart. Free `stream`'s W8A16 split-K workspaces after waiting for the
+ * stream (graphs captured on it before must not be replayed after). Not during capture.
+ * Returns 0, or -1 if the stream is capturing or the runtime fails. */
+int int8_tile_gemm_workspace_release(struct ihipStream_t *stream);
 
 #ifdef __cplusplus
 }

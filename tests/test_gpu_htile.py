@@ -9,6 +9,8 @@ f32 ABI (launch_glint_htile_s3_f32[_stream]): the reference's device tests resta
 bf16 path (launch_glint_htile_bf16_stream): rel Frobenius <= 1e-2 vs an f32 GEMM on
   the expanded weights, and far tighter in practice.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -30,6 +32,35 @@ def _kbounds_inputs(M, N, K, bs):
     j = np.arange(M * K, dtype=np.int64)
     x = bf16_bits((((j * 3 + j // 19) % 17) - 8).astype(np.float32) * 0.0625)
     return hole, plug, scales, x
+
+
+@pytest.mark.parametrize("K", [0, -5])
+def test_k_nonpositive_writes_zeros(K):
+    """K <= 0: no k term, so every output is the empty sum. As the reference's launcher
+    (its k loop runs no iteration and stores the zero accumulators,
+    cuda/glint_htile.cu:141-163), y is overwritten with zeros and the call returns 0, for
+    f32 out, BF16 out and the no-allocation entry; M = 0 or N = 0 writes nothing."""
+    torch = torch_cuda()
+    lib = H.encode_lib()
+    M, N = 3, 1000
+    b = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    a = torch.ones(16, dtype=torch.float32, device="cuda")
+    x = torch.zeros(64, dtype=torch.bfloat16, device="cuda")
+    yf = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    yb = torch.full((M, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    yn = torch.full((M, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    assert lib.launch_glint_htile_s3_f32_stream(P(b), P(b), P(a), P(x), P(yf), M, N, K, 64, None) == 0
+    assert lib.launch_glint_htile_bf16_stream(P(b), P(b), P(a), P(x), P(yb), M, N, K, 64, None) == 0
+    assert lib.launch_glint_htile_bf16_stream_noalloc(P(b), P(b), P(a), P(x), P(yn), M, N, K, 64, None) == 0
+    torch.cuda.synchronize()
+    assert (yf == 0).all() and (yb.view(torch.int16) == 0).all() and (yn.view(torch.int16) == 0).all()
+    keep = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    assert lib.launch_glint_htile_s3_f32_stream(P(b), P(b), P(a), P(x), P(keep), 0, N, K, 64, None) == 0
+    assert lib.launch_glint_htile_s3_f32_stream(P(b), P(b), P(a), P(x), P(keep), M, 0, K, 64, None) == 0
+    assert lib.launch_glint_htile_s3_f32_stream(P(b), P(b), P(a), P(x), P(keep), M, N, K, 0, None) == -2
+    torch.cuda.synchronize()
+    assert (keep == 7.0).all()
 
 
 @pytest.mark.parametrize("shift", [0, 1])
@@ -419,3 +450,63 @@ def test_workspace_reserve_entry():
     s = torch.cuda.Stream()
     assert H.encode_lib().glint_htile_workspace_reserve(H._stream(s)) == 0
     assert H.encode_lib().glint_htile_workspace_reserve(H._stream(s)) == 0
+
+
+def test_split_workspace_capture_cycles_bounded(oracle):
+    """Capture -> eager cycles on one stream allocate nothing after the first: every capture
+    binds the stream's one graph workspace and every eager call its one eager workspace, so
+    device memory stays flat over five more cycles; each graph's replays, interleaved with
+    eager split launches on the same stream, equal the eager result bit for bit. Then
+    glint_htile_workspace_release frees both workspaces and a later call allocates afresh
+    with the same result."""
+    torch = torch_cuda()
+    M, N, K = 64, 4096, 14336
+    hole, plug, am = _encoded_weight(oracle, N, K, 3401)
+    g = torch.Generator(device="cuda").manual_seed(3402)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    sh = H._stream(s)
+    lib = H.encode_lib()
+    with torch.cuda.stream(s):
+        want = H.htile_bf16(hole, plug, am, x, N, K, 64, stream=s)
+    outs = [torch.empty(M, N, dtype=torch.bfloat16, device="cuda") for _ in range(6)]
+    eager = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    graphs = []
+    torch.cuda.synchronize()
+    free0 = None
+    for c in range(6):
+        print(f"capture/eager cycle {c}", flush=True)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            H.htile_bf16(hole, plug, am, x, N, K, 64, out=outs[c], stream=s)
+        graphs.append(graph)
+        with torch.cuda.stream(s):
+            H.htile_bf16(hole, plug, am, x, N, K, 64, out=eager, stream=s)
+        torch.cuda.synchronize()
+        assert torch.equal(eager.view(torch.int16), want.view(torch.int16)), c
+        if c == 0:
+            free0 = torch.cuda.mem_get_info()[0]
+    free5 = torch.cuda.mem_get_info()[0]
+    assert free0 - free5 < 16 << 20, (free0 - free5) / 2 ** 20  # without the bound: 5 x 64 MiB
+    for rep in range(2):
+        for c, graph in enumerate(graphs):
+            with torch.cuda.stream(s):
+                outs[c].zero_()
+                graph.replay()
+                H.htile_bf16(hole, plug, am, x, N, K, 64, out=eager, stream=s)
+            torch.cuda.synchronize()
+            assert torch.equal(outs[c].view(torch.int16), want.view(torch.int16)), (rep, c)
+            assert torch.equal(eager.view(torch.int16), want.view(torch.int16)), (rep, c)
+    del graphs
+    torch.cuda.synchronize()
+    before = torch.cuda.mem_get_info()[0]
+    assert lib.glint_htile_workspace_release(sh) == 0
+    after = torch.cuda.mem_get_info()[0]
+    assert after - before >= 100 << 20, (after - before) / 2 ** 20  # the eager and the graph workspace
+    assert lib.glint_htile_workspace_release(sh) == 0  # nothing left: a no-op
+    with torch.cuda.stream(s):
+        again = H.htile_bf16(hole, plug, am, x, N, K, 64, stream=s)
+    torch.cuda.synchronize()
+    assert torch.equal(again.view(torch.int16), want.view(torch.int16))
+    assert lib.glint_htile_workspace_release(sh) == 0

@@ -204,15 +204,54 @@ def test_decode_step_under_graph_capture(oracle):
         want2 = oracle.apply_corr_km(hk, pk, sk, x2, oracle.select_topk(x2, K, K // 10), N, K,
                                      oracle.gemv_km_fold(hk, sk, x2, N, K, ksg), ks)
         for rep in range(3):
-            y.zero_()
-            graph.replay()
+            # the replay and the eager step share `part`: both go on `s`, one after the other
             with torch.cuda.stream(s):
+                y.zero_()
+                graph.replay()
                 e_idx, e_cnt = torch.empty_like(idx), torch.empty_like(cnt)
                 step(dx2, ye, e_idx, e_cnt, s)
             torch.cuda.synchronize()
             assert host(y).tobytes() == want.tobytes(), (warm, rep)
             assert host(ye).tobytes() == want2.tobytes(), (warm, rep)
         del graph
+
+
+def test_fold_and_correction_allocate_nothing(oracle):
+    """The fold and the correction with K slices (ksg, ks > 1) never allocate: on a stream
+    with no split-K workspace they meet their slices in the combine kernel (device memory
+    unchanged), on a stream with one (reserved ahead) through its arrival counters; both
+    equal the oracle bit for bit."""
+    torch = torch_cuda()
+    N, K, ksg, ks = 4096, 14336, 8, 4
+    h, p, am = _pin(oracle, N, K, 41)
+    hk, pk, sk = oracle.kmajor_pack(h, p, am, N, K)
+    dhk, dpk, dsk = dev(hk), dev(pk), dev(sk)
+    x = _x(K, 42)
+    dx = dev(x)
+    idx = oracle.select_topk(x, K, K // 10)
+    fold = oracle.gemv_km_fold(hk, sk, x, N, K, ksg)
+    want = oracle.apply_corr_km(hk, pk, sk, x, idx, N, K, fold, ks)
+    part = torch.empty(32 * N, dtype=torch.float32, device="cuda")
+    y = torch.empty(N, dtype=torch.float32, device="cuda")
+    di, dc = torch.empty(K, dtype=torch.int32, device="cuda"), torch.empty(1, dtype=torch.int32, device="cuda")
+    got_fold = torch.empty_like(y)
+    for reserve in (False, True):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        if reserve:
+            assert H.encode_lib().glint_htile_workspace_reserve(H._stream(s)) == 0
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        with torch.cuda.stream(s):
+            H.gemv_km_fold(dhk, dsk, dx, N, K, ksg, y=y, part=part, stream=s)
+            got_fold.copy_(y)
+            H.select_topk(dx, K // 10, idx=di, cnt=dc, stream=s)
+            H.apply_corr_km(dhk, dpk, dsk, dx, di, dc, y, N, K, ks, part=part, stream=s)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free0, reserve
+        assert host(got_fold).tobytes() == fold.tobytes(), reserve
+        assert host(y).tobytes() == want.tobytes(), reserve
+        assert H.encode_lib().glint_htile_workspace_release(H._stream(s)) == 0
 
 
 def test_argument_codes():

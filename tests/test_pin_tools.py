@@ -42,6 +42,22 @@ def test_container_offsets_are_contiguous_and_header_aligned():
         assert [p.name for p in Path(td).iterdir()] == ["m.safetensors"]  # no temporary file left
 
 
+def test_saved_file_mode_follows_the_umask():
+    """save() writes through a temporary file (mkstemp, mode 0600) and renames it; the file
+    it leaves has the mode a plain open(path, "wb") would give: 0666 less the umask."""
+    import os
+    old = os.umask(0o022)
+    try:
+        with tempfile.TemporaryDirectory() as d:
+            for mask in (0o022, 0o002, 0o077):
+                os.umask(mask)
+                path = Path(d) / f"m{mask:o}.safetensors"
+                save(path, [("w", "F32", [2], np.zeros(2, np.float32))])
+                assert (path.stat().st_mode & 0o777) == (0o666 & ~mask), (oct(mask), oct(path.stat().st_mode))
+    finally:
+        os.umask(old)
+
+
 def test_official_reader_accepts_our_files():
     safetensors = pytest.importorskip("safetensors")
     with tempfile.TemporaryDirectory() as td:
