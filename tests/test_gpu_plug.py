@@ -6,9 +6,15 @@ The INT8 late-plug family is checked bit for bit against the oracle:
 - p7_int8_gemm_plug_flat is the fused kernel with flat arguments;
 - int8_mma_gemm_resolve adds a re-quantized activation residual.
 
-The plug streamer's 2-slot ring is checked in three ways:
+The plug streamer's 2-slot ring is checked in five ways:
 - delayed readers over several passes, with 1, 2, 3 and 8 layers: only 3+ layers can
   observe a refill that skipped its slot_free wait (test_glint_plug_streamer.cu:1-4);
+- poison after release (test_plug_evict_real.cu:1-12): each acquired slot is compared with
+  a resident copy and then overwritten with poison before release, over two passes; the
+  control pass poisons before the compare and must see mismatches;
+- GLINT plug planes streamed into launch_glint_htile_s3_f32_stream over plain, poisoned
+  and delayed passes, bitwise equal to the resident plug (test_streamer_real_weights.cu:
+  1-9, 216-233);
 - the ordering return codes;
 - the attach self-test.
 
@@ -162,6 +168,140 @@ def test_streamer_delayed_readers_see_their_own_layer(n_layers):
         assert st.n_layers == n_layers
         assert st.total_stall_ms >= 0.0
     finally:
+        ps.close()
+
+
+class _DevBytes:
+    """A raw device byte range as a torch tensor view (through __cuda_array_interface__)."""
+
+    def __init__(self, ptr, nbytes):
+        self.__cuda_array_interface__ = {"shape": (nbytes,), "typestr": "|u1", "data": (ptr, False), "version": 3,
+                                         "strides": None}
+
+
+def _slot_view(torch, ptr, nbytes):
+    return torch.as_tensor(_DevBytes(ptr, nbytes), device="cuda")
+
+
+def test_streamer_poison_after_release_and_control():
+    """test_plug_evict_real.cu restated on synthetic layers of mixed sizes (>= 64 KiB, one
+    odd): for every layer, acquire, compare the slot byte for byte with a resident copy,
+    overwrite the slot with poison, release, all on the compute stream. If a read ever saw
+    a slot before its copy landed, or a refill overwrote a slot still being read, bytes
+    would differ. Two passes, so a stale slot from pass 1 cannot satisfy pass 2. Control:
+    with the poison moved before the compare, mismatches must appear, or the harness could
+    not see poison at all."""
+    torch = torch_cuda()
+    sizes = [65536, 200_000, 1_048_583, 98_304, 300_000]
+    rng = np.random.default_rng(77)
+    data = [rng.integers(0, 256, n, dtype=np.uint8) for n in sizes]
+    for d in data:
+        d[d == 0xA5] = 0x5A  # no byte equals the poison, so the control counts every byte
+    ref = [dev(d) for d in data]
+    copy_s, comp_s = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    ps = H.PlugStreamer(sizes, copy_s, comp_s)
+    bad = torch.zeros(1, dtype=torch.int64, device="cuda")
+
+    def run_pass(poison_before_read):
+        bad.zero_()
+        torch.cuda.synchronize()
+        assert ps.start() == 0
+        for l, n in enumerate(sizes):
+            rc, ptr = ps.acquire(l)
+            assert rc == 0 and ptr
+            with torch.cuda.stream(comp_s):
+                slot = _slot_view(torch, ptr, n)
+                if poison_before_read:
+                    slot.fill_(0xA5)
+                bad.add_((slot != ref[l]).sum())
+                if not poison_before_read:
+                    slot.fill_(0xA5)
+            assert ps.release(l) == 0
+        torch.cuda.synchronize()
+        return int(bad.item())
+
+    try:
+        for l, d in enumerate(data):
+            assert ps.set_host_data(l, d.tobytes()) == 0
+        for p in range(2):
+            print(f"poison-after-release pass {p}", flush=True)
+            assert run_pass(False) == 0, p
+        print("control pass: poison before the compare", flush=True)
+        assert run_pass(True) == sum(sizes)
+        assert ps.stats().total_h2d_bytes == 3 * sum(sizes)
+    finally:
+        torch.cuda.synchronize()
+        ps.close()
+
+
+def test_streamer_glint_plug_into_htile(oracle):
+    """test_streamer_real_weights.cu restated on synthetic GLINT units: the plug planes of
+    four encoded weights (mixed N, K, bs 64) go through the 2-slot streamer into
+    launch_glint_htile_s3_f32_stream on the compute stream (M = 4), hole and absmax resident.
+    Over six back-to-back passes (plain, plain, poisoned, poisoned, delayed, delayed) every
+    streamed output equals the output of the resident plug bit for bit. A poisoned pass
+    copies random bytes into each released slot on the copy stream behind the release; a
+    delayed pass spins about 1 ms on the compute stream before each launch, so a refill
+    that skipped its slot wait would land under the reader."""
+    torch = torch_cuda()
+    M = 4
+    shapes = [(256, 1024), (512, 2048), (384, 4096), (128, 2048)]
+    rng = np.random.default_rng(91)
+    units = []
+    for i, (N, K) in enumerate(shapes):
+        w = rng.normal(0, 0.02, N * K).astype(np.float32)
+        hole, plug, am = oracle.encode_f32(w, 64)
+        x = bf16_bits(rng.normal(0, 1, M * K).astype(np.float32))
+        units.append(dict(N=N, K=K, hole=dev(hole), plug=plug, dplug=dev(plug), am=dev(am), x=dev(x)))
+    copy_s, comp_s = torch.cuda.Stream(), torch.cuda.Stream()
+    lib = H.encode_lib()
+    cs = H._stream(comp_s)
+
+    def htile(u, plug_ptr, y):
+        assert lib.launch_glint_htile_s3_f32_stream(u["hole"].data_ptr(), plug_ptr, u["am"].data_ptr(),
+                                                    u["x"].data_ptr(), y.data_ptr(), M, u["N"], u["K"], 64, cs) == 0
+
+    torch.cuda.synchronize()
+    resident = []
+    for u in units:
+        y = torch.empty(M * u["N"], dtype=torch.float32, device="cuda")
+        htile(u, u["dplug"].data_ptr(), y)
+        resident.append(y)
+    torch.cuda.synchronize()
+    sizes = [u["plug"].size for u in units]
+    poison = torch.from_numpy(rng.integers(0, 256, max(sizes), dtype=np.uint8)).pin_memory()
+    kinds = ["plain", "plain", "poisoned", "poisoned", "delayed", "delayed"]
+    outs = [[torch.empty(M * u["N"], dtype=torch.float32, device="cuda") for u in units] for _ in kinds]
+    ps = H.PlugStreamer(sizes, copy_s, comp_s)
+    try:
+        for i, u in enumerate(units):
+            assert ps.set_host_data(i, u["plug"].tobytes()) == 0
+        for p, kind in enumerate(kinds):
+            print(f"streamed H-TILE pass {p} ({kind})", flush=True)
+            assert ps.start() == 0
+            assert ps.acquire(1)[0] == -10  # layer 1 before layer 0 is released
+            for i, u in enumerate(units):
+                rc, ptr = ps.acquire(i)
+                assert rc == 0 and ptr
+                if kind == "delayed":
+                    with torch.cuda.stream(comp_s):
+                        torch.cuda._sleep(int(2.4e6))  # a bounded ~1 ms spin
+                htile(u, ptr, outs[p][i])
+                assert ps.release(i) == 0
+                if kind == "poisoned":
+                    ev = torch.cuda.Event()
+                    ev.record(comp_s)
+                    copy_s.wait_event(ev)
+                    with torch.cuda.stream(copy_s):
+                        _slot_view(torch, ptr, sizes[i]).copy_(poison[:sizes[i]], non_blocking=True)
+        torch.cuda.synchronize()
+        for p, kind in enumerate(kinds):
+            for i, u in enumerate(units):
+                got, want = host(outs[p][i]), host(resident[i])
+                assert got.tobytes() == want.tobytes(), (p, kind, i, first_diff(got.view(np.uint32), want.view(np.uint32)))
+    finally:
+        torch.cuda.synchronize()
         ps.close()
 
 
