@@ -711,7 +711,7 @@ def cpu_baseline(seconds_target: float = 24.0):
 
 
 # ---------------------------------------------------------------- profile summaries
-GEMV_KERNEL = "k_htile_gemv_xreg<32,true,"  # headline dispatch (bf16 out), spaces removed
+GEMV_KERNEL = "k_htile_gemv_cu<true,1,512,"  # headline dispatch (bf16 out, 512-thread form), spaces removed
 TRAFFIC_JSON = ROOT / "profiles" / "htile_gemv_m1_14336x4096.traffic.json"
 PMC_CMD = ("rocprofv3 --pmc {ctr} -d <dir> -o run -- python3 bench.py --quick --no-cpu --headline-only "
            "--calibrate-copy --steps 20 --warmup 5")
