@@ -1063,6 +1063,9 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             planned = tile_ss_launch<64, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 1, fixed);
         else if (M < MF2_MIN_M)
             planned = tile_ss_launch<128, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 1, fixed);
+        else if (TILE_BIG && TILE_SK && tile_big_fits(M, N, K) && tile_sk_pays(M, N, K) &&
+                 tile_big_sk_launch<TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, fixed))
+            planned = true;
         else if (TILE_BIG && tile_big_fits(M, N, K) && tile_big_pays(M, N))
             planned = tile_big_launch<TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, fixed);
         else if (TILE_BIG && tile_big_fits(M, N, K) && tile_big_split_fills(M, N, K) &&

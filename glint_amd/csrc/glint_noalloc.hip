@@ -12,9 +12,10 @@
 int glint_htile_bf16_launch_ws(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax, const void *d_x,
                                uint16_t *d_y, int M, int N, int K, int bs, hipStream_t st, const GlintSplitWs *ws);
 
-/* Counters first, then the f32 partial tiles. The size is what a split plan can need on a
+/* Counters first, then the f32 partial tiles. The size is what a K-split plan can need on a
  * 256-CU part: 2 x 256 counters and 256 partial tiles of 256 x 256 (64 MiB). A plan that
- * needs more (a part with more CUs) is refused with -5. */
+ * needs more (a part with more CUs) is refused with -5. Stream-K, which needs twice the
+ * partials, does not fit and those shapes run whole tiles here. */
 #define GLINT_NOALLOC_CTRS 512
 #define GLINT_NOALLOC_CTR_BYTES 4096
 #define GLINT_NOALLOC_PART_FLOATS (256u * GLINT_SPLIT_TILE_FLOATS_MAX)

@@ -331,6 +331,110 @@ __device__ __forceinline__ bool tile_splitk_epilogue(glint_f32x4 (&acc)[NA][NB],
     return true;
 }
 
+/* Stream-K partition of a tile GEMM: the flattened units (tile, K step), tile-major, tiles
+ * numbered row-major over the gx-wide tile grid, are cut into `wgs` contiguous ranges of
+ * equal length (to one unit), workgroup g owning [start(g), start(g + 1)) with start(g) =
+ * floor(g units / wgs). A workgroup walks its range as segments, one per tile it touches:
+ * the tail of one tile, whole tiles, the head of another. Whole tiles are stored directly;
+ * the contributors of a split tile meet through the split-K workspace (tile_sk_fixup).
+ * With one workgroup per CU and units spread evenly, no CU idles while another still has a
+ * tile to finish, whatever the tile count. */
+struct TileSK {
+    int units; /* tiles * nk < 2^31 (the host checks) */
+    int wgs, nk, gx;
+};
+#define TILE_SK_SEGS 3 /* most segments (tiles touched) per workgroup */
+__device__ __forceinline__ int tile_sk_start(const TileSK &sk, int g) {
+    return (int)((int64_t)g * sk.units / sk.wgs);
+}
+/* the workgroup whose range holds unit v: the largest g with start(g) <= v */
+__device__ __forceinline__ int tile_sk_owner(const TileSK &sk, int v) {
+    return (int)(((int64_t)(v + 1) * sk.wgs + sk.units - 1) / sk.units) - 1;
+}
+
+/* Stream-K epilogue of a segment that covers part of tile t (workgroup g). The tile's
+ * contributors are workgroups glo .. ghi (at most CMAX, which the host checks); each that
+ * is not the last to arrive writes its f32 partial to its slot (2 h + e: e = 0 where tile t
+ * holds the start of h's range, else 1, so a workgroup's first and last segments never
+ * share a slot) and counts itself in ctr[glo] (glo's range ends inside t, so no other split
+ * tile uses that counter). A workgroup that finds all others counted skips its own write.
+ * The last adds the partials in contributor order, whichever workgroup it is, so the sum
+ * and the result are deterministic, clears the counter and returns true with the sum in
+ * acc. Ordering and atomics as in tile_splitk_epilogue. s_flag: one word of LDS that
+ * nothing else uses any more; tid: threadIdx.x. */
+template <int NA, int NB, int T, int CMAX>
+__device__ __forceinline__ bool tile_sk_fixup(glint_f32x4 (&acc)[NA][NB], const TileSK &sk, int g, int t,
+                                              float *__restrict__ part, unsigned *ctr, unsigned &s_flag, int tid) {
+    constexpr int NV = NA * NB * 4;
+    const int t0 = t * sk.nk;
+    const int glo = tile_sk_owner(sk, t0), ghi = tile_sk_owner(sk, t0 + sk.nk - 1);
+    const unsigned c = (unsigned)(ghi - glo + 1);
+    unsigned *cnt = ctr + glo;
+    auto slot = [&](int h) -> float * {
+        const int e = tile_sk_start(sk, h) >= t0 ? 0 : 1;
+        return part + (size_t)(2 * h + e) * ((size_t)NV * T);
+    };
+    if (tid == 0)
+        s_flag = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c - 1;
+    __syncthreads();
+    bool last = s_flag != 0;
+    __syncthreads(); /* every thread has read s_flag before it is written again */
+    if (!last) {
+        float *mine = slot(g);
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    __hip_atomic_store(mine + ((a * NB + b) * 4 + i) * T + tid, acc[a][b][i], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0);
+        __syncthreads();
+        if (tid == 0)
+            s_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c - 1;
+        __syncthreads();
+        last = s_flag != 0;
+    }
+    if (!last)
+        return false;
+    /* the other contributors' partials in rounds of CH accumulators, all in flight at once
+     * (other contributor i is contributor i, or i + 1 from the reducer's own index on;
+     * indices past the last contributor are clamped to it, loaded and ignored, so no load
+     * sits under a branch) */
+    constexpr int CH = NV < 16 ? NV : 16, NO = CMAX - 1;
+    const int me = g - glo;
+    const float *src[NO];
+#pragma unroll
+    for (int i = 0; i < NO; ++i)
+        src[i] = slot(glo + min(i < me ? i : i + 1, (int)c - 1));
+#pragma unroll
+    for (int c0 = 0; c0 < NV; c0 += CH) {
+        float v[NO][CH];
+#pragma unroll
+        for (int i = 0; i < NO; ++i)
+#pragma unroll
+            for (int k = 0; k < CH; ++k)
+                v[i][k] = __hip_atomic_load(src[i] + (size_t)(c0 + k) * T + tid, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int e = c0 + k, a = e / (NB * 4), b = (e / 4) % NB, q = e % 4;
+            const float mine = acc[a][b][q];
+            float sum = me == 0 ? mine : v[0][k];
+#pragma unroll
+            for (int j = 1; j < CMAX; ++j)
+                if ((unsigned)j < c)
+                    sum += j == me ? mine : (j < me ? v[j < NO ? j : NO - 1][k] : v[j - 1][k]);
+            acc[a][b][q] = sum;
+        }
+        __builtin_amdgcn_sched_barrier(0); /* one round's loads in flight at a time */
+    }
+    if (tid == 0)
+        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 /* NP = 1: W is one BF16 plane (the BF16-out GEMMs). NP = 3: the producer's finish_split
  * makes three BF16 planes whose sum is the f32 weight exactly, and every x fragment is
  * multiplied with all three (the f32-out H-TILE: f32 products, f32 accumulation). */
@@ -669,10 +773,13 @@ __global__ __launch_bounds__(256, (BM == 64 && P::LDS_WORDS == 0) ? 2 : 1) void 
  * k_tile_mfma (each thread makes 16 weights of two rows, t / 4 and t / 4 + 128). LDS:
  * 2 x 32 KiB of x, 2 x 32 KiB of W, the producer's table (160 KiB in all). The producer
  * must provide row_base / load_at (32-bit row offsets) and REG_WORDS. */
-template <int R, class P, class Out>
+/* SK (CMAX > 0): Stream-K, one workgroup per range of TileSK units (blockIdx.x), the cell
+ * table filled once for all of the workgroup's segments; CMAX bounds a split tile's
+ * contributors. Otherwise one tile (and K split z) per workgroup. */
+template <int R, class P, class Out, int CMAX = 0>
 __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restrict__ x, typename Out::T *__restrict__ y,
                                                   int M, int N, int K, int kps, float *__restrict__ part,
-                                                  unsigned *ctr) {
+                                                  unsigned *ctr, TileSK sk) {
     constexpr int T = 512, BM = 256, BN = 256, TM = 8, TN = 4;
     constexpr int U = (R % 2) ? 2 * R : R;
     static_assert(R >= 2 && R <= 4, "register stages");
@@ -683,24 +790,22 @@ __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restric
     __shared__ __attribute__((aligned(16))) uint16_t sW0[BN * TILE_LDW], sW1[BN * TILE_LDW];
     auto sX = [&](int b) { return b ? sX1 : sX0; };
     auto sW = [&](int b) { return b ? sW1 : sW0; };
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    /* tid, lane, wr and wq are set again at the start of every Stream-K segment from a
+     * value the compiler cannot see through, so what it derives from them (LDS and row
+     * offsets) is recomputed per segment instead of held live through the segment's epilogue */
+    int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 2, wn = wave & 3;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int kb0 = blockIdx.z * kps;
-    const int ns = min(K >> 6, kb0 + kps) - kb0; /* >= 1: the host sizes gridDim.z */
-    const int wr = tid >> 2, wq = tid & 3;
+    /* the segment: output tile at (m0, n0), K steps [kb0, kb0 + ns), ns >= 1 */
+    int m0 = 0, n0 = 0, kb0 = 0, ns = 1;
+    int wr = tid >> 2, wq = tid & 3;
     glint_f32x4 acc[TM][TN];
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b)
-            acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
 
     struct Stage {
         typename P::Regs w[2];
     };
     Stage st[R];
-    const uint32_t wbase[2] = {p.row_base(min(n0 + wr, N - 1)), p.row_base(min(n0 + wr + 128, N - 1))};
+    uint32_t wbase[2];
     auto gload = [&](int j, Stage &sg) {
         const int kb = kb0 + min(j, ns - 1);
         p.load_at(sg.w[0], wbase[0], wq, kb);
@@ -716,12 +821,6 @@ __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restric
     const __amdgpu_buffer_rsrc_t xres =
         __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), GLINT_BUF_DWORD3);
     uint32_t xvo[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int r = 8 * (4 * wave + q) + (lane >> 3);
-        const int chunk = ((lane & 7) ^ (((r >> 1) ^ ((r & 1) << 2)) & 7));
-        xvo[q] = ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)chunk * 8u) * 2u;
-    }
     auto xdma = [&](int j, int buf) {
         const uint32_t kb = (uint32_t)(kb0 + min(j, ns - 1));
 #pragma unroll
@@ -787,47 +886,102 @@ __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restric
         __syncthreads();
     };
 
-    p.setup(ptab, (float *)sX1); /* sX1 is free until step 0's x DMA */
-    xdma(0, 0);
+    /* one segment: accumulators cleared, row offsets, the pipeline filled, the K loop */
+    auto run = [&]() {
 #pragma unroll
-    for (int i = 0; i < R; ++i)
-        gload(i, st[i]);
-    {
-        float v[16];
-        p.lookup(st[0].w[0], v, lane);
-        store_row(0, st[0].w[0], wr, v);
-        p.lookup(st[0].w[1], v, lane);
-        store_row(0, st[0].w[1], wr + 128, v);
-    }
-    gload(R, st[0]);
-    /* only the refill just issued stays outstanding: the loop then enters with the counter
-     * state of its own back edge, and the compiler adds no full wait inside it */
-    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT(2 * P::LOADS));
-    __syncthreads();
-    int j = 0;
-    for (; j + U <= ns; j += U) {
+        for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-            step(j + u, u);
-    }
+            for (int b = 0; b < TN; ++b)
+                acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
+        wbase[0] = p.row_base(min(n0 + wr, N - 1));
+        wbase[1] = p.row_base(min(n0 + wr + 128, N - 1));
 #pragma unroll
-    for (int u = 0; u + 1 < U; ++u)
-        if (j + u < ns)
-            step(j + u, u);
+        for (int q = 0; q < 4; ++q) {
+            const int r = 8 * (4 * wave + q) + (lane >> 3);
+            const int chunk = ((lane & 7) ^ (((r >> 1) ^ ((r & 1) << 2)) & 7));
+            xvo[q] = ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)chunk * 8u) * 2u;
+        }
+        xdma(0, 0);
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+            gload(i, st[i]);
+        {
+            float v[16];
+            p.lookup(st[0].w[0], v, lane);
+            store_row(0, st[0].w[0], wr, v);
+            p.lookup(st[0].w[1], v, lane);
+            store_row(0, st[0].w[1], wr + 128, v);
+        }
+        gload(R, st[0]);
+        /* only the refill just issued stays outstanding: the loop then enters with the
+         * counter state of its own back edge, and the compiler adds no full wait inside it */
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT(2 * P::LOADS));
+        __syncthreads();
+        int j = 0;
+        for (; j + U <= ns; j += U) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                step(j + u, u);
+        }
+#pragma unroll
+        for (int u = 0; u + 1 < U; ++u)
+            if (j + u < ns)
+                step(j + u, u);
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = m0 + wm * TM * 16 + a * 16 + (lane >> 4) * 4 + i;
+                    const int n = n0 + wn * TN * 16 + b * 16 + (lane & 15);
+                    if (m < M && n < N)
+                        Out::store(y, (int64_t)m * N + n, acc[a][b][i]);
+                }
+    };
 
-    if (gridDim.z > 1 && !tile_splitk_epilogue<TM, TN, T>(acc, part, ctr, *(unsigned *)sX0))
-        return;
+    p.setup(ptab, (float *)sX1); /* sX1 is free until step 0's x DMA */
+    if constexpr (CMAX == 0) {
+        m0 = blockIdx.y * BM;
+        n0 = blockIdx.x * BN;
+        kb0 = blockIdx.z * kps;
+        ns = min(K >> 6, kb0 + kps) - kb0; /* >= 1: the host sizes gridDim.z */
+        run();
+        if (gridDim.z > 1 && !tile_splitk_epilogue<TM, TN, T>(acc, part, ctr, *(unsigned *)sX0))
+            return;
+        store_tile();
+    } else {
+        const int g = blockIdx.x;
+        int u = tile_sk_start(sk, g);
+        const int u1 = tile_sk_start(sk, g + 1);
+        /* at most TILE_SK_SEGS segments (the host checks), unrolled: as a loop the compiler
+         * kept more values live through the K loop than the registers hold and spilled
+         * inside it */
 #pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = m0 + wm * TM * 16 + a * 16 + (lane >> 4) * 4 + i;
-                const int n = n0 + wn * TN * 16 + b * 16 + (lane & 15);
-                if (m < M && n < N)
-                    Out::store(y, (int64_t)m * N + n, acc[a][b][i]);
-            }
+        for (int seg = 0; seg < TILE_SK_SEGS; ++seg) {
+            if (u >= u1)
+                break;
+            const int t = u / sk.nk;
+            kb0 = u - t * sk.nk;
+            ns = min(sk.nk - kb0, u1 - u);
+            m0 = (t / sk.gx) * BM;
+            n0 = (t % sk.gx) * BN;
+            u += ns;
+            __syncthreads(); /* the previous segment's last LDS reads (s_flag in sX0) */
+            asm volatile("" : "+v"(tid));
+            lane = tid & 63;
+            wr = tid >> 2;
+            wq = tid & 3;
+            run();
+            /* again after the K loop: the epilogue's offsets are formed here, not held through it */
+            asm volatile("" : "+v"(tid));
+            lane = tid & 63;
+            if (ns == sk.nk || tile_sk_fixup<TM, TN, T, CMAX>(acc, sk, g, t, part, ctr, *(unsigned *)sX0, tid))
+                store_tile();
+        }
+    }
 }
 
 /* ---------------------------------------------------------- split-K host side */
@@ -840,10 +994,12 @@ __global__ __launch_bounds__(512) void k_tile_big(P p, const uint16_t *__restric
 /* A split-K workspace: f32 partial tiles plus one arrival counter per output tile. The
  * counters are zero between launches: the last workgroup of each tile clears its own, so
  * a workspace stays valid as long as every launch that used it ran to completion.
- * Capacity: the 256 x 256 tiles (65536 floats) split only to fill each CU once (tiles x
- * splits <= CUs), the 256 x 128 ones likewise, the smaller ones at most 2 x CUs x 8192
- * floats, so CUs x 65536 floats and 2 x CUs counters always suffice; tile_split_plan checks
- * the plan against the capacity and runs unsplit where it would not fit. */
+ * Capacity: 2 x CUs x 65536 floats and 2 x CUs counters. The 256 x 256 tiles (65536 floats)
+ * split only to fill each CU once (tiles x splits <= CUs), the 256 x 128 ones likewise, the
+ * smaller ones at most 2 x CUs x 8192 floats; Stream-K takes two 256 x 256 partial slots
+ * and one counter per workgroup (one workgroup per CU). tile_split_plan and
+ * tile_big_sk_launch check their plans against the capacity and fall back (unsplit, or
+ * whole tiles) where they would not fit. */
 #define GLINT_SPLIT_TILE_FLOATS_MAX 65536
 static inline size_t glint_split_ctr_bytes(size_t nctr) { return (nctr * sizeof(unsigned) + 255) & ~(size_t)255; }
 
@@ -894,7 +1050,7 @@ static inline bool glint_split_ws_key(hipStream_t st, uint64_t &key) {
 static inline size_t glint_split_ws_bytes(size_t &cb, size_t &nctr, size_t &part_floats) {
     const size_t cus = (size_t)glint_cu_count();
     nctr = 2 * cus;
-    part_floats = cus * GLINT_SPLIT_TILE_FLOATS_MAX;
+    part_floats = 2 * cus * GLINT_SPLIT_TILE_FLOATS_MAX;
     cb = glint_split_ctr_bytes(nctr);
     return cb + part_floats * sizeof(float);
 }
@@ -1041,7 +1197,8 @@ static bool tile_big_launch(const P &p, const uint16_t *x, typename Out::T *y, i
     GlintSplitWs ws;
     if (!tile_split_plan(st, gx, gy, K >> 6, (size_t)256 * 256, kps, ks, ws, 1, fixed))
         return false;
-    k_tile_big<R, P, Out><<<dim3(gx, gy, (unsigned)ks), 512, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
+    k_tile_big<R, P, Out><<<dim3(gx, gy, (unsigned)ks), 512, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr,
+                                                                       TileSK{0, 1, 1, 1});
     return true;
 }
 
@@ -1066,7 +1223,79 @@ static bool tile_big_split_launch(const P &p, const uint16_t *x, typename Out::T
     GlintSplitWs ws;
     if (!tile_split_plan(st, gx, gy, K >> 6, (size_t)256 * 256, kps, ks, ws, 1, fixed) || ks <= 1)
         return false;
-    k_tile_big<R, P, Out><<<dim3(gx, gy, (unsigned)ks), 512, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
+    k_tile_big<R, P, Out><<<dim3(gx, gy, (unsigned)ks), 512, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr,
+                                                                       TileSK{0, 1, 1, 1});
+    return true;
+}
+
+/* Stream-K k_tile_big (TileSK): one workgroup per CU over the 256 x 256 tiles' units. */
+#ifndef TILE_SK
+#define TILE_SK 1 /* 0: never Stream-K; 1: where tile_sk_pays; 2: wherever it can run */
+#endif
+#define TILE_SK_CMAX 4 /* most workgroups sharing one tile */
+/* cmax: the most workgroups one tile can have; segs: the most tiles one workgroup touches
+ * (both 0 where units >= 2^31: no plan) */
+static inline TileSK tile_sk_plan(int64_t tiles, int nk, int gx, int &cmax, int &segs) {
+    const int64_t units = tiles * nk;
+    if (units >= ((int64_t)1 << 31) || units < 1) {
+        cmax = segs = 0;
+        return TileSK{0, 1, 1, 1};
+    }
+    const int wgs = (int)std::min<int64_t>(glint_cu_count(), units);
+    /* ranges are floor(units / wgs) or one more units long: nk units meet at most cmax of
+     * them, and a range meets at most segs tiles */
+    const int64_t len = units / wgs, len_max = (units + wgs - 1) / wgs;
+    cmax = (int)((nk - 1 + len - 1) / len) + 1;
+    segs = (int)((len_max - 1 + nk - 1) / nk) + 1;
+    return TileSK{(int)units, wgs, nk, gx};
+}
+/* Share of the CUs a launch of `wgs` workgroups (one resident per CU, equal work) keeps
+ * busy on average over its rounds. */
+static inline double tile_fill(int64_t wgs) {
+    const int64_t cus = glint_cu_count(), rounds = (wgs + cus - 1) / cus;
+    return (double)wgs / (double)(rounds * cus);
+}
+/* Stream-K against the whole-tile plans the dispatch would otherwise take. Measured on the
+ * 14336 x 4096 and 4096 x 14336 shapes (6 rotated weight copies, one box): a Stream-K K
+ * step costs about 1.2x a whole-tile one, mostly the split tiles' f32 partials going
+ * through memory, so it wins only where the whole tiles leave many CUs idle. M = 1536 gate
+ * (336 tiles, 66% fill) 261 -> 219 us; M = 1536 down (192 256 x 128 tiles, 75%) 257 -> 214
+ * us. It lost at 87.5% fill: M = 1024 gate 137 -> 150 us, M = 2048 gate 268 -> 274 us
+ * (448 tiles), M = 512 gate 92 -> 102 us against the 256 x 128 tiles; and it gains nothing
+ * where a K split already fills the CUs exactly (M = 1024 and 2048 down). */
+static inline bool tile_sk_pays(int M, int N, int K) {
+    if (TILE_SK == 2)
+        return true;
+    const int64_t big = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    if (tile_big_pays(M, N))
+        return tile_fill(big) < 0.7;
+    if (tile_big_split_fills(M, N, K))
+        return false;
+    /* the 256 x 128 tiles with their K split */
+    const int64_t t2 = (int64_t)((M + 255) / 256) * ((N + 127) / 128);
+    const int kps = glint_split_kps(t2, glint_cu_count(), K >> 6, TILE_SPLIT_MIN_STEPS);
+    return tile_fill(t2 * (((K >> 6) + kps - 1) / kps)) < 0.8;
+}
+/* Launches Stream-K k_tile_big; returns false, launching nothing, where the plan does not
+ * fit (more than TILE_SK_CMAX workgroups per tile or TILE_SK_SEGS tiles per workgroup, or
+ * a workspace short of 2 partial tiles per workgroup: a stream being captured without one,
+ * or a `fixed` one that is too small), so the caller takes the whole-tile launch. */
+template <int R, class P, class Out>
+static bool tile_big_sk_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st,
+                               const GlintSplitWs *fixed = nullptr) {
+    const int gx = (N + 255) / 256, gy = (M + 255) / 256;
+    int cmax = 0, segs = 0;
+    const TileSK sk = tile_sk_plan((int64_t)gx * gy, K >> 6, gx, cmax, segs);
+    if (cmax < 1 || cmax > TILE_SK_CMAX || segs > TILE_SK_SEGS)
+        return false;
+    GlintSplitWs ws;
+    const bool got = fixed ? (ws = *fixed, true) : glint_split_ws_stream(st, ws);
+    if (!got || (size_t)2 * sk.wgs * (256 * 256) > ws.part_floats || (size_t)sk.wgs > ws.nctr)
+        return false;
+    if (cmax <= 2)
+        k_tile_big<R, P, Out, 2><<<sk.wgs, 512, 0, st>>>(p, x, y, M, N, K, 0, ws.part, ws.ctr, sk);
+    else
+        k_tile_big<R, P, Out, TILE_SK_CMAX><<<sk.wgs, 512, 0, st>>>(p, x, y, M, N, K, 0, ws.part, ws.ctr, sk);
     return true;
 }
 

@@ -38,8 +38,8 @@ int launch_glint_htile_s3_f32(const uint8_t *d_hole, const uint8_t *d_plug, cons
  * 1e-2 relative Frobenius error of an f32 GEMM on the expanded weights; results are
  * deterministic (split K adds its partial tiles in a fixed order).
  * Split-K workspace (M > 1 on the MFMA routes, both outputs): at most two per (device,
- * stream), each allocated once at full size (CUs x 256 KiB of partials plus counters,
- * 64 MiB on MI355X), its counters zeroed by a kernel on the stream, never grown; freed by
+ * stream), each allocated once at full size (CUs x 512 KiB of partials plus counters,
+ * 128 MiB on MI355X), its counters zeroed by a kernel on the stream, never grown; freed by
  * glint_htile_workspace_release. The eager one is allocated by the first call that
  * splits. The first launch captured into a graph takes it over as the stream's graph
  * workspace, which every later capture on that stream binds too; the next eager call gets
@@ -64,7 +64,9 @@ int glint_htile_workspace_release(struct ihipStream_t *stream);
  * tight serving loops, harnesses that forbid hipMalloc): launch_glint_htile_bf16_stream
  * with the split-K partials and counters in a static per-GPU scratch array of the library
  * (64 MiB plus 4 KiB, held until the process ends) instead of a per-stream workspace. Same
- * kernels, split plan and results; allocates nothing. Calls that overlap on one GPU share
+ * kernels, split plan and results, except where launch_glint_htile_bf16_stream would run
+ * Stream-K (it needs twice the partials): there whole tiles run, within the same contract,
+ * the last bits possibly different. Allocates nothing. Calls that overlap on one GPU share
  * the array and race. Returns the codes above, or -5 when the split plan would need more
  * than the array holds (possible only on a part with more than 256 CUs). */
 int launch_glint_htile_bf16_stream_noalloc(const uint8_t *d_hole, const uint8_t *d_plug, const float *d_absmax,

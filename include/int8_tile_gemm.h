@@ -32,7 +32,7 @@ typedef struct {
  * Before checking its arguments it returns, and clears, an error already pending on the
  * calling thread (hipGetLastError), without launching.
  * At m > 4 the first call on a stream may allocate the stream's split-K workspace
- * (hipMalloc, 64 MiB; at most two per stream, the second bound by graph captures, as in
+ * (hipMalloc, 128 MiB; at most two per stream, the second bound by graph captures, as in
  * glint_htile.h), kept until int8_tile_gemm_workspace_release; a capture on a stream with
  * no workspace runs unsplit. Results are deterministic.
  * Reference: include/int8_tile_gemm.h:20-27 (cuda/int8_tile_gemm.cu:169-180). */

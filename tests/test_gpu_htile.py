@@ -279,6 +279,60 @@ def test_bf16_split_k_workspace_growth(oracle):
     assert torch.equal(res[0].view(torch.int16), res[2].view(torch.int16))
 
 
+# Shapes whose whole-tile plans fill 256 CUs poorly, so they run Stream-K on a 256-CU part:
+# 336 and 330 256 x 256 tiles (two rounds, the second about 1/3 full; 21 and 12.9 K steps per
+# workgroup, so ranges hold up to 3 segments), and two shapes whose 256 x 128 tiles fill 75%
+# and 66% (84 and 42 K steps per workgroup over 96 and 168 256 x 256 tiles: up to 4 and 3
+# workgroups share a tile); ragged M and N in the second and third.
+SK_SHAPES = [(1536, 14336, 1024), (1300, 14000, 640), (1500, 4000, 14336), (768, 14336, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", SK_SHAPES)
+def test_bf16_stream_k(oracle, M, N, K):
+    """Where whole 256 x 256 tiles would leave CUs idle, the tiles run Stream-K: one
+    workgroup per CU over equal ranges of (tile, K step) units, each range cut into
+    segments at tile edges; a tile shared by several workgroups is added up by the last to
+    arrive, in workgroup order. Checked: relative Frobenius error against fp32 on the
+    expanded weights (a lost or doubled segment fails it), every row bounded, bitwise-equal
+    repeats and two streams at once (each with its own workspace), and agreement with the
+    whole-tile kernel (the no-allocation entry: its fixed workspace is too small for the
+    Stream-K plan, so it runs one tile per workgroup) within the same tolerance."""
+    torch = torch_cuda()
+    print(f"stream-K M={M} N={N} K={K}", flush=True)
+    hole, plug, am = _encoded_weight(oracle, N, K, 3205 + K)
+    g = torch.Generator(device="cuda").manual_seed(3206 + M)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    y = H.htile_bf16(hole, plug, am, x, N, K, 64)
+    w = H.expand_f32(hole, plug, am, N * K, 64).reshape(N, K)
+    ref = x.float() @ w.T
+    del w
+    yf = y.float()
+    rel = float(torch.linalg.norm(yf - ref) / torch.linalg.norm(ref))
+    assert rel <= 4e-3, rel
+    row_rel = torch.linalg.norm(yf - ref, dim=1) / torch.linalg.norm(ref, dim=1)
+    assert float(row_rel.max()) <= 1e-2
+    whole = torch.empty_like(y)
+    rc = H.encode_lib().launch_glint_htile_bf16_stream_noalloc(H._p(hole), H._p(plug), H._p(am), H._p(x),
+                                                               H._p(whole), M, N, K, 64, H._stream())
+    assert rc == 0
+    wrel = float(torch.linalg.norm(whole.float() - ref) / torch.linalg.norm(ref))
+    assert wrel <= 4e-3, wrel
+    assert float(torch.linalg.norm(yf - whole.float()) / torch.linalg.norm(ref)) <= 4e-3
+    del ref
+    again = H.htile_bf16(hole, plug, am, x, N, K, 64)
+    assert torch.equal(again.view(torch.int16), y.view(torch.int16))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for s in (s1, s2, s1, s2):
+        with torch.cuda.stream(s):
+            outs.append(H.htile_bf16(hole, plug, am, x, N, K, 64, stream=s))
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o.view(torch.int16), y.view(torch.int16))
+
+
 F32_SHAPES = [(2, 64, 64), (3, 300, 1088), (64, 1024, 4096), (127, 520, 2368), (128, 4096, 576), (300, 1100, 1024),
               (513, 2048, 4096), (64, 4096, 14336), (100, 14336, 4096)]
 
