@@ -889,6 +889,9 @@ __global__ __launch_bounds__(256) void k_htile_generic(const uint8_t *__restrict
 /* Prefill GEMM, large M: the shared double-buffered tile kernel with 256 (M) x 128 (N)
  * blocks over 8 waves in 4 x 2 (wave tile 64 x 64); each thread dequantizes 16 weights
  * (8 B of each plane) per K step through the 32-copy cell table. */
+#ifndef TILE_SS_BN32
+#define TILE_SS_BN32 1 /* M <= 64: 64 x 32 tiles, two workgroups per CU */
+#endif
 #ifndef TILE_RX
 #define TILE_RX 4 /* x register stages of k_tile_ss (M < 256) */
 #endif
@@ -1060,9 +1063,11 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         uint16_t *yb = (uint16_t *)y;
         bool planned;
         if (M <= 64)
-            planned = tile_ss_launch<64, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 1, fixed);
+            planned = TILE_SS_BN32
+                          ? tile_ss_launch<64, 32, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 2, fixed)
+                          : tile_ss_launch<64, 64, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 1, fixed);
         else if (M < MF2_MIN_M)
-            planned = tile_ss_launch<128, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 1, fixed);
+            planned = tile_ss_launch<128, 64, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 1, fixed);
         else if (TILE_BIG && TILE_SK && tile_big_fits(M, N, K) && tile_sk_pays(M, N, K) &&
                  tile_big_sk_launch<TILE_R_BIG, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, fixed))
             planned = true;

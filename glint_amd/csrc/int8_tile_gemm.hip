@@ -326,7 +326,7 @@ static void i8tile_launch_ss(const uint16_t *x, const Int8PinLinear &w, float *y
     const Int8PinTileProducer p{(const glint_u32x4 *)w.q, w.scale, w.n_out, w.k_in};
     for (int64_t r0 = 0; r0 < m; r0 += (int64_t)I8_MAX_YBLOCKS * BM) {
         const int mm = (int)std::min<int64_t>((int64_t)I8_MAX_YBLOCKS * BM, m - r0);
-        tile_ss_launch<BM, 4, Int8PinTileProducer, TileOutF32>(p, x + r0 * w.k_in, y + r0 * w.n_out, mm, w.n_out,
+        tile_ss_launch<BM, 64, 4, Int8PinTileProducer, TileOutF32>(p, x + r0 * w.k_in, y + r0 * w.n_out, mm, w.n_out,
                                                                w.k_in, st, BM == 64 ? I8_SS_PER_CU : 1);
     }
 }

@@ -603,24 +603,27 @@ __global__ __launch_bounds__(64 * WM * WN) void k_tile_mfma(P p, const uint16_t 
             }
 }
 
-/* Tile GEMM for BN = 64 W rows (M up to a few hundred) with the weights streamed in
- * super-steps of 4 K steps (256 elements): per super-step a thread loads 16-B pieces of two
- * W rows such that 8 consecutive lanes cover a whole 128-B line of a plane (P::sload). Loads
- * that cover whole lines stream at about twice the rate of the per-step 8-byte pieces
- * k_tile_mfma uses, which bounded it at small M. The 4 groups of 16 weights a thread holds
- * are dequantized one per K step into a double-buffered 4-step W tile in LDS (super-step
- * s + 1 while s is multiplied); x keeps the per-step ring (RX stages) and double buffer
- * of k_tile_mfma. Block tile BM x 64 over 2 x 2 waves (BM = 64 or 128); W rows 8 w +
- * lane / 8 and 32 more (wave w), piece lane % 8. Clamping and split K as in k_tile_mfma. */
-/* BM = 64 without a producer table: at most 256 VGPRs (two waves per SIMD), so two
- * workgroups fit a CU when the split plan asks for them */
-template <int BM, int RX, class P, class Out>
-__global__ __launch_bounds__(256, (BM == 64 && P::LDS_WORDS == 0) ? 2 : 1) void k_tile_ss(P p, const uint16_t *__restrict__ x, typename Out::T *__restrict__ y,
+/* Tile GEMM for BN = 64 or 32 W rows (M up to a few hundred) with the weights streamed in
+ * super-steps of 4 K steps (256 elements): per super-step a thread loads 16-B pieces of
+ * RR = BN / 32 W rows such that 8 consecutive lanes cover a whole 128-B line of a plane
+ * (P::sload). Loads that cover whole lines stream at about twice the rate of the per-step
+ * 8-byte pieces k_tile_mfma uses, which bounded it at small M. The 2 RR groups of 16
+ * weights a thread holds are dequantized into a double-buffered 4-step W tile in LDS
+ * (super-step s + 1 while s is multiplied): at RR = 2 one group per K step, at RR = 1 one
+ * every other step (looked up in one step, stored in the next). x keeps the per-step ring
+ * (RX stages) and double buffer of k_tile_mfma. Block tile BM x BN over 2 x 2 waves
+ * (BM = 64 or 128); W rows 8 w + lane / 8 (+ 32) of wave w, piece lane % 8. Clamping and
+ * split K as in k_tile_mfma. */
+/* BM = 64 without a producer table, or BN = 32 (80 KiB of LDS with the table): at most 256
+ * VGPRs (two waves per SIMD), so two workgroups fit a CU */
+template <int BM, int BN, int RX, class P, class Out>
+__global__ __launch_bounds__(256, (BN == 32 || (BM == 64 && P::LDS_WORDS == 0)) ? 2 : 1) void k_tile_ss(P p, const uint16_t *__restrict__ x, typename Out::T *__restrict__ y,
                                                  int M, int N, int K, int kps, float *__restrict__ part,
                                                  unsigned *ctr) {
-    constexpr int T = 256, BN = 64, WN = 2, TM = BM / 32, TN = 2, XV = BM * 8 / T;
+    constexpr int T = 256, WN = 2, TM = BM / 32, TN = BN / 32, RR = BN / 32, XV = BM * 8 / T;
     constexpr int U = 8; /* steps per unrolled round: two super-steps, RX | 8 */
-    static_assert((BM == 64 || BM == 128) && (RX == 2 || RX == 4 || RX == 8), "tile shape, x stages");
+    static_assert((BM == 64 || BM == 128) && (BN == 32 || BN == 64) && (RX == 2 || RX == 4 || RX == 8),
+                  "tile shape, x stages");
     __shared__ float ptab[P::LDS_WORDS > 0 ? P::LDS_WORDS : 1];
     __shared__ __attribute__((aligned(16))) uint16_t sX[2][BM * TILE_LDW];
     __shared__ __attribute__((aligned(16))) uint16_t sW[2][4][BN * TILE_LDW];
@@ -631,9 +634,9 @@ __global__ __launch_bounds__(256, (BM == 64 && P::LDS_WORDS == 0) ? 2 : 1) void 
     const int ns = min(K >> 6, kb0 + kps) - kb0; /* >= 1: the host sizes gridDim.z */
     const int last = kb0 + ns - 1;               /* W loads past the split clamp here */
     const int c = lane & 7;
-    int lrow[2], wrow[2];
+    int lrow[RR], wrow[RR];
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
+    for (int rr = 0; rr < RR; ++rr) {
         lrow[rr] = wave * 8 + (lane >> 3) + 32 * rr;
         wrow[rr] = min(n0 + lrow[rr], N - 1);
     }
@@ -645,11 +648,11 @@ __global__ __launch_bounds__(256, (BM == 64 && P::LDS_WORDS == 0) ? 2 : 1) void 
         for (int b = 0; b < TN; ++b)
             acc[a][b] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
 
-    typename P::SRegs sw[2][2]; /* [super-stage][row set] */
+    typename P::SRegs sw[2][RR]; /* [super-stage][row set] */
     glint_u32x4 xs[RX][XV];
-    auto gload_w = [&](int ss, typename P::SRegs (&sg)[2]) {
+    auto gload_w = [&](int ss, typename P::SRegs (&sg)[RR]) {
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr)
+        for (int rr = 0; rr < RR; ++rr)
             p.sload(sg[rr], wrow[rr], kb0 + 4 * ss, c, last);
     };
     auto gload_x = [&](int j, glint_u32x4 (&xg)[XV]) {
@@ -668,7 +671,7 @@ __global__ __launch_bounds__(256, (BM == 64 && P::LDS_WORDS == 0) ? 2 : 1) void 
     /* group t of a super-stage: row set t / 2, half t % 2. The 16-B chunks of W step slot s
      * are additionally XORed with s: the 8 lanes of a store instruction (one row, 4 slots)
      * then hit 8 distinct bank groups, and a fragment read (one slot) is unchanged. */
-    auto finish_w = [&](int buf, const typename P::SRegs (&sg)[2], int t, const float (&v)[16]) {
+    auto finish_w = [&](int buf, const typename P::SRegs (&sg)[RR], int t, const float (&v)[16]) {
         uint32_t pk[8];
         p.sfinish(sg[t >> 1], t & 1, v, pk);
         const int slot = P::sstep(c, t & 1), qq = P::squarter(c, t & 1);
@@ -684,8 +687,12 @@ __global__ __launch_bounds__(256, (BM == 64 && P::LDS_WORDS == 0) ? 2 : 1) void 
     float v[16]; /* table reads of the next group to store */
     auto step = [&](int j, int u) {
         const int t = u & 3, sb = (u >> 2) & 1;
-        typename P::SRegs(&nw)[2] = sw[sb ^ 1];
-        finish_w(sb ^ 1, nw, t, v); /* past the end: clamped data nobody reads */
+        typename P::SRegs(&nw)[RR] = sw[sb ^ 1];
+        /* past the end: clamped data nobody reads */
+        if constexpr (RR == 2)
+            finish_w(sb ^ 1, nw, t, v);
+        else if (t & 1)
+            finish_w(sb ^ 1, nw, t >> 1, v);
         store_x((u & 1) ^ 1, xs[(u + 1) % RX]);
         glint_bf16x8 af[2][TM], bfr[2][TN];
 #pragma unroll
@@ -701,10 +708,14 @@ __global__ __launch_bounds__(256, (BM == 64 && P::LDS_WORDS == 0) ? 2 : 1) void 
                 bfr[ks][b] = __builtin_bit_cast(
                     glint_bf16x8, *(const glint_u32x4 *)(sW[sb][t] + (wn * TN * 16 + b * 16) * TILE_LDW + wofs));
         }
-        if (t < 3)
+        if constexpr (RR == 1) {
+            if (!(t & 1))
+                p.slookup(nw[0], t >> 1, v, lane);
+        } else if (t < 3) {
             p.slookup(nw[(t + 1) >> 1], (t + 1) & 1, v, lane);
-        else
+        } else {
             p.slookup(sw[sb][0], 0, v, lane); /* group 0 of super-step j / 4 + 2 */
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
@@ -727,11 +738,12 @@ __global__ __launch_bounds__(256, (BM == 64 && P::LDS_WORDS == 0) ? 2 : 1) void 
     for (int i = 0; i < RX; ++i)
         gload_x(i, xs[i]);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 2 * RR; ++t) {
         p.slookup(sw[0][t >> 1], t & 1, v, lane);
         finish_w(0, sw[0], t, v);
     }
-    p.slookup(sw[1][0], 0, v, lane);
+    if constexpr (RR == 2)
+        p.slookup(sw[1][0], 0, v, lane);
     gload_w(2, sw[0]);
     store_x(0, xs[0]);
     gload_x(RX, xs[0]);
@@ -1300,15 +1312,15 @@ static bool tile_big_sk_launch(const P &p, const uint16_t *x, typename Out::T *y
 }
 
 /* Launch k_tile_ss over an M x N output. K % 64 == 0, M, N >= 1. */
-template <int BM, int RX, class P, class Out>
+template <int BM, int BN, int RX, class P, class Out>
 static bool tile_ss_launch(const P &p, const uint16_t *x, typename Out::T *y, int M, int N, int K, hipStream_t st,
                            int per_cu = 1, const GlintSplitWs *fixed = nullptr) {
-    const unsigned gx = (unsigned)((N + 63) / 64), gy = (unsigned)((M + BM - 1) / BM);
+    const unsigned gx = (unsigned)((N + BN - 1) / BN), gy = (unsigned)((M + BM - 1) / BM);
     int kps, ks;
     GlintSplitWs ws;
-    if (!tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * 64, kps, ks, ws, per_cu, fixed))
+    if (!tile_split_plan(st, gx, gy, K >> 6, (size_t)BM * BN, kps, ks, ws, per_cu, fixed))
         return false;
-    k_tile_ss<BM, RX, P, Out><<<dim3(gx, gy, (unsigned)ks), 256, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
+    k_tile_ss<BM, BN, RX, P, Out><<<dim3(gx, gy, (unsigned)ks), 256, 0, st>>>(p, x, y, M, N, K, kps, ws.part, ws.ctr);
     return true;
 }
 
