@@ -456,6 +456,9 @@ __global__ __launch_bounds__(512) void k_int8_gemm_256(const int8_t *__restrict_
  * The four A and four B buffers are separate arrays, so the compiler sees that a DMA into
  * one does not alias fragment reads of another. */
 #define G3_NBUF 4
+#ifndef G3_PREFETCH
+#define G3_PREFETCH 1
+#endif
 #ifndef G3_THREADS
 #define G3_THREADS 512
 #endif
@@ -511,6 +514,57 @@ __global__ __launch_bounds__(G3_THREADS) void k_int8_gemm_dma(const int8_t *__re
         }
     };
     const int fr_ofs = g2_lds_ofs(lane & 15, lane >> 4);
+#if G3_PREFETCH
+    /* Fragments one step ahead: step kb multiplies fragments read during step kb - 1 while
+     * it reads step kb + 1's, so no LDS read latency sits between MFMAs. Two register sets
+     * alternate with the step's parity. */
+    struct Frags {
+        glint_i32x4 a[TM], b[TN];
+    };
+    Frags fr[2];
+    auto read_frags = [&](int u, Frags &f) {
+        const int8_t *ta = bufA(u), *tb = bufB(u);
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+            f.b[b] = *(const glint_i32x4 *)(tb + (wn * TN * 16 + b * 16) * G2_LDS_ROW + fr_ofs);
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+            f.a[a] = *(const glint_i32x4 *)(ta + (wm * 128 + a * 16) * G2_LDS_ROW + fr_ofs);
+    };
+    auto step = [&](int kb, int u) {
+        /* this wave's loads of step kb + 1 are done once only step kb + 2's 2 QN remain, and
+         * its fragment reads of step kb are done; after the barrier every wave's are, and
+         * slot (u + 3) % 4, last read during step kb - 2, is free */
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(2 * QN * (G3_NBUF - 3)));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
+        dma(kb + G3_NBUF - 1, (u + G3_NBUF - 1) % G3_NBUF);
+        __builtin_amdgcn_sched_barrier(0); /* issue the loads first, not after the MFMAs */
+        Frags &f = fr[u & 1];
+        read_frags((u + 1) % G3_NBUF, fr[(u + 1) & 1]); /* past the end: clamped data nobody uses */
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+                acc[a][b] = glint_mfma_i8(f.a[a], f.b[b], acc[a][b]);
+        /* the next step's reads spread over the first MFMAs, one read per two MFMAs */
+#pragma unroll
+        for (int i = 0; i < TM + TN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); /* LDS read */
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0); /* MFMA */
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < G3_NBUF - 1; ++i)
+        dma(i, i);
+    /* step 0's loads (only steps 1 and 2's remain), then its fragments */
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(2 * QN * (G3_NBUF - 2)));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
+    read_frags(0, fr[0]);
+#else
     /* step kb from ring slot u = kb % G3_NBUF (a constant after unrolling) */
     auto step = [&](int kb, int u) {
         /* this wave's loads of step kb are done once only the later steps' 2 QN each remain,
@@ -541,6 +595,7 @@ __global__ __launch_bounds__(G3_THREADS) void k_int8_gemm_dma(const int8_t *__re
 #pragma unroll
     for (int i = 0; i < G3_NBUF - 1; ++i)
         dma(i, i);
+#endif
     int kb = 0;
     for (; kb + G3_NBUF <= nkb; kb += G3_NBUF) {
 #pragma unroll
