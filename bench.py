@@ -213,14 +213,16 @@ def llama3_8b_shapes():
 MODEL_STREAMS = 4
 
 
-def spread_over_streams(torch, make_call, count: int, nstreams: int):
-    """One pass over `count` independent calls, call i on stream i % nstreams (HIP streams
-    at the default priority), fenced by events so the pass starts and ends on the current
-    stream and times like one call. make_call(i, stream_handle) -> zero-argument call."""
+def spread_over_streams(torch, make_call, count: int, nstreams: int, rounds: int = 1):
+    """One pass over `count` independent calls, `rounds` times, call j on stream j % nstreams
+    (HIP streams at the default priority), fenced by events so the pass starts and ends on
+    the current stream and times like one call. The fence empties the GPU once per pass (the
+    next pass's streams wait for this one to end on the current stream), so a pass should
+    hold many calls. make_call(i, stream_handle) -> zero-argument call."""
     import ctypes
     main = torch.cuda.current_stream()
     streams = [torch.cuda.Stream() for _ in range(nstreams)]
-    calls = [make_call(i, ctypes.c_void_p(streams[i % nstreams].cuda_stream)) for i in range(count)]
+    calls = [make_call(j % count, ctypes.c_void_p(streams[j % nstreams].cuda_stream)) for j in range(count * rounds)]
 
     def run():
         start = torch.cuda.Event()
@@ -256,16 +258,18 @@ def bench_model_encode(torch, H, passes: int):
     lib = H.encode_lib()
     enc = lambda i, st: bound(lib.glint_encode_bf16_device, ws[i], ws[i].numel(), 64, pins[i][0], pins[i][1],
                               pins[i][2], st)
-    ms_enc = timed(torch, [spread_over_streams(torch, enc, len(shapes), MODEL_STREAMS)], passes, 1)
-    ms_enc1 = timed(torch, [spread_over_streams(torch, enc, len(shapes), 1)], passes, 1)
+    nt = len(shapes)
+    cur = stream_handle(torch)
+    ms_enc = timed(torch, [spread_over_streams(torch, enc, nt, MODEL_STREAMS)], passes, 1)
+    ms_enc1 = timed(torch, [enc(i, cur) for i in range(nt)], passes * nt, nt) * nt  # in order on one stream
     del ws
     torch.cuda.empty_cache()
     outs = [torch.empty(p[0].numel() * 2, dtype=torch.bfloat16, device="cuda") for p in pins]
     ns = [a * b for a, b in shapes]
     exp = lambda i, st: bound(lib.glint_expand_packed_to_bf16_device, pins[i][0], pins[i][1], pins[i][2], ns[i], 64,
                               outs[i], st)
-    ms_exp = timed(torch, [spread_over_streams(torch, exp, len(shapes), MODEL_STREAMS)], passes, 1)
-    ms_exp1 = timed(torch, [spread_over_streams(torch, exp, len(shapes), 1)], passes, 1)
+    ms_exp = timed(torch, [spread_over_streams(torch, exp, nt, MODEL_STREAMS)], passes, 1)
+    ms_exp1 = timed(torch, [exp(i, cur) for i in range(nt)], passes * nt, nt) * nt
     del outs, pins
     torch.cuda.empty_cache()
     b = 3.0625 * total
@@ -281,8 +285,8 @@ def bench_model_encode(torch, H, passes: int):
 
 def bench_encode_4096(torch, H, passes: int = 5):
     """The CPU-reference configuration on the GPU: 4096x4096 BF16 (seed 1001, 0.1% outliers
-    x10), bs 64, 20 distinct copies (> 256 MB Infinity Cache) encoded per pass, spread over
-    MODEL_STREAMS streams; also on one stream."""
+    x10), bs 64, 20 distinct copies (> 256 MB Infinity Cache) cycled 4 times per pass, spread
+    over MODEL_STREAMS streams; also in order on the current stream (no fork and join)."""
     import numpy as np
     rng = np.random.default_rng(1001)
     n = 4096 * 4096
@@ -297,11 +301,13 @@ def bench_encode_4096(torch, H, passes: int = 5):
              torch.empty(n // 64, dtype=torch.float32, device="cuda")) for _ in range(copies)]
     lib = H.encode_lib()
     enc = lambda i, st: bound(lib.glint_encode_bf16_device, ws[i], n, 64, pins[i][0], pins[i][1], pins[i][2], st)
-    ms = timed(torch, [spread_over_streams(torch, enc, copies, MODEL_STREAMS)], passes, 1) / copies
-    ms1 = timed(torch, [spread_over_streams(torch, enc, copies, 1)], passes, 1) / copies
+    ms = timed(torch, [spread_over_streams(torch, enc, copies, MODEL_STREAMS, rounds=4)], passes, 1) / (4 * copies)
+    # one stream: the calls in order on the current stream, no fork and join per pass
+    cur = stream_handle(torch)
+    ms1 = timed(torch, [enc(i, cur) for i in range(copies)], passes * copies * 4, copies)
     del ws, pins, src
     torch.cuda.empty_cache()
-    return {"config": "4096x4096 BF16, seed 1001, 0.1% outliers x10, bs 64; 20 copies per pass",
+    return {"config": "4096x4096 BF16, seed 1001, 0.1% outliers x10, bs 64; 20 copies cycled 4 times per pass",
             "streams": MODEL_STREAMS, "ms_per_matrix": ms, "encode_bf16_in_gbs": 2 * n / ms / 1e6,
             "encode_frac": 3.0625 * n / ms / 1e6 / HBM_PEAK_GBS,
             "one_stream_ms_per_matrix": ms1, "one_stream_frac": 3.0625 * n / ms1 / 1e6 / HBM_PEAK_GBS}

@@ -62,7 +62,7 @@ __device__ __forceinline__ glint_i16x2 glint_mag_key(uint32_t d) {
  * of copy j at byte (b * ENC_COPIES + j) * 16, lane l reading copy l % ENC_COPIES, to
  * spread the random lookups over the banks. */
 #ifndef ENC_COPIES
-#define ENC_COPIES 8
+#define ENC_COPIES 4
 #endif
 static_assert(ENC_COPIES >= 1 && ENC_COPIES <= 64 && (ENC_COPIES & (ENC_COPIES - 1)) == 0, "power-of-two table copies");
 #define ENC_ENTRY_SHIFT (4 + __builtin_ctz(ENC_COPIES)) /* log2 of the byte stride of one entry's copies */
@@ -70,7 +70,7 @@ static_assert(ENC_COPIES >= 1 && ENC_COPIES <= 64 && (ENC_COPIES & (ENC_COPIES -
 #define ENC_THREADS 1024
 #endif
 #ifndef ENC_UNROLL
-#define ENC_UNROLL 2
+#define ENC_UNROLL 1
 #endif
 #ifndef ENC_WPE /* minimum waves per SIMD the register allocation must allow */
 #define ENC_WPE 4
