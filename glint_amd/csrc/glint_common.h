@@ -136,23 +136,29 @@ __device__ __forceinline__ void glint_cells_fill_store(float *ltab, const GlintC
  * 14336 x 4096: 12.30-12.59 -> 11.87-11.95 us. A 16-copy form was slower (12.8 us), and so
  * was a generic form of this fill (12.3 us): keep the prologue's code as it is. */
 #define GLINT_FILLH_STEPS 5 /* covers 2048 runs for blockDim.x >= 410 */
-struct GlintCellFillH {
-    glint_f32x4 c[GLINT_FILLH_STEPS][2];
+/* STEPS scalar steps cover the table for blockDim.x >= 2048 / STEPS (8 for 256 threads, so no
+ * vector load of the table and no wait for the kernel's own first loads is needed) */
+template <int STEPS>
+struct GlintCellFillHN {
+    glint_f32x4 c[STEPS][2];
 };
-__device__ __forceinline__ void glint_cells_fillh_sload(GlintCellFillH &f) {
+typedef GlintCellFillHN<GLINT_FILLH_STEPS> GlintCellFillH;
+template <int STEPS>
+__device__ __forceinline__ void glint_cells_fillh_sload(GlintCellFillHN<STEPS> &f) {
     const int wbase = __builtin_amdgcn_readfirstlane((int)threadIdx.x & ~63);
 #pragma unroll
-    for (int k = 0; k < GLINT_FILLH_STEPS; ++k) {
+    for (int k = 0; k < STEPS; ++k) {
         const int c0 = min((wbase + k * (int)blockDim.x) >> 3, 248);
         f.c[k][0] = *(const glint_f32x4 *)(&kCells[0][0] + c0);
         f.c[k][1] = *(const glint_f32x4 *)(&kCells[0][0] + c0 + 4);
     }
 }
-__device__ __forceinline__ void glint_cells_fillh_sstore(float *ltab, const GlintCellFillH &f) {
+template <int STEPS>
+__device__ __forceinline__ void glint_cells_fillh_sstore(float *ltab, const GlintCellFillHN<STEPS> &f) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     const int lane = threadIdx.x & 63, ci = lane >> 3; /* cell c0 + ci (blockDim.x % 64 == 0) */
 #pragma unroll
-    for (int k = 0; k < GLINT_FILLH_STEPS; ++k) {
+    for (int k = 0; k < STEPS; ++k) {
         const int u = (int)threadIdx.x + k * (int)blockDim.x;
         const glint_f32x4 lo = f.c[k][0], hi = f.c[k][1];
         const float vl = (ci & 2) ? ((ci & 1) ? lo.w : lo.z) : ((ci & 1) ? lo.y : lo.x);
@@ -161,7 +167,7 @@ __device__ __forceinline__ void glint_cells_fillh_sstore(float *ltab, const Glin
         if (u < 2048)
             ((f32x4 *)ltab)[(u >> 3) * 16 + (u & 7)] = f32x4{v, v, v, v};
     }
-    for (int u = threadIdx.x + GLINT_FILLH_STEPS * blockDim.x; u < 2048; u += blockDim.x) {
+    for (int u = threadIdx.x + STEPS * blockDim.x; u < 2048; u += blockDim.x) {
         const float v = (&kCells[0][0])[u >> 3];
         ((f32x4 *)ltab)[(u >> 3) * 16 + (u & 7)] = f32x4{v, v, v, v};
     }

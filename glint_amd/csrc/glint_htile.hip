@@ -990,6 +990,309 @@ static int htile_launch_gemv_cu(const uint8_t *hole, const uint8_t *plug, const 
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
+/* ------------------------------------ small-M prefill, weights dequantized into registers */
+/* k_htile_rd: M <= 64 rows of x (MB = 1, 2 or 4 MFMA row blocks of 16), bs = 64,
+ * K % 128 == 0, aligned, BF16 out. The MFMA tiles stage W through LDS and meet at a barrier
+ * every 64-wide K step; at small M a step holds too little work to hide that chain. Here
+ * each wave owns a strip of 16 W rows and turns its own loads straight into MFMA B operands:
+ *   - K runs in W chunks of 128. Lane l loads 16 B of each plane of row l % 16 at chunk
+ *     elements [32 (l / 16), +32) and one absmax. Word s of those 16 B is elements [8 s, +8)
+ *     of its quarter, which is what v_mfma_f32_16x16x32_bf16 step s wants from the lane when
+ *     the K order inside a chunk is permuted so that step s takes elements 32 g + 8 s .. +8
+ *     of lane group g. x is read in the same order, so each product is the one the GEMM
+ *     defines; only the order of the f32 sums changes.
+ *   - KW waves share a strip: x moves in chunks of KW W chunks, and wave kw of the strip
+ *     takes W chunk kw of each (its partial sums are added to the others' in kw order at
+ *     the end, through LDS). Two waves per SIMD (KW = 2) overlap one wave's dequantization
+ *     with the other's MFMAs and loads; with one, the phases of a chunk ran back to back.
+ *   - W loads go out in bursts of RD_BURST chunks per wave, two bursts in registers: a load
+ *     instruction covers 16 rows x 64 B, and a burst of the KW waves of a strip puts
+ *     KW RD_BURST x 64 B of each row in flight together. Read one chunk at a time (all waves
+ *     walking K together, 64 B of each 2-KiB row per chunk) these planes streamed at 40% of
+ *     HBM; in bursts of 4 chunks per row at 54% (a read-only probe over 14336 x 4096).
+ *   - dequantization per element: half a VALU op forms the code byte, one v_perm the lookup
+ *     address in the 64-copy cell table, one LDS read, one multiply by the block absmax,
+ *     half a v_cvt_pk_bf16_f32 (BF16(cell * absmax), the rounding the other BF16 kernels
+ *     apply).
+ *   - x chunks (16 MB rows x 256 KW bytes) are loaded three chunks ahead into registers and
+ *     written one chunk ahead into an LDS double buffer whose 16-B pieces are XOR-swizzled by
+ *     row within each W chunk's 256 bytes (an A fragment read, 16 rows x one piece, hits
+ *     distinct banks). One barrier per x chunk, which waits for LDS accesses only.
+ *   - a workgroup holds R <= 64 rows, R about N ks / CUs, so one workgroup per CU covers
+ *     N (14336 x 4096: 56 rows each, 256 workgroups); K is split ks ways through the split-K
+ *     workspace where N alone leaves too few rows per CU (4096 x 14336: 4 ways of 64 rows).
+ * Loads past the workgroup's rows, x rows past M and chunk loads past the K range are out of
+ * their buffer's range: the hardware drops them and returns zeros. */
+#ifndef RD_ON
+#define RD_ON 1
+#endif
+#define RD_STRIPS 4 /* 16-row W strips per workgroup */
+#ifndef RD_KW
+#define RD_KW 2 /* waves per strip (1: 4-20% slower) */
+#endif
+#ifndef RD_BURST
+#define RD_BURST 2 /* W chunks per load burst of one wave; two bursts in registers (4: 3-8% slower) */
+#endif
+#define RD_OOR 0x7FFFFF00u /* a buffer offset past every range */
+#ifndef RD_W_AUX
+#define RD_W_AUX 0 /* cache policy of the weight loads */
+#endif
+
+template <int MB, int KW>
+__global__ __launch_bounds__(64 * RD_STRIPS * KW, 1) void k_htile_rd(const uint8_t *__restrict__ hole,
+                                                                     const uint8_t *__restrict__ plug,
+                                                                     const float *__restrict__ absmax,
+                                                                     const uint16_t *__restrict__ x,
+                                                                     uint16_t *__restrict__ y, int M, int N, int K,
+                                                                     int R, int cps, float *__restrict__ part,
+                                                                     unsigned *ctr) {
+    constexpr int T = 64 * RD_STRIPS * KW;
+    constexpr int XROW = 256 * KW;                /* bytes of one x row of an x chunk */
+    constexpr int XCH = 16 * MB * XROW;           /* bytes of one x chunk */
+    constexpr int NX = XCH / 16 / T;              /* 16-B pieces of an x chunk per thread */
+    constexpr int U = 2 * RD_BURST;               /* x chunks per unrolled round */
+    static_assert(NX >= 1 && NX * 16 * T == XCH, "x chunk split over the threads");
+    static_assert(U % 2 == 0, "two x register stages per round");
+    __shared__ float ltab[GLINT_LDS_CELLS64_WORDS];
+    __shared__ __attribute__((aligned(16))) uint8_t xb0[XCH], xb1[XCH];
+    const int lane = threadIdx.x & 63, m16 = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int strip = w % RD_STRIPS, kw = w / RD_STRIPS;
+    const uint32_t lane4 = (uint32_t)(lane & 31) * 4u; /* the half-filled table: copy lane % 32 */
+    const int n0 = blockIdx.x * R;
+    const int nrows = min(R, N - n0); /* >= 1 */
+    const int c0 = blockIdx.z * cps;
+    const int nj = min(K >> 7, c0 + cps) - c0;  /* W chunks of the split, >= 1 (the host sizes gridDim.z) */
+    const int nxc = (nj + KW - 1) / KW;         /* x chunks */
+    const uint32_t rowb = (uint32_t)K >> 1;
+
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(hole + (int64_t)n0 * rowb), (short)0, (int)((uint32_t)nrows * rowb), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(plug + (int64_t)n0 * rowb), (short)0, (int)((uint32_t)nrows * rowb), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(absmax + (int64_t)n0 * (K >> 6)), (short)0, (int)((uint32_t)nrows * (rowb >> 3)), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), GLINT_BUF_DWORD3);
+    const uint32_t wrow = (uint32_t)(16 * strip + m16);
+    const uint32_t wofs = wrow * rowb + 16u * (uint32_t)g;
+    const uint32_t aofs = (wrow * (uint32_t)(K >> 6) + (uint32_t)(g >> 1)) * 4u;
+    /* x piece i of thread t: slot s = t + T i of the chunk (row s / (16 KW), piece
+     * s % (16 KW); consecutive threads read one row's contiguous bytes), stored at piece
+     * (s % (16 KW)) ^ (row % 16) of its LDS row (the XOR keeps a piece in its W chunk's
+     * 256 bytes) */
+    uint32_t xgo[NX], xlo[NX];
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+        const int sl = (int)threadIdx.x + T * i, r = sl / (16 * KW), pc = sl % (16 * KW);
+        xgo[i] = (uint32_t)r * (uint32_t)K * 2u + (uint32_t)(pc << 4);
+        xlo[i] = (uint32_t)(r * XROW + ((pc ^ (r & 15)) << 4));
+    }
+
+    struct WReg {
+        glint_u32x4 h, p;
+        float a;
+    };
+    WReg wr[U];
+    glint_u32x4 xr[2][NX];
+    /* this wave's W chunk of x chunk X: KW X + kw of the split */
+    auto wload = [&](int X, WReg &s) {
+        const int j = KW * X + kw;
+        const uint32_t c = (uint32_t)(c0 + j);
+        const bool in = j < nj;
+        const uint32_t o = in ? wofs + c * 64u : RD_OOR, oa = in ? aofs + c * 8u : RD_OOR;
+        s.h = __builtin_amdgcn_raw_buffer_load_b128(rh, o, 0, RD_W_AUX);
+        s.p = __builtin_amdgcn_raw_buffer_load_b128(rp, o, 0, RD_W_AUX);
+        s.a = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, oa, 0, RD_W_AUX));
+    };
+    auto wburst = [&](int X0, int st) {
+#pragma unroll
+        for (int c = 0; c < RD_BURST; ++c)
+            wload(X0 + c, wr[st + c]);
+    };
+    auto xload = [&](int X, glint_u32x4 (&xs)[NX]) {
+        const uint32_t c = (uint32_t)(c0 + KW * X);
+        const bool in = X < nxc;
+#pragma unroll
+        for (int i = 0; i < NX; ++i)
+            xs[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, in ? xgo[i] + c * 256u : RD_OOR, 0, 0);
+    };
+    auto xstore = [&](uint8_t *buf, const glint_u32x4 (&xs)[NX]) {
+#pragma unroll
+        for (int i = 0; i < NX; ++i)
+            *(glint_u32x4 *)(buf + xlo[i]) = xs[i];
+    };
+    auto dequant = [&](const WReg &s, glint_bf16x8 (&bq)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t E = glint_codes_even(s.h[q], s.p[q]), O = glint_codes_odd(s.h[q], s.p[q]);
+            const float f0 = glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4));
+            const float f1 = glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4));
+            const float f2 = glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4));
+            const float f3 = glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4));
+            const float f4 = glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4));
+            const float f5 = glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4));
+            const float f6 = glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4));
+            const float f7 = glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4));
+            bq[q] = __builtin_bit_cast(glint_bf16x8,
+                                       glint_u32x4{glint_cvt_bf16x2(f0 * s.a, f1 * s.a), glint_cvt_bf16x2(f2 * s.a, f3 * s.a),
+                                                   glint_cvt_bf16x2(f4 * s.a, f5 * s.a), glint_cvt_bf16x2(f6 * s.a, f7 * s.a)});
+        }
+    };
+    glint_f32x4 acc[MB][1];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+        acc[mb][0] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
+    /* A fragments of MFMA step s of this wave's W chunk in an x chunk */
+    auto aread = [&](const uint8_t *xs, int s, glint_bf16x8 (&af)[MB]) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+            af[mb] = __builtin_bit_cast(glint_bf16x8, *(const glint_u32x4 *)(xs + (16 * mb + m16) * XROW +
+                                                                             (((16 * kw + 4 * g + s) ^ m16) << 4)));
+    };
+    /* the chunk's 4 MFMA steps, step s + 1's fragments read while step s multiplies */
+    auto mma = [&](const uint8_t *xs, const glint_bf16x8 (&bq)[4]) {
+        glint_bf16x8 af[2][MB];
+        aread(xs, 0, af[0]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (s + 1 < 4)
+                aread(xs, s + 1, af[(s + 1) & 1]);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                acc[mb][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[s & 1][mb], bq[s], acc[mb][0], 0, 0, 0);
+        }
+    };
+    /* x chunk X (u = X % U) is in LDS buffer u % 2 (written one chunk earlier, published by
+     * this barrier, which also ends every read of the other buffer); x chunk X + 1 goes into
+     * that buffer from register stage (u + 1) % 2, which then takes x chunk X + 3. The last
+     * chunk of a burst refills the burst's stages with the burst after next. */
+    /* (Pinning these phases in order with sched_barrier measured 5-13% slower: the compiler's
+     * interleaving of one step's MFMAs with the next step's loads and lookups pays.) */
+    auto step = [&](int X, int u) {
+        __syncthreads();
+        xstore((u & 1) ? xb0 : xb1, xr[(u + 1) & 1]);
+        xload(X + 3, xr[(u + 1) & 1]);
+        glint_bf16x8 bq[4];
+        dequant(wr[u], bq);
+        if (u % RD_BURST == RD_BURST - 1)
+            wburst(X + 1 + RD_BURST, u + 1 - RD_BURST);
+        mma((u & 1) ? xb1 : xb0, bq);
+    };
+
+    /* the steady state's order of loads from the start (a reordered prologue would leave the
+     * first chunks' wait counts short): table (scalar), x chunks 0 and 1, two W bursts, then
+     * x chunk 2 into the stage x chunk 0 leaves */
+    GlintCellFillHN<(2048 + T - 1) / T> fill;
+    glint_cells_fillh_sload(fill);
+    __builtin_amdgcn_sched_barrier(0);
+    xload(0, xr[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    xload(1, xr[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    wburst(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    wburst(RD_BURST, RD_BURST);
+    __builtin_amdgcn_sched_barrier(0);
+    glint_cells_fillh_sstore(ltab, fill);
+    xstore(xb0, xr[0]); /* the first step's barrier publishes the table and x chunk 0 */
+    xload(2, xr[0]);
+    int X = 0;
+    for (; X + U <= nxc; X += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            step(X + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < U; ++u)
+        if (X + u < nxc)
+            step(X + u, u);
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0); /* the trailing dropped loads */
+
+    /* the strip's KW partials, added in kw order by wave kw = 0 (the x buffers are free) */
+    if constexpr (KW > 1) {
+        float *red = (float *)xb0;
+        static_assert((KW - 1) * RD_STRIPS * 64 * MB * 4 * 4 <= XCH, "partials fit an x buffer");
+        __syncthreads();
+        if (kw > 0)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    red[((((kw - 1) * RD_STRIPS + strip) * MB + mb) * 4 + i) * 64 + lane] = acc[mb][0][i];
+        __syncthreads();
+        if (kw == 0)
+#pragma unroll
+            for (int k = 1; k < KW; ++k)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[mb][0][i] += red[((((k - 1) * RD_STRIPS + strip) * MB + mb) * 4 + i) * 64 + lane];
+        __syncthreads(); /* the split-K epilogue's flag word lives in xb0 */
+    }
+    if (gridDim.z > 1 && !tile_splitk_epilogue<MB, 1, 64 * RD_STRIPS>(acc, part, ctr, *(unsigned *)xb1,
+                                                                       (int)threadIdx.x, kw == 0))
+        return;
+    const int nl = 16 * strip + m16;
+    if (kw == 0 && nl < nrows)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 16 * mb + 4 * g + i;
+                if (m < M)
+                    y[(int64_t)m * N + n0 + nl] = glint_f32_to_bf16(acc[mb][0][i]);
+            }
+}
+
+/* k_htile_rd over an M <= 64, BF16-out prefill. Returns 1 where the shape does not fit
+ * (K % 128 != 0, offsets beyond 31 bits; the caller takes the LDS tiles), -5 where a
+ * `fixed` workspace is too small for the split plan, else 0 or -3. */
+template <int MB>
+static int htile_launch_rd_mb(const uint8_t *hole, const uint8_t *plug, const float *absmax, const uint16_t *x,
+                              uint16_t *y, int M, int N, int K, hipStream_t st, const GlintSplitWs *fixed) {
+    const int cus = glint_cu_count(), nc = K >> 7;
+    constexpr int RMAX = 16 * RD_STRIPS, TILE_FLOATS = MB * 4 * 64 * RD_STRIPS;
+    auto plan = [&](int ks, int &cps, int &R, unsigned &gx) {
+        cps = (nc + ks - 1) / ks;
+        ks = (nc + cps - 1) / cps;
+        R = (int)std::min<int64_t>(RMAX, (((int64_t)N * ks + cus - 1) / cus + 7) / 8 * 8);
+        gx = (unsigned)((N + R - 1) / R);
+        return ks;
+    };
+    int cps, R;
+    unsigned gx;
+    int ks = plan(std::max(1, std::min(std::min(TILE_SPLIT_MAX, nc), (int)((int64_t)cus * RMAX / N))), cps, R, gx);
+    GlintSplitWs ws{nullptr, nullptr, 0, 0};
+    if (ks > 1) {
+        const bool got = fixed ? (ws = *fixed, true) : glint_split_ws_stream(st, ws);
+        const bool fits = got && (size_t)ks * gx * TILE_FLOATS <= ws.part_floats && (size_t)gx <= ws.nctr;
+        if (!fits) {
+            if (fixed)
+                return -5;
+            ks = plan(1, cps, R, gx); /* no workspace (a capture without one): unsplit */
+            ws = GlintSplitWs{nullptr, nullptr, 0, 0};
+        }
+    }
+    k_htile_rd<MB, RD_KW><<<dim3(gx, 1, (unsigned)ks), 64 * RD_STRIPS * RD_KW, 0, st>>>(
+        hole, plug, absmax, x, y, M, N, K, R, cps, ws.part, ws.ctr);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+static int htile_launch_rd(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y,
+                           int M, int N, int K, hipStream_t st, const GlintSplitWs *fixed) {
+    if (!RD_ON || M < 1 || M > 64 || K % 128 != 0 || (int64_t)M * K * 2 >= (int64_t)RD_OOR ||
+        (int64_t)16 * RD_STRIPS * (K / 2) >= (int64_t)RD_OOR)
+        return 1;
+    const uint16_t *xb = (const uint16_t *)x;
+    uint16_t *yb = (uint16_t *)y;
+    if (M <= 16)
+        return htile_launch_rd_mb<1>(hole, plug, absmax, xb, yb, M, N, K, st, fixed);
+    if (M <= 32)
+        return htile_launch_rd_mb<2>(hole, plug, absmax, xb, yb, M, N, K, st, fixed);
+    return htile_launch_rd_mb<4>(hole, plug, absmax, xb, yb, M, N, K, st, fixed);
+}
+
 /* f32 output at M > 1 (the reference ABI's prefill use): 3-plane k_tile_mfma, whose
  * products are exact and whose sums are f32. 128 x 128 tiles over 8 waves (2 x 4, wave tile
  * 64 x 32) fill the 160 KiB of LDS: x 32 KiB, three W planes 96 KiB, cell table 32 KiB;
@@ -1062,6 +1365,11 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
         const uint16_t *xb = (const uint16_t *)x;
         uint16_t *yb = (uint16_t *)y;
         bool planned;
+        if (M <= 64) {
+            const int rc = htile_launch_rd(hole, plug, absmax, x, y, M, N, K, st, fixed);
+            if (rc != 1)
+                return rc;
+        }
         if (M <= 64)
             planned = TILE_SS_BN32
                           ? tile_ss_launch<64, 32, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 2, fixed)

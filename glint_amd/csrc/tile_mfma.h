@@ -278,29 +278,34 @@ struct Int8PinTileProducer {
  * element e of thread t sits at e T + t. Returns true in the last workgroup of the tile,
  * whose acc then holds the z-ordered sum; the others return false and store nothing.
  * s_last: one word of LDS that nothing else uses any more. */
+/* tid: the thread's index among the T that hold the tile (threadIdx.x unless the block has
+ * more threads than that); threads with active false hold no part of it, store and load
+ * nothing and only join the barriers. */
 template <int NA, int NB, int T>
 __device__ __forceinline__ bool tile_splitk_epilogue(glint_f32x4 (&acc)[NA][NB], float *__restrict__ part,
-                                                     unsigned *ctr, unsigned &s_last) {
+                                                     unsigned *ctr, unsigned &s_last, int tid, bool active) {
     constexpr int NV = NA * NB * 4;
-    const int tid = threadIdx.x;
     const unsigned tile = blockIdx.y * gridDim.x + blockIdx.x;
     const size_t tsz = (size_t)NV * T, zstride = (size_t)gridDim.x * gridDim.y * tsz;
     float *mine = part + blockIdx.z * zstride + tile * tsz;
+    if (active)
 #pragma unroll
-    for (int a = 0; a < NA; ++a)
+        for (int a = 0; a < NA; ++a)
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+            for (int b = 0; b < NB; ++b)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                __hip_atomic_store(mine + ((a * NB + b) * 4 + i) * T + tid, acc[a][b][i], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+                for (int i = 0; i < 4; ++i)
+                    __hip_atomic_store(mine + ((a * NB + b) * 4 + i) * T + tid, acc[a][b][i], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0);
     __syncthreads();
-    if (tid == 0)
+    if (threadIdx.x == 0)
         s_last = __hip_atomic_fetch_add(&ctr[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.z - 1;
     __syncthreads();
     if (!s_last)
         return false;
+    if (!active)
+        return true;
     /* The partials are read in rounds of CH accumulators, all TILE_SPLIT_MAX splits of a
      * round in flight at once (z clamped; a split past gridDim.z is loaded and ignored). */
     constexpr int CH = NV < 16 ? NV : 16;
@@ -326,9 +331,14 @@ __device__ __forceinline__ bool tile_splitk_epilogue(glint_f32x4 (&acc)[NA][NB],
             acc[a][b][i] = sum;
         }
     }
-    if (tid == 0)
+    if (threadIdx.x == 0)
         __hip_atomic_store(&ctr[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
+}
+template <int NA, int NB, int T>
+__device__ __forceinline__ bool tile_splitk_epilogue(glint_f32x4 (&acc)[NA][NB], float *__restrict__ part,
+                                                     unsigned *ctr, unsigned &s_last) {
+    return tile_splitk_epilogue<NA, NB, T>(acc, part, ctr, s_last, (int)threadIdx.x, true);
 }
 
 /* Stream-K partition of a tile GEMM: the flattened units (tile, K step), tile-major, tiles

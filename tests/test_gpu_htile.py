@@ -198,6 +198,46 @@ def test_small_m_gemv_vs_float64(oracle, M, N, K):
     assert rel <= 4e-3, rel
 
 
+# 9 <= M <= 64 with K % 128 == 0: the register-dequantized tiles (one, two or four MFMA row
+# blocks; a workgroup of about N / CUs rows, the last strip partly filled; K split 4 ways
+# where N is small). Odd W-chunk counts leave the last x chunk half used (K = 640, 896,
+# 14464); N = 13 and 56 give workgroups of fewer rows than one strip; N = 14336 at M = 9 is
+# the gate shape with 56-row workgroups, 4096 x 14336 the down shape split 4 ways.
+RD_SHAPES = [(9, 14336, 4096), (16, 777, 896), (17, 56, 2048), (32, 4097, 1152), (33, 300, 14464),
+             (48, 2000, 640), (64, 13, 512), (64, 1000, 2304), (64, 4096, 14336), (40, 130, 128)]
+
+
+@pytest.mark.parametrize("M,N,K", RD_SHAPES)
+def test_bf16_small_m_tiles_vs_float64(oracle, M, N, K):
+    """9 <= M <= 64 on the register-dequantized MFMA tiles, each output bounded against
+    float64 on the expanded weights: the BF16 output rounding (2^-8 |ref|), the BF16 rounding
+    of each weight (2^-9 sum |w x|) and f32 accumulation in any order ((K + 2) 2^-23
+    sum |w x|). Also rel-Frobenius <= 4e-3, no write past row M - 1, and a repeat equal bit
+    for bit (the K split adds its partials in a fixed order)."""
+    torch = torch_cuda()
+    print(f"small-M tiles M={M} N={N} K={K}", flush=True)
+    hole, plug, am = _encoded_weight(oracle, N, K, 5002 + K)
+    g = torch.Generator(device="cuda").manual_seed(5001 + M)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.full((M + 1, N), 1234.0, dtype=torch.bfloat16, device="cuda")
+    lib = H.encode_lib()
+    assert lib.launch_glint_htile_bf16_stream(H._p(hole), H._p(plug), H._p(am), H._p(x), H._p(y), M, N, K, 64,
+                                              H._stream()) == 0
+    yh = host(y, np.uint16)
+    assert (yh[M] == np.uint16(0x449A)).all()  # 1234.0 in BF16: row M untouched
+    got = G.bf16_bits_to_f32(yh[:M].reshape(-1)).astype(np.float64).reshape(M, N)
+    ref, asum = oracle.htile_f64(host(hole), host(plug), host(am), host(x, np.uint16), M, N, K, 64)
+    ref, asum = ref.reshape(M, N), asum.reshape(M, N)
+    bound = np.abs(ref) * 2.0 ** -8 + asum * (2.0 ** -9 + (K + 2) * 2.0 ** -23) * 1.01
+    assert (np.abs(got - ref) <= bound).all(), float((np.abs(got - ref) / bound).max())
+    rel = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+    assert rel <= 4e-3, rel
+    again = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    assert lib.launch_glint_htile_bf16_stream(H._p(hole), H._p(plug), H._p(am), H._p(x), H._p(again), M, N, K, 64,
+                                              H._stream()) == 0
+    assert torch.equal(again.view(torch.int16), y[:M].view(torch.int16))
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 1024, 4096), (300, 1000, 576), (513, 1100, 1024), (2048, 384, 640),
                                    (2000, 6100, 1088), (4096, 4096, 576)])
 def test_bf16_prefill_tiles_rel_frobenius(oracle, M, N, K):
