@@ -3,8 +3,13 @@
  *
  * int8_mma_gemm — the attach ABI (reference cuda/int8_mma_gemm.cu:11-155): activations
  *   quantized per (row, 64-block) (s = amax > 0 ? amax / 127 : 1, q = clamp(rint(x / s))),
- *   then per 64-slice kb: ic = exact int32 dot product, acc += ((float)ic * sx) * sw,
- *   kb ascending, as separate f32 multiplies and add (bit-identical to the CPU emulation).
+ *   then per 64-slice kb: ic = exact int32 dot product, acc = fma(RN((float)ic * sx), sw,
+ *   acc), kb ascending. That is the reference kernel's statement acc += ((float)ic * x0) * w0
+ *   (cuda/int8_mma_gemm.cu:115-124) as its build compiles it: nvcc -O2 with the default
+ *   --fmad=true (scripts/build_p7_kernels.sh:7) contracts the last multiply and add into one
+ *   fused multiply-add. The reference's host emulation keeps them separate and its test
+ *   allows for exactly that difference (1e-5, "only fp32 contraction order may differ",
+ *   tests/test_int8_mma_gemm.cu:207).
  * glint_int8_gemm_i32 / _scaled_bf16 — the plain INT8 GEMM C = A B^T with int32
  *   accumulation over all of K (|C| <= K * 127^2 < 2^31 for K < 133152), optionally
  *   scaled to BF16 RNE(((float)C * sa[m]) * sb[n]).
@@ -70,9 +75,9 @@ __global__ __launch_bounds__(256) void k_quant_act(const glint_u32x4 *__restrict
 
 /* 256 threads = 4 waves in 2x2; wave (wm, wn) owns rows [32 wm, +32) x cols [32 wn, +32) of
  * the 64x64 tile = 2x2 MFMA tiles. Per 64-slice kb: ic = exact int32 dot product (one MFMA
- * with zero C), acc = acc + ((float)ic * sx) * sw. PLUG adds, per kb and right after the
+ * with zero C), acc = fma((float)ic * sx, sw, acc). PLUG adds, per kb and right after the
  * base term, a p7_plug_res4_v1 slice read from its nibbles (element 2i in the low nibble,
- * value nibble - 8) with its own block scales: acc = acc + ((float)ip * sx) * sp. ACCUM
+ * value nibble - 8) with its own block scales: acc = fma((float)ip * sx, sp, acc). ACCUM
  * stores y + acc instead of acc (the second pass of the two-pass forms). */
 template <bool PLUG, bool ACCUM>
 __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict__ xq, const float *__restrict__ sx,
@@ -193,9 +198,9 @@ __global__ __launch_bounds__(256) void k_int8_mma_gemm(const int8_t *__restrict_
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float sxv = sSx[cur][wm * 32 + a * 16 + (lane >> 4) * 4 + i];
-                    acc[a][b][i] = acc[a][b][i] + ((float)ic[i] * sxv) * swv;
+                    acc[a][b][i] = __builtin_fmaf((float)ic[i] * sxv, swv, acc[a][b][i]);
                     if (PLUG)
-                        acc[a][b][i] = acc[a][b][i] + ((float)ip[i] * sxv) * spv;
+                        acc[a][b][i] = __builtin_fmaf((float)ip[i] * sxv, spv, acc[a][b][i]);
                 }
             }
         if (kb + 1 < nkb)
@@ -225,7 +230,8 @@ __global__ __launch_bounds__(256) void k_unpack_res4(const uint8_t *__restrict__
 }
 
 /* Quantization residual of the activation, quantized again by the same rule: per (row,
- * 64-block), r = x - (float)xq * sx (a product, then a difference), s = amax|r| > 0 ?
+ * 64-block), r = fma(-(float)xq, sx, x) (the reference's x - xq * sx under nvcc's
+ * default contraction), s = amax|r| > 0 ?
  * amax / 127 : 1, rq = clamp(rint(r / s), -127, 127). One wave per block, one element per
  * lane. Reference cuda/int8_mma_gemm.cu:172-190. */
 __global__ __launch_bounds__(256) void k_quant_act_resid(const uint16_t *__restrict__ x, const int8_t *__restrict__ xq,
@@ -235,7 +241,7 @@ __global__ __launch_bounds__(256) void k_quant_act_resid(const uint16_t *__restr
     const int64_t waves = (int64_t)gridDim.x * (blockDim.x / 64);
     for (int64_t b = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); b < nblocks; b += waves) {
         const int64_t i = b * 64 + lane;
-        const float r = __uint_as_float((uint32_t)x[i] << 16) - (float)xq[i] * sx[b];
+        const float r = __builtin_fmaf(-(float)xq[i], sx[b], __uint_as_float((uint32_t)x[i] << 16));
         const float am = glint_wave_max(fabsf(r));
         const float s = (am > 0.0f) ? (am / 127.0f) : 1.0f;
         int v = (int)rintf(r / s);
@@ -629,12 +635,12 @@ __global__ __launch_bounds__(G3_THREADS) void k_int8_gemm_dma(const int8_t *__re
 /* The attach ABI's W8A8 GEMM on the same 256 x 256 DMA ring (int8_mma_gemm at the shapes
  * with at least 3/4 as many 256 x 256 tiles as CUs). Per 64-slice kb the wave's 32 MFMAs
  * run with zero C (ic = the slice's exact int32 dot products), and each A tile's 4 results
- * go straight into the f32 accumulators as acc = acc + ((float)ic * sx[m, kb]) * sw[n, kb]
- * (separate multiplies and add, kb ascending: bit-identical to the 64 x 64 kernel and to
- * the CPU emulation). A third ring carries the slice's scales: 256 sx (rows of the tile)
- * and 256 sw (columns), one 4-byte DMA per wave per step (waves 0-3 rows, 4-7 columns).
- * That epilogue is 4 VALU ops per output per slice against one MFMA per 16 x 16 x 64, so
- * the kernel is VALU-bound: at 2048 x 8192 x 8192 about 218 us of VALU issue on 256 CUs.
+ * go straight into the f32 accumulators as acc = fma((float)ic * sx[m, kb], sw[n, kb], acc)
+ * (kb ascending: bit-identical to the 64 x 64 kernel). A third ring carries the slice's
+ * scales: 256 sx (rows of the tile) and 256 sw (columns), one 4-byte DMA per wave per step
+ * (waves 0-3 rows, 4-7 columns). That epilogue is 3 VALU ops per output per slice (convert,
+ * multiply, fused multiply-add) against one MFMA per 16 x 16 x 64, so the kernel is
+ * VALU-bound: at 2048 x 8192 x 8192 about 164 us of VALU issue on 256 CUs.
  * ACCUM stores y + acc (the second pass of the two-pass forms). Offsets are 32-bit:
  * M K, N K, M K / 16 and N K / 16 < 2^31 (the host checks). */
 template <bool ACCUM>
@@ -724,7 +730,7 @@ __global__ __launch_bounds__(512) void k_int8_mma_dma(const int8_t *__restrict__
                 const glint_i32x4 ic = glint_mfma_i8(af, bf[b], glint_i32x4{0, 0, 0, 0});
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[a][b][i] = acc[a][b][i] + ((float)ic[i] * sxv[i]) * swv[b];
+                    acc[a][b][i] = __builtin_fmaf((float)ic[i] * sxv[i], swv[b], acc[a][b][i]);
             }
         }
     };
@@ -855,7 +861,7 @@ __global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict_
                 const glint_i32x4 ic = glint_mfma_i8(af[a], bf[b], glint_i32x4{0, 0, 0, 0});
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[a][b][i] = acc[a][b][i] + ((float)ic[i] * sxv[i]) * swv[b];
+                    acc[a][b][i] = __builtin_fmaf((float)ic[i] * sxv[i], swv[b], acc[a][b][i]);
             }
         }
     };

@@ -197,7 +197,7 @@ P7_API int p7_abi_selftest(char *msg, size_t msg_n) {
                     int ic = 0;
                     for (int j = 0; j < 64; ++j)
                         ic += (int)xq[(size_t)mi * kK + kb * 64 + j] * (int)wq[(size_t)ni * kK + kb * 64 + j];
-                    acc = acc + ((float)ic * sx[(size_t)mi * kKB + kb]) * sw[(size_t)ni * kKB + kb];
+                    acc = fmaf((float)ic * sx[(size_t)mi * kKB + kb], sw[(size_t)ni * kKB + kb], acc);
                 }
                 const double got = res[(size_t)mi * kN + ni], err = fabs(got - (double)acc);
                 const double rel = err / (fabs((double)acc) + 1e-6);

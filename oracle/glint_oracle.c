@@ -19,6 +19,9 @@
  *                      small integers (every f32 step exact, so fused, two-pass and the
  *                      integer formula agree bit for bit); the residual by the rounding
  *                      bound |r - rq sr| <= sr / 2 and the sign of the reconstruction;
+ *                      fmaf (the fused last step of the W8A8 epilogue and the residual)
+ *                      against exact rational arithmetic, and the fused emulation against
+ *                      the reference test's separate-step one within its 1e-5 gate;
  *   oracle_kmajor_pack / oracle_gemv_km_fold / oracle_select_topk / oracle_apply_corr_km
  *                      the K-major round trip against a numpy transpose; one-hot x (a single
  *                      term, so y is PARENT[h] * s or delta * s exactly); the selection
@@ -219,8 +222,10 @@ EXPORT void oracle_quant_act(const uint16_t *x, int m, int k, int8_t *xq, float 
         }
 }
 
-/* W8A8 per-64-slice arithmetic (test_int8_mma_gemm.cu:89-112, p7_abi_selftest.cu:118-125):
- * ic = exact int32 sum over the slice; acc += ((float)ic * sx) * sw, kb ascending. */
+/* W8A8 per-64-slice arithmetic of the reference kernel (cuda/int8_mma_gemm.cu:105-118) as
+ * its build compiles it (nvcc -O2, default --fmad=true, scripts/build_p7_kernels.sh:7):
+ * ic = exact int32 sum over the slice; acc = fmaf(RN((float)ic * sx), sw, acc), kb
+ * ascending. */
 EXPORT void oracle_int8_mma_emu(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw, int m, int n,
                                 int k, float *y) {
     const int nkb = k / 64;
@@ -233,10 +238,39 @@ EXPORT void oracle_int8_mma_emu(const int8_t *xq, const float *sx, const int8_t 
                 for (int t = 0; t < 64; ++t)
                     ic += (int)xq[(int64_t)i * k + kb * 64 + t] * (int)wq[(int64_t)j * k + kb * 64 + t];
                 const float a = (float)ic * sx[(int64_t)i * nkb + kb];
-                acc += a * sw[(int64_t)j * nkb + kb];
+                acc = fmaf(a, sw[(int64_t)j * nkb + kb], acc);
             }
             y[(int64_t)i * n + j] = acc;
         }
+}
+
+/* The reference test's host emulation (tests/test_int8_mma_gemm.cu:102-112): the same with
+ * the last multiply and add separate, acc += ((float)ic * sx) * sw. Its gate against the
+ * kernel is 1e-5 relative (test_int8_mma_gemm.cu:207). */
+EXPORT void oracle_int8_mma_emu_sep(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw, int m,
+                                    int n, int k, float *y) {
+    const int nkb = k / 64;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < n; ++j) {
+            float acc = 0.f;
+            for (int kb = 0; kb < nkb; ++kb) {
+                int ic = 0;
+                for (int t = 0; t < 64; ++t)
+                    ic += (int)xq[(int64_t)i * k + kb * 64 + t] * (int)wq[(int64_t)j * k + kb * 64 + t];
+                const float a = (float)ic * sx[(int64_t)i * nkb + kb];
+                const float p = a * sw[(int64_t)j * nkb + kb];
+                acc = acc + p;
+            }
+            y[(int64_t)i * n + j] = acc;
+        }
+}
+
+/* fmaf over arrays (the oracle's fused multiply-add, pinned against exact rational
+ * arithmetic in the tests) */
+EXPORT void oracle_fmaf_n(const float *a, const float *b, const float *c, int64_t n, float *out) {
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = fmaf(a[i], b[i], c[i]);
 }
 
 /* p7_plug_res4_v1 slice to int8 (cuda/int8_mma_gemm.cu:157-163): element i is nibble i of
@@ -248,7 +282,7 @@ EXPORT void oracle_unpack_res4(const uint8_t *q4, int64_t n, int8_t *out) {
 }
 
 /* Fused late plug (cuda/int8_mma_gemm.cu:105-124,224-240): per kb, the base term then the
- * plug term are added to one accumulator: acc += (ic*sx)*sw; acc += (ip*sx)*sp. */
+ * plug term go into one accumulator: acc = fmaf(ic*sx, sw, acc); acc = fmaf(ip*sx, sp, acc). */
 EXPORT void oracle_int8_mma_plug_fused(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw,
                                        const int8_t *pq, const float *sp, int m, int n, int k, float *y) {
     const int nkb = k / 64;
@@ -264,15 +298,16 @@ EXPORT void oracle_int8_mma_plug_fused(const int8_t *xq, const float *sx, const 
                     ip += a * (int)pq[(int64_t)j * k + kb * 64 + t];
                 }
                 const float xs = sx[(int64_t)i * nkb + kb];
-                acc += ((float)ic * xs) * sw[(int64_t)j * nkb + kb];
-                acc += ((float)ip * xs) * sp[(int64_t)j * nkb + kb];
+                acc = fmaf((float)ic * xs, sw[(int64_t)j * nkb + kb], acc);
+                acc = fmaf((float)ip * xs, sp[(int64_t)j * nkb + kb], acc);
             }
             y[(int64_t)i * n + j] = acc;
         }
 }
 
-/* Activation quantization residual re-quantized (cuda/int8_mma_gemm.cu:172-190): per (row,
- * 64-block) r = x - (float)xq * sx as a product then a difference (no fused multiply-add),
+/* Activation quantization residual re-quantized (cuda/int8_mma_gemm.cu:182-200): per (row,
+ * 64-block) r = fmaf(-(float)xq, sx, x) (the reference's x - xq * sx under nvcc's default
+ * contraction),
  * s = amax|r| > 0 ? amax / 127 : 1 (NaN skipped), rq = clamp(cvt(rint(r / s)), -127, 127). */
 EXPORT void oracle_quant_act_resid(const uint16_t *x, const int8_t *xq, const float *sx, int m, int k, int8_t *rq,
                                    float *sr) {
@@ -284,8 +319,7 @@ EXPORT void oracle_quant_act_resid(const uint16_t *x, const int8_t *xq, const fl
             const float s0 = sx[(int64_t)r * nkb + kb];
             float res[64], am = 0.f;
             for (int t = 0; t < 64; ++t) {
-                const float prod = (float)xq[base + t] * s0;
-                res[t] = bf16_to_f32(x[base + t]) - prod;
+                res[t] = fmaf(-(float)xq[base + t], s0, bf16_to_f32(x[base + t]));
                 am = fmaxf(am, fabsf(res[t]));
             }
             const float s = (am > 0.f) ? (am / 127.f) : 1.f;

@@ -213,6 +213,8 @@ class Oracle:
             "oracle_htile_f64": ([vp, vp, vp, vp, vp, vp, i32, i32, i32, i32], None),
             "oracle_quant_act": ([vp, i32, i32, vp, vp], None),
             "oracle_int8_mma_emu": ([vp, vp, vp, vp, i32, i32, i32, vp], None),
+            "oracle_int8_mma_emu_sep": ([vp, vp, vp, vp, i32, i32, i32, vp], None),
+            "oracle_fmaf_n": ([vp, vp, vp, i64, vp], None),
             "oracle_int8_gemm_i32": ([vp, vp, i32, i32, i32, i32, i32, vp], None),
             "oracle_int8_scale_bf16": ([vp, vp, vp, i32, i32, vp], None),
             "oracle_unpack_res4": ([vp, i64, vp], None),
@@ -293,10 +295,25 @@ class Oracle:
         return xq, sx
 
     def int8_mma_emu(self, xq, sx, wq, sw, m, n, k) -> np.ndarray:
+        """The reference kernel's W8A8 arithmetic as its nvcc build compiles it (fused
+        multiply-add for the last step)."""
         y = np.empty(m * n, np.float32)
         xq, sx, wq, sw = (np.ascontiguousarray(t) for t in (xq, sx, wq, sw))
         self.lib.oracle_int8_mma_emu(_ptr(xq), _ptr(sx), _ptr(wq), _ptr(sw), m, n, k, _ptr(y))
         return y.reshape(m, n)
+
+    def int8_mma_emu_sep(self, xq, sx, wq, sw, m, n, k) -> np.ndarray:
+        """The reference test's host emulation: the last multiply and add separate."""
+        y = np.empty(m * n, np.float32)
+        xq, sx, wq, sw = (np.ascontiguousarray(t) for t in (xq, sx, wq, sw))
+        self.lib.oracle_int8_mma_emu_sep(_ptr(xq), _ptr(sx), _ptr(wq), _ptr(sw), m, n, k, _ptr(y))
+        return y.reshape(m, n)
+
+    def fmaf(self, a, b, c) -> np.ndarray:
+        a, b, c = (np.ascontiguousarray(t, np.float32) for t in (a, b, c))
+        out = np.empty(a.size, np.float32)
+        self.lib.oracle_fmaf_n(_ptr(a), _ptr(b), _ptr(c), a.size, _ptr(out))
+        return out
 
     def unpack_res4(self, q4, n: int) -> np.ndarray:
         q4 = np.ascontiguousarray(q4, np.uint8)

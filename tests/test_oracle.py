@@ -293,6 +293,63 @@ def test_int8_integer_parts_are_exact(oracle):
     assert np.array_equal(out, ref)
 
 
+def _round_f32(q):
+    """The f32 nearest to the rational q, ties to even (exact, no double rounding)."""
+    from fractions import Fraction
+    f = np.float32(float(q))
+    best = None
+    for cand in (np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))):
+        if not np.isfinite(cand):
+            continue
+        d = abs(Fraction(float(cand)) - q)
+        if best is None or d < best[0] or (d == best[0] and int(cand.view(np.uint32)) % 2 == 0):
+            best = (d, cand)
+    return best[1]
+
+
+def test_fmaf_is_one_rounding(oracle):
+    """The oracle's fused multiply-add is RN(a * b + c) computed once: checked against exact
+    rational arithmetic on random triples, on cancelling triples (c = -RN(a * b), where a
+    separate multiply and add gives exactly 0 and the fused form keeps the product's
+    rounding error) and on the INT8 epilogue's own operand ranges."""
+    from fractions import Fraction
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal(400).astype(np.float32) * np.float32(3.0)
+    b = rng.standard_normal(400).astype(np.float32)
+    c = rng.standard_normal(400).astype(np.float32)
+    c[:100] = -(a[:100] * b[:100])  # cancellation
+    a[300:] = (rng.integers(-260000, 260000, 100) * rng.uniform(1e-5, 1e-3, 100)).astype(np.float32)
+    b[300:] = rng.uniform(1e-4, 2e-2, 100).astype(np.float32)
+    c[300:] = rng.standard_normal(100).astype(np.float32) * np.float32(100.0)
+    got = oracle.fmaf(a, b, c)
+    for i in range(a.size):
+        want = _round_f32(Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i])))
+        assert got[i] == want, (i, a[i], b[i], c[i], got[i], want)
+    assert (got[:100] != 0).sum() > 50  # the separate form would give 0 for all of them
+
+
+def test_int8_emulation_within_the_reference_gate(oracle):
+    """The kernel-arithmetic emulation (fused last step, as nvcc's default contraction
+    compiles the reference kernel) against the reference test's host emulation (separate
+    multiply and add): within that test's pre-registered 1e-5 relative gate
+    (tests/test_int8_mma_gemm.cu:207) on its own kind of data (bf16 activations quantized by
+    the rule, N(0, 0.02) weights quantized per 64-block), and different in some bits, so the
+    two emulations are not the same function."""
+    rng = np.random.default_rng(12)
+    m, n, k = 9, 70, 1024
+    x = rng.standard_normal(m * k).astype(np.float32)
+    xq, sx = oracle.quant_act(G.f32_to_bf16_bits(x), m, k)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wb = w.reshape(n, k // 64, 64)
+    sw = (np.abs(wb).max(axis=2) / np.float32(127.0)).astype(np.float32)
+    wq = np.clip(np.rint(wb / sw[:, :, None]), -127, 127).astype(np.int8).reshape(-1)
+    fused = oracle.int8_mma_emu(xq, sx, wq, sw.reshape(-1), m, n, k)
+    sep = oracle.int8_mma_emu_sep(xq, sx, wq, sw.reshape(-1), m, n, k)
+    rel = float(np.linalg.norm((fused - sep).astype(np.float64)) / np.linalg.norm(sep.astype(np.float64)))
+    assert rel <= 1e-5, rel
+    assert (fused.view(np.uint32) != sep.view(np.uint32)).any()
+
+
 def test_int8_scale_bf16_special_cases(oracle):
     """The bf16 epilogue RNE(f32(acc) * sa * sb) on inputs whose answer is fixed without
     the formula: unit scales on |acc| <= 256 give the integer itself (exact in bf16);
