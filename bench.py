@@ -867,8 +867,8 @@ def counter_workload(torch, H, manifest_path):
     phase("gemv_m1_14336x4096", GEMV_KERNEL, 38, lambda: [c() for c in calls + calls], nbytes=38 * gemv_bytes(N, K))
     # prefill on the gate shape, 6 rotated pins (373 MB)
     pins = pins[:6]
-    for M, key, name in ((2048, "k_tile_big<2,GlintTileProducer,TileOutBF16>", "prefill_m2048_14336x4096"),
-                         (64, "k_tile_ss<64,", "prefill_m64_14336x4096")):
+    for M, key, name in ((2048, "k_tile_big<2,GlintTileProducer,TileOutBF16,0>", "prefill_m2048_14336x4096"),
+                         (64, "k_htile_rd<4,2>", "prefill_m64_14336x4096")):
         xm = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
         ym = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
         calls = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], xm, ym, M, N, K, 64, st) for p in pins]
@@ -896,7 +896,7 @@ def counter_workload(torch, H, manifest_path):
     lin = H.Int8MmaLinear(q.data_ptr(), sc.data_ptr(), N8, K8)
     call = bound(p7.int8_mma_gemm, xb, lin, yf, M, xq, sx, st)
     phase("int8_mma_gemm_abi_2048x8192x8192", "k_int8_mma_dma", 4, lambda: [call() for _ in range(4)],
-          ops=4 * 2.0 * M * N8 * K8, note="per-64 scales, kb-ordered f32 epilogue")
+          ops=4 * 2.0 * M * N8 * K8, note="per-64 scales, kb-ordered f32 epilogue, last step fused")
     Path(manifest_path).write_text(json.dumps({"phases": phases, "cu_num": CU_NUM, "simd_num": SIMD_NUM}, indent=1) + "\n")
 
 
