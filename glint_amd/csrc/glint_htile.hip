@@ -1246,6 +1246,241 @@ __global__ __launch_bounds__(64 * RD_STRIPS * KW, 1) void k_htile_rd(const uint8
             }
 }
 
+/* k_htile_rl: k_htile_rd (KW = 2) with the weights read as whole 128-B lines. In k_htile_rd
+ * a load instruction covers 16 rows x 64 B, half of a 128-B line per row, because lane l must
+ * hold row l % 16 for the MFMA; the two waves of a strip each take one half of every line.
+ * Here a wave's load instruction covers 8 rows x 128 B (lane l: row 8 kw + l / 8 of the strip,
+ * 16-B piece l % 8 of the line that holds both waves' chunks of an x chunk), so the memory
+ * requests are whole lines: with the same bytes and the same work, a timing probe of that load
+ * form ran the 14336 x 4096 M = 64 launch 12% faster, M = 16 18%.
+ *   - The lines go register -> LDS -> register into the MFMA layout, through the upper 128 B
+ *     of each 256-B row of the cell table, which the half fill leaves unused (256 rows: 4
+ *     strips x 2 buffers x 2 planes x 16 W rows). 16-B pieces are XOR-swizzled by row.
+ *   - Line X is loaded 2-3 steps before it is written to LDS (step X - 2, after that step's
+ *     barrier) and read back into registers at step X - 1 (after the next barrier); step X
+ *     dequantizes it. The absmax of a lane's 64-block comes by its own load, 3 steps ahead.
+ *   - x as in k_htile_rd; halves of an x chunk past the split's chunks are not loaded (zeros),
+ *     so a non-finite x value there cannot reach another row's sum through a zero weight. */
+#ifndef RD_FL
+#define RD_FL 1 /* M <= 64: k_htile_rl (0: k_htile_rd) */
+#endif
+template <int MB>
+__global__ __launch_bounds__(512, 1) void k_htile_rl(const uint8_t *__restrict__ hole, const uint8_t *__restrict__ plug,
+                                                     const float *__restrict__ absmax, const uint16_t *__restrict__ x,
+                                                     uint16_t *__restrict__ y, int M, int N, int K, int R, int cps,
+                                                     float *__restrict__ part, unsigned *ctr) {
+    constexpr int KW = 2, T = 512, STRIPS = 4;
+    constexpr int XROW = 256 * KW;      /* bytes of one x row of an x chunk (one W line) */
+    constexpr int XCH = 16 * MB * XROW; /* bytes of one x chunk */
+    constexpr int NX = XCH / 16 / T;    /* 16-B pieces of an x chunk per thread */
+    constexpr int U = 4;                /* W line register stages (x chunks per unrolled round) */
+    static_assert(NX >= 1 && NX * 16 * T == XCH, "x chunk split over the threads");
+    __shared__ float ltab[GLINT_LDS_CELLS64_WORDS];
+    __shared__ __attribute__((aligned(16))) uint8_t xb0[XCH], xb1[XCH];
+    uint8_t *const lt = (uint8_t *)ltab;
+    const int lane = threadIdx.x & 63, m16 = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int strip = w % STRIPS, kw = w / STRIPS;
+    const uint32_t lane4 = (uint32_t)(lane & 31) * 4u; /* the half-filled table: copy lane % 32 */
+    const int n0 = blockIdx.x * R;
+    const int nrows = min(R, N - n0); /* >= 1 */
+    const int c0 = blockIdx.z * cps;  /* even: the host keeps cps even */
+    const int nj = min(K >> 7, c0 + cps) - c0;
+    const int nxc = (nj + 1) >> 1; /* x chunks = W lines */
+    const uint32_t rowb = (uint32_t)K >> 1;
+
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(hole + (int64_t)n0 * rowb), (short)0, (int)((uint32_t)nrows * rowb), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(plug + (int64_t)n0 * rowb), (short)0, (int)((uint32_t)nrows * rowb), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(absmax + (int64_t)n0 * (K >> 6)), (short)0, (int)((uint32_t)nrows * (rowb >> 3)), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), GLINT_BUF_DWORD3);
+    /* the lane's line piece: row lr of the strip, 16-B piece lane % 8 */
+    const int lr = 8 * kw + (lane >> 3);
+    const uint32_t lofs = (uint32_t)(16 * strip + lr) * rowb + (uint32_t)(lane & 7) * 16u;
+    /* the lane's absmax: MFMA row 16 strip + m16, block g / 2 of the wave's chunk */
+    const uint32_t aofs = ((uint32_t)(16 * strip + m16) * (uint32_t)(K >> 6) + (uint32_t)(g >> 1)) * 4u;
+    /* LDS slots: W row r of plane pl in buffer b of this strip is table row
+     * ((strip * 2 + b) * 2 + pl) * 16 + r, bytes 128 .. 255; piece c sits at c ^ (r % 8) */
+    const uint32_t put0 = ((uint32_t)((strip * 2) * 2 * 16 + lr) << 8) + 128u +
+                          ((uint32_t)((lane & 7) ^ (lr & 7)) << 4);
+    const uint32_t get0 = ((uint32_t)((strip * 2) * 2 * 16 + m16) << 8) + 128u +
+                          ((uint32_t)((4 * kw + g) ^ (m16 & 7)) << 4);
+    constexpr uint32_t BUF = 2 * 16 * 256, PLANE = 16 * 256; /* byte steps of b and pl */
+    uint32_t xgo[NX], xlo[NX];
+    int xhalf[NX];
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+        const int sl = (int)threadIdx.x + T * i, r = sl / (16 * KW), pc = sl % (16 * KW);
+        xgo[i] = (uint32_t)r * (uint32_t)K * 2u + (uint32_t)(pc << 4);
+        xlo[i] = (uint32_t)(r * XROW + ((pc ^ (r & 15)) << 4));
+        xhalf[i] = pc >> 4; /* the W chunk of the line the piece belongs to */
+    }
+
+    struct WLine {
+        glint_u32x4 h, p;
+    };
+    WLine wl[U];      /* lines in the load layout */
+    WLine wb[2];      /* lines in the MFMA layout (this wave's chunk), from LDS */
+    float am[U];      /* absmax of the wave's chunk of x chunk X, stage X % U */
+    glint_u32x4 xr[2][NX];
+    auto wline = [&](int X, WLine &s) {
+        const uint32_t o = 2 * X < nj ? lofs + (uint32_t)(c0 + 2 * X) * 64u : RD_OOR;
+        s.h = __builtin_amdgcn_raw_buffer_load_b128(rh, o, 0, 0);
+        s.p = __builtin_amdgcn_raw_buffer_load_b128(rp, o, 0, 0);
+    };
+    auto aload = [&](int X, float &a) {
+        const int j = 2 * X + kw;
+        a = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(ra, j < nj ? aofs + (uint32_t)(c0 + j) * 8u : RD_OOR, 0, 0));
+    };
+    auto xload = [&](int X, glint_u32x4 (&xs)[NX]) {
+        const uint32_t c = (uint32_t)(c0 + KW * X);
+#pragma unroll
+        for (int i = 0; i < NX; ++i)
+            xs[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, 2 * X + xhalf[i] < nj ? xgo[i] + c * 256u : RD_OOR, 0, 0);
+    };
+    auto xstore = [&](uint8_t *buf, const glint_u32x4 (&xs)[NX]) {
+#pragma unroll
+        for (int i = 0; i < NX; ++i)
+            *(glint_u32x4 *)(buf + xlo[i]) = xs[i];
+    };
+    auto wput = [&](int X, const WLine &s) {
+        const uint32_t a = put0 + (uint32_t)(X & 1) * BUF;
+        *(glint_u32x4 *)(lt + a) = s.h;
+        *(glint_u32x4 *)(lt + a + PLANE) = s.p;
+    };
+    auto wget = [&](int X, WLine &s) {
+        const uint32_t a = get0 + (uint32_t)(X & 1) * BUF;
+        s.h = *(const glint_u32x4 *)(lt + a);
+        s.p = *(const glint_u32x4 *)(lt + a + PLANE);
+    };
+    auto dequant = [&](const WLine &s, float a, glint_bf16x8 (&bq)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t E = glint_codes_even(s.h[q], s.p[q]), O = glint_codes_odd(s.h[q], s.p[q]);
+            const float f0 = glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4));
+            const float f1 = glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4));
+            const float f2 = glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4));
+            const float f3 = glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4));
+            const float f4 = glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4));
+            const float f5 = glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4));
+            const float f6 = glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4));
+            const float f7 = glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4));
+            bq[q] = __builtin_bit_cast(glint_bf16x8,
+                                       glint_u32x4{glint_cvt_bf16x2(f0 * a, f1 * a), glint_cvt_bf16x2(f2 * a, f3 * a),
+                                                   glint_cvt_bf16x2(f4 * a, f5 * a), glint_cvt_bf16x2(f6 * a, f7 * a)});
+        }
+    };
+    glint_f32x4 acc[MB][1];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+        acc[mb][0] = glint_f32x4{0.f, 0.f, 0.f, 0.f};
+    auto aread = [&](const uint8_t *xs, int s, glint_bf16x8 (&af)[MB]) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+            af[mb] = __builtin_bit_cast(glint_bf16x8, *(const glint_u32x4 *)(xs + (16 * mb + m16) * XROW +
+                                                                             (((16 * kw + 4 * g + s) ^ m16) << 4)));
+    };
+    auto mma = [&](const uint8_t *xs, const glint_bf16x8 (&bq)[4]) {
+        glint_bf16x8 af[2][MB];
+        aread(xs, 0, af[0]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (s + 1 < 4)
+                aread(xs, s + 1, af[(s + 1) & 1]);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                acc[mb][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[s & 1][mb], bq[s], acc[mb][0], 0, 0, 0);
+        }
+    };
+    /* step X (u = X % U): x chunk X + 1 into LDS, x chunk X + 3 and the absmax of X + 3
+     * issued, line X + 2 into LDS, line X + 1 out of LDS, line X dequantized and multiplied;
+     * on even steps lines X + 4 and X + 5 go out into the stages lines X and X + 1 left */
+    auto step = [&](int X, int u) {
+        __syncthreads();
+        xstore((u & 1) ? xb0 : xb1, xr[(u + 1) & 1]);
+        xload(X + 3, xr[(u + 1) & 1]);
+        aload(X + 3, am[(u + 3) % U]);
+        wput(X + 2, wl[(u + 2) % U]);
+        wget(X + 1, wb[(u + 1) & 1]);
+        glint_bf16x8 bq[4];
+        dequant(wb[u & 1], am[u], bq);
+        if ((u & 1) == 0) {
+            wline(X + 4, wl[u]);
+            wline(X + 5, wl[u + 1]);
+        }
+        mma((u & 1) ? xb1 : xb0, bq);
+    };
+
+    GlintCellFillHN<(2048 + T - 1) / T> fill;
+    glint_cells_fillh_sload(fill);
+    __builtin_amdgcn_sched_barrier(0);
+    xload(0, xr[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    xload(1, xr[1]);
+    aload(0, am[0]);
+    aload(1, am[1]);
+    aload(2, am[2]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < U; ++s)
+        wline(s, wl[s]);
+    __builtin_amdgcn_sched_barrier(0);
+    glint_cells_fillh_sstore(ltab, fill);
+    xstore(xb0, xr[0]);
+    xload(2, xr[0]);
+    wput(0, wl[0]);
+    wput(1, wl[1]);
+    __syncthreads();
+    wget(0, wb[0]);
+    int X = 0;
+    for (; X + U <= nxc; X += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            step(X + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < U; ++u)
+        if (X + u < nxc)
+            step(X + u, u);
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0); /* the trailing dropped loads */
+
+    /* the strip's two partials, added in kw order by wave kw = 0 (the x buffers are free) */
+    float *red = (float *)xb0;
+    static_assert(STRIPS * 64 * MB * 4 * 4 <= XCH, "partials fit an x buffer");
+    __syncthreads();
+    if (kw > 0)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                red[((strip * MB + mb) * 4 + i) * 64 + lane] = acc[mb][0][i];
+    __syncthreads();
+    if (kw == 0)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[mb][0][i] += red[((strip * MB + mb) * 4 + i) * 64 + lane];
+    __syncthreads(); /* the split-K epilogue's flag word lives in xb0 */
+    if (gridDim.z > 1 && !tile_splitk_epilogue<MB, 1, 64 * STRIPS>(acc, part, ctr, *(unsigned *)xb1,
+                                                                    (int)threadIdx.x, kw == 0))
+        return;
+    const int nl = 16 * strip + m16;
+    if (kw == 0 && nl < nrows)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 16 * mb + 4 * g + i;
+                if (m < M)
+                    y[(int64_t)m * N + n0 + nl] = glint_f32_to_bf16(acc[mb][0][i]);
+            }
+}
+
 /* k_htile_rd over an M <= 64, BF16-out prefill. Returns 1 where the shape does not fit
  * (K % 128 != 0, offsets beyond 31 bits; the caller takes the LDS tiles), -5 where a
  * `fixed` workspace is too small for the split plan, else 0 or -3. */
@@ -1256,6 +1491,8 @@ static int htile_launch_rd_mb(const uint8_t *hole, const uint8_t *plug, const fl
     constexpr int RMAX = 16 * RD_STRIPS, TILE_FLOATS = MB * 4 * 64 * RD_STRIPS;
     auto plan = [&](int ks, int &cps, int &R, unsigned &gx) {
         cps = (nc + ks - 1) / ks;
+        if (RD_FL)
+            cps = (cps + 1) & ~1; /* k_htile_rl: splits start on a W line */
         ks = (nc + cps - 1) / cps;
         R = (int)std::min<int64_t>(RMAX, (((int64_t)N * ks + cus - 1) / cus + 7) / 8 * 8);
         gx = (unsigned)((N + R - 1) / R);
@@ -1275,8 +1512,12 @@ static int htile_launch_rd_mb(const uint8_t *hole, const uint8_t *plug, const fl
             ws = GlintSplitWs{nullptr, nullptr, 0, 0};
         }
     }
-    k_htile_rd<MB, RD_KW><<<dim3(gx, 1, (unsigned)ks), 64 * RD_STRIPS * RD_KW, 0, st>>>(
-        hole, plug, absmax, x, y, M, N, K, R, cps, ws.part, ws.ctr);
+    if (RD_FL)
+        k_htile_rl<MB><<<dim3(gx, 1, (unsigned)ks), 512, 0, st>>>(hole, plug, absmax, x, y, M, N, K, R, cps, ws.part,
+                                                                ws.ctr);
+    else
+        k_htile_rd<MB, RD_KW><<<dim3(gx, 1, (unsigned)ks), 64 * RD_STRIPS * RD_KW, 0, st>>>(
+            hole, plug, absmax, x, y, M, N, K, R, cps, ws.part, ws.ctr);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 static int htile_launch_rd(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y,
