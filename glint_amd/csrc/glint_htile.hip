@@ -716,6 +716,12 @@ __global__ __launch_bounds__(MAXT) void k_htile_gemv_mr(const void *__restrict__
  * Measured against the 64-row MFMA tile (k_tile_ss) on 14336 x 4096: M = 2 14.2-15.6 us
  * against 35.0, M = 4 17.8-18.2 against 35.3, M = 5..8 24.7-24.9 against 34.3-34.6 (the
  * 8-row template holds 128 VGPRs of x and runs at 2 waves per SIMD). */
+#ifndef GEMV_MR_RL
+#define GEMV_MR_RL 4 /* BF16 out: above this many rows k_htile_rl goes first where it takes the shape */
+#endif
+#ifndef GEMV_MR_RL_F32
+#define GEMV_MR_RL_F32 6 /* f32 out: above this many rows k_htile_rl goes first where it takes the shape */
+#endif
 #ifndef GEMV_MR_MAX_F32
 #define GEMV_MR_MAX_F32 4 /* largest M of the f32-out small-M GEMV (x as f32: MR x 32 registers) */
 #endif
@@ -1264,11 +1270,19 @@ __global__ __launch_bounds__(64 * RD_STRIPS * KW, 1) void k_htile_rd(const uint8
 #ifndef RD_FL
 #define RD_FL 1 /* M <= 64: k_htile_rl (0: k_htile_rd) */
 #endif
-template <int MB>
+#ifndef RD_FL_F32
+#define RD_FL_F32 1 /* f32 out at M <= 64: k_htile_rl's three-plane form (0: the f32 tiles) */
+#endif
+/* F32: f32 out (the reference ABI) with the weights w = CELLS * absmax split into three exact
+ * BF16 planes (GlintTileProducer::finish_split's rule), each multiplied by x in the MFMA: the
+ * products are exact and only the f32 sums differ from a scalar loop's. A step dequantizes
+ * and multiplies one MFMA step at a time (3 B operands, 3 MB MFMAs). */
+template <int MB, bool F32 = false>
 __global__ __launch_bounds__(512, 1) void k_htile_rl(const uint8_t *__restrict__ hole, const uint8_t *__restrict__ plug,
                                                      const float *__restrict__ absmax, const uint16_t *__restrict__ x,
-                                                     uint16_t *__restrict__ y, int M, int N, int K, int R, int cps,
-                                                     float *__restrict__ part, unsigned *ctr) {
+                                                     typename std::conditional<F32, float, uint16_t>::type *__restrict__ y,
+                                                     int M, int N, int K, int R, int cps, float *__restrict__ part,
+                                                     unsigned *ctr) {
     constexpr int KW = 2, T = 512, STRIPS = 4;
     constexpr int XROW = 256 * KW;      /* bytes of one x row of an x chunk (one W line) */
     constexpr int XCH = 16 * MB * XROW; /* bytes of one x chunk */
@@ -1396,6 +1410,60 @@ __global__ __launch_bounds__(512, 1) void k_htile_rl(const uint8_t *__restrict__
                 acc[mb][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[s & 1][mb], bq[s], acc[mb][0], 0, 0, 0);
         }
     };
+    /* F32: MFMA step s's 8 weights of this lane as three BF16 planes (hi, mid, lo: w == hi + mid
+     * + lo exactly; an infinite w keeps mid = lo = 0, a NaN w stays NaN in hi) */
+    auto split3 = [&](const WLine &s, float a, int q, glint_bf16x8 (&bp)[3]) {
+        const uint32_t E = glint_codes_even(s.h[q], s.p[q]), O = glint_codes_odd(s.h[q], s.p[q]);
+        float v[8];
+        v[0] = glint_lds_f32(ltab, glint_cell_addr<0>(E, lane4));
+        v[1] = glint_lds_f32(ltab, glint_cell_addr<0>(O, lane4));
+        v[2] = glint_lds_f32(ltab, glint_cell_addr<1>(E, lane4));
+        v[3] = glint_lds_f32(ltab, glint_cell_addr<1>(O, lane4));
+        v[4] = glint_lds_f32(ltab, glint_cell_addr<2>(E, lane4));
+        v[5] = glint_lds_f32(ltab, glint_cell_addr<2>(O, lane4));
+        v[6] = glint_lds_f32(ltab, glint_cell_addr<3>(E, lane4));
+        v[7] = glint_lds_f32(ltab, glint_cell_addr<3>(O, lane4));
+        const bool big = !(__builtin_fabsf(a) < 0x1p126f); /* only there can w be infinite */
+        uint32_t hi[8], mid[8], lo[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float w = v[i] * a;
+            const float h = __uint_as_float(__float_as_uint(w) & 0xFFFF0000u);
+            float r1 = w - h;
+            if (big)
+                r1 = __builtin_isinf(w) ? 0.0f : r1;
+            const float md = __uint_as_float(__float_as_uint(r1) & 0xFFFF0000u);
+            hi[i] = __float_as_uint(h);
+            mid[i] = __float_as_uint(md);
+            lo[i] = __float_as_uint(r1 - md);
+        }
+        uint32_t ph[4], pm[4], pl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ph[j] = __builtin_amdgcn_perm(hi[2 * j + 1], hi[2 * j], 0x07060302u);
+            pm[j] = __builtin_amdgcn_perm(mid[2 * j + 1], mid[2 * j], 0x07060302u);
+            pl[j] = __builtin_amdgcn_perm(lo[2 * j + 1], lo[2 * j], 0x07060302u);
+        }
+        bp[0] = __builtin_bit_cast(glint_bf16x8, glint_u32x4{ph[0], ph[1], ph[2], ph[3]});
+        bp[1] = __builtin_bit_cast(glint_bf16x8, glint_u32x4{pm[0], pm[1], pm[2], pm[3]});
+        bp[2] = __builtin_bit_cast(glint_bf16x8, glint_u32x4{pl[0], pl[1], pl[2], pl[3]});
+    };
+    auto mma3 = [&](const uint8_t *xs, const WLine &s, float a) {
+        glint_bf16x8 af[2][MB];
+        aread(xs, 0, af[0]);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            glint_bf16x8 bp[3];
+            split3(s, a, st, bp);
+            if (st + 1 < 4)
+                aread(xs, st + 1, af[(st + 1) & 1]);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+                    acc[mb][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[st & 1][mb], bp[pl], acc[mb][0], 0, 0, 0);
+        }
+    };
     /* step X (u = X % U): x chunk X + 1 into LDS, x chunk X + 3 and the absmax of X + 3
      * issued, line X + 2 into LDS, line X + 1 out of LDS, line X dequantized and multiplied;
      * on even steps lines X + 4 and X + 5 go out into the stages lines X and X + 1 left */
@@ -1406,13 +1474,21 @@ __global__ __launch_bounds__(512, 1) void k_htile_rl(const uint8_t *__restrict__
         aload(X + 3, am[(u + 3) % U]);
         wput(X + 2, wl[(u + 2) % U]);
         wget(X + 1, wb[(u + 1) & 1]);
-        glint_bf16x8 bq[4];
-        dequant(wb[u & 1], am[u], bq);
-        if ((u & 1) == 0) {
-            wline(X + 4, wl[u]);
-            wline(X + 5, wl[u + 1]);
+        if constexpr (F32) {
+            if ((u & 1) == 0) {
+                wline(X + 4, wl[u]);
+                wline(X + 5, wl[u + 1]);
+            }
+            mma3((u & 1) ? xb1 : xb0, wb[u & 1], am[u]);
+        } else {
+            glint_bf16x8 bq[4];
+            dequant(wb[u & 1], am[u], bq);
+            if ((u & 1) == 0) {
+                wline(X + 4, wl[u]);
+                wline(X + 5, wl[u + 1]);
+            }
+            mma((u & 1) ? xb1 : xb0, bq);
         }
-        mma((u & 1) ? xb1 : xb0, bq);
     };
 
     GlintCellFillHN<(2048 + T - 1) / T> fill;
@@ -1476,17 +1552,22 @@ __global__ __launch_bounds__(512, 1) void k_htile_rl(const uint8_t *__restrict__
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = 16 * mb + 4 * g + i;
-                if (m < M)
-                    y[(int64_t)m * N + n0 + nl] = glint_f32_to_bf16(acc[mb][0][i]);
+                if (m < M) {
+                    if constexpr (F32)
+                        y[(int64_t)m * N + n0 + nl] = acc[mb][0][i];
+                    else
+                        y[(int64_t)m * N + n0 + nl] = glint_f32_to_bf16(acc[mb][0][i]);
+                }
             }
 }
 
-/* k_htile_rd over an M <= 64, BF16-out prefill. Returns 1 where the shape does not fit
- * (K % 128 != 0, offsets beyond 31 bits; the caller takes the LDS tiles), -5 where a
- * `fixed` workspace is too small for the split plan, else 0 or -3. */
-template <int MB>
+/* k_htile_rl (k_htile_rd) over an M <= 64 prefill, BF16 out, or f32 out (F32: k_htile_rl
+ * only). Returns 1 where the shape does not fit (K % 128 != 0, offsets beyond 31 bits; the
+ * caller takes the LDS tiles), -5 where a `fixed` workspace is too small for the split plan,
+ * else 0 or -3. */
+template <int MB, bool F32>
 static int htile_launch_rd_mb(const uint8_t *hole, const uint8_t *plug, const float *absmax, const uint16_t *x,
-                              uint16_t *y, int M, int N, int K, hipStream_t st, const GlintSplitWs *fixed) {
+                              void *y, int M, int N, int K, hipStream_t st, const GlintSplitWs *fixed) {
     const int cus = glint_cu_count(), nc = K >> 7;
     constexpr int RMAX = 16 * RD_STRIPS, TILE_FLOATS = MB * 4 * 64 * RD_STRIPS;
     auto plan = [&](int ks, int &cps, int &R, unsigned &gx) {
@@ -1512,26 +1593,29 @@ static int htile_launch_rd_mb(const uint8_t *hole, const uint8_t *plug, const fl
             ws = GlintSplitWs{nullptr, nullptr, 0, 0};
         }
     }
-    if (RD_FL)
-        k_htile_rl<MB><<<dim3(gx, 1, (unsigned)ks), 512, 0, st>>>(hole, plug, absmax, x, y, M, N, K, R, cps, ws.part,
-                                                                ws.ctr);
+    if (F32)
+        k_htile_rl<MB, true><<<dim3(gx, 1, (unsigned)ks), 512, 0, st>>>(hole, plug, absmax, x, (float *)y, M, N, K, R,
+                                                                      cps, ws.part, ws.ctr);
+    else if (RD_FL)
+        k_htile_rl<MB><<<dim3(gx, 1, (unsigned)ks), 512, 0, st>>>(hole, plug, absmax, x, (uint16_t *)y, M, N, K, R, cps,
+                                                                ws.part, ws.ctr);
     else
         k_htile_rd<MB, RD_KW><<<dim3(gx, 1, (unsigned)ks), 64 * RD_STRIPS * RD_KW, 0, st>>>(
-            hole, plug, absmax, x, y, M, N, K, R, cps, ws.part, ws.ctr);
+            hole, plug, absmax, x, (uint16_t *)y, M, N, K, R, cps, ws.part, ws.ctr);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
+template <bool F32 = false>
 static int htile_launch_rd(const uint8_t *hole, const uint8_t *plug, const float *absmax, const void *x, void *y,
                            int M, int N, int K, hipStream_t st, const GlintSplitWs *fixed) {
-    if (!RD_ON || M < 1 || M > 64 || K % 128 != 0 || (int64_t)M * K * 2 >= (int64_t)RD_OOR ||
+    if (!RD_ON || (F32 && !RD_FL_F32) || M < 1 || M > 64 || K % 128 != 0 || (int64_t)M * K * 2 >= (int64_t)RD_OOR ||
         (int64_t)16 * RD_STRIPS * (K / 2) >= (int64_t)RD_OOR)
         return 1;
     const uint16_t *xb = (const uint16_t *)x;
-    uint16_t *yb = (uint16_t *)y;
     if (M <= 16)
-        return htile_launch_rd_mb<1>(hole, plug, absmax, xb, yb, M, N, K, st, fixed);
+        return htile_launch_rd_mb<1, F32>(hole, plug, absmax, xb, y, M, N, K, st, fixed);
     if (M <= 32)
-        return htile_launch_rd_mb<2>(hole, plug, absmax, xb, yb, M, N, K, st, fixed);
-    return htile_launch_rd_mb<4>(hole, plug, absmax, xb, yb, M, N, K, st, fixed);
+        return htile_launch_rd_mb<2, F32>(hole, plug, absmax, xb, y, M, N, K, st, fixed);
+    return htile_launch_rd_mb<4, F32>(hole, plug, absmax, xb, y, M, N, K, st, fixed);
 }
 
 /* f32 output at M > 1 (the reference ABI's prefill use): 3-plane k_tile_mfma, whose
@@ -1581,8 +1665,21 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
      * the tiles */
     const bool gemv_x_ok = M == 1 && fast_ok && (K / GEMV_X_EL + 63) / 64 <= GEMV_X_S_MAX;
     const bool mfma_ok = fast_ok && !gemv_x_ok;
-    if (mfma_ok && GEMV_MR_ON && gemv_mr_takes(M, K, !OUT_BF16))
+    /* BF16 out above GEMV_MR_RL rows: k_htile_rl first (14336 x 4096 M = 5 .. 8: 18.0-19.2 us
+     * against 22.5-23.8 for the 8-row small-M GEMV; 4096 x 14336 18.3-18.4 against 24.8-25.0),
+     * the small-M GEMV where that does not take the shape */
+    const bool rl_first = M > (OUT_BF16 ? GEMV_MR_RL : GEMV_MR_RL_F32);
+    if (mfma_ok && GEMV_MR_ON && !rl_first && gemv_mr_takes(M, K, !OUT_BF16))
         return htile_launch_gemv_mr<!OUT_BF16>(hole, plug, absmax, x, y, M, N, K, st);
+    /* f32 out from GEMV_MR_RL_F32 + 1 rows: k_htile_rl's three-plane form (14336 x 4096 M = 8
+     * 31.3 -> 30.1 us, 16 49.7 -> 30.2, 32 49.9 -> 33.9, 64 50.3 -> 41.4; 4096 x 14336 M = 8
+     * 33.6 -> 29.2, 64 61.8 -> 39.8, against the two small-M launches and the f32 tiles; at
+     * M = 5 the two launches were faster, 30.6 against 31.5) */
+    if (!OUT_BF16 && mfma_ok && M > GEMV_MR_RL_F32 && M <= 64) {
+        const int rc = htile_launch_rd<true>(hole, plug, absmax, x, y, M, N, K, st, fixed);
+        if (rc != 1)
+            return rc;
+    }
     if (!OUT_BF16 && mfma_ok && GEMV_MR_ON && GEMV_MR_F32_TWICE && M > GEMV_MR_MAX_F32 && M <= 2 * GEMV_MR_MAX_F32 &&
         gemv_mr_takes(GEMV_MR_MAX_F32, K, true)) {
         /* f32 out at M = 5 .. 8: the 4-row form twice (the weights are read twice), rows 4 ..
@@ -1611,6 +1708,8 @@ static int htile_launch(const uint8_t *hole, const uint8_t *plug, const float *a
             if (rc != 1)
                 return rc;
         }
+        if (rl_first && GEMV_MR_ON && gemv_mr_takes(M, K, false))
+            return htile_launch_gemv_mr<false>(hole, plug, absmax, x, y, M, N, K, st);
         if (M <= 64)
             planned = TILE_SS_BN32
                           ? tile_ss_launch<64, 32, TILE_RX, GlintTileProducer, TileOutBF16>(p, xb, yb, M, N, K, st, 2, fixed)
