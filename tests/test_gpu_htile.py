@@ -238,6 +238,41 @@ def test_bf16_small_m_tiles_vs_float64(oracle, M, N, K):
     assert torch.equal(again.view(torch.int16), y[:M].view(torch.int16))
 
 
+@pytest.mark.parametrize("f32", [False, True])
+@pytest.mark.parametrize("M,N,K", [(16, 300, 1152), (64, 64, 14464)])
+def test_small_m_tiles_nonfinite_x_stays_in_its_row(oracle, M, N, K, f32):
+    """An infinite x value reaches its own output row only. K % 256 == 128 leaves the last
+    W line of a row half used, so the second half of the last x chunk lies past the row's end
+    (the next row's first 128 values), or past the split's chunks where K is split (N = 64 at
+    K = 14464: 4 splits); those halves are not loaded, so no zero weight meets them. x row 1
+    holds +inf at k = 5, row 2 -inf at k = K - 3: rows 1 and 2 come out non-finite, every
+    other row finite and within the bound against float64 (BF16 out and the f32 ABI)."""
+    torch = torch_cuda()
+    print(f"small-M non-finite x M={M} N={N} K={K} f32={f32}", flush=True)
+    hole, plug, am = _encoded_weight(oracle, N, K, 5100 + K)
+    rng = np.random.default_rng(5101 + M)
+    xb = bf16_bits(rng.normal(0, 1, M * K).astype(np.float32)).reshape(M, K)
+    xb[1, 5] = 0x7F80   # +inf
+    xb[2, K - 3] = 0xFF80  # -inf
+    x = dev(xb.reshape(-1))
+    if f32:
+        got = host(H.htile_f32(hole, plug, am, x.reshape(M, K), N, K, 64)).reshape(M, N).astype(np.float64)
+    else:
+        got = G.bf16_bits_to_f32(host(H.htile_bf16(hole, plug, am, x.reshape(M, K), N, K, 64), np.uint16).reshape(-1))
+        got = got.astype(np.float64).reshape(M, N)
+    assert not np.isfinite(got[1:3]).any()
+    rows = np.array([r for r in range(M) if r not in (1, 2)])
+    ref, asum = oracle.htile_f64(host(hole), host(plug), host(am), xb[rows].reshape(-1), rows.size, N, K, 64)
+    ref, asum = ref.reshape(rows.size, N), asum.reshape(rows.size, N)
+    g = got[rows]
+    assert np.isfinite(g).all()
+    if f32:
+        bound = (K + 2) * 2.0 ** -23 * asum
+    else:
+        bound = np.abs(ref) * 2.0 ** -8 + asum * (2.0 ** -9 + (K + 2) * 2.0 ** -23) * 1.01
+    assert (np.abs(g - ref) <= bound).all(), float((np.abs(g - ref) / bound).max())
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 1024, 4096), (300, 1000, 576), (513, 1100, 1024), (2048, 384, 640),
                                    (2000, 6100, 1088), (4096, 4096, 576)])
 def test_bf16_prefill_tiles_rel_frobenius(oracle, M, N, K):
