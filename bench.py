@@ -868,7 +868,7 @@ def counter_workload(torch, H, manifest_path):
     # prefill on the gate shape, 6 rotated pins (373 MB)
     pins = pins[:6]
     for M, key, name in ((2048, "k_tile_big<2,GlintTileProducer,TileOutBF16,0>", "prefill_m2048_14336x4096"),
-                         (64, "k_htile_rl<4>", "prefill_m64_14336x4096")):
+                         (64, "k_htile_rl<4,false>", "prefill_m64_14336x4096")):
         xm = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
         ym = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
         calls = [bound(lib.launch_glint_htile_bf16_stream, p[0], p[1], p[2], xm, ym, M, N, K, 64, st) for p in pins]
