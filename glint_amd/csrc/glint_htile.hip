@@ -1270,6 +1270,10 @@ __global__ __launch_bounds__(64 * RD_STRIPS * KW, 1) void k_htile_rd(const uint8
 #ifndef RD_FL
 #define RD_FL 1 /* M <= 64: k_htile_rl (0: k_htile_rd) */
 #endif
+#ifndef RL_STAGES
+#define RL_STAGES 4 /* k_htile_rl: W line register stages (6: M = 64 gate 29.5 -> 30.2 us, 8: 31.1; the
+                     * prologue's longer first load burst costs more than the deeper lead gains) */
+#endif
 #ifndef RD_FL_F32
 #define RD_FL_F32 1 /* f32 out at M <= 64: k_htile_rl's three-plane form (0: the f32 tiles) */
 #endif
@@ -1287,7 +1291,8 @@ __global__ __launch_bounds__(512, 1) void k_htile_rl(const uint8_t *__restrict__
     constexpr int XROW = 256 * KW;      /* bytes of one x row of an x chunk (one W line) */
     constexpr int XCH = 16 * MB * XROW; /* bytes of one x chunk */
     constexpr int NX = XCH / 16 / T;    /* 16-B pieces of an x chunk per thread */
-    constexpr int U = 4;                /* W line register stages (x chunks per unrolled round) */
+    constexpr int U = RL_STAGES;        /* W line register stages (x chunks per unrolled round) */
+    static_assert(U % 2 == 0 && U >= 4, "stages in pairs, lines loaded U - 2 steps ahead of their LDS write");
     static_assert(NX >= 1 && NX * 16 * T == XCH, "x chunk split over the threads");
     __shared__ float ltab[GLINT_LDS_CELLS64_WORDS];
     __shared__ __attribute__((aligned(16))) uint8_t xb0[XCH], xb1[XCH];
@@ -1476,16 +1481,16 @@ __global__ __launch_bounds__(512, 1) void k_htile_rl(const uint8_t *__restrict__
         wget(X + 1, wb[(u + 1) & 1]);
         if constexpr (F32) {
             if ((u & 1) == 0) {
-                wline(X + 4, wl[u]);
-                wline(X + 5, wl[u + 1]);
+                wline(X + U, wl[u]);
+                wline(X + U + 1, wl[u + 1]);
             }
             mma3((u & 1) ? xb1 : xb0, wb[u & 1], am[u]);
         } else {
             glint_bf16x8 bq[4];
             dequant(wb[u & 1], am[u], bq);
             if ((u & 1) == 0) {
-                wline(X + 4, wl[u]);
-                wline(X + 5, wl[u + 1]);
+                wline(X + U, wl[u]);
+                wline(X + U + 1, wl[u + 1]);
             }
             mma((u & 1) ? xb1 : xb0, bq);
         }
