@@ -794,6 +794,10 @@ __global__ __launch_bounds__(512) void k_int8_mma_dma(const int8_t *__restrict__
 #ifndef Q_RING8
 #define Q_RING8 1 /* the narrow tiles on 8 waves (k_int8_mma_ring8) */
 #endif
+#ifndef Q_RING8_WIDE
+#define Q_RING8_WIDE 0 /* the 64 x 64 tiles on 8 waves too (slower: 128 x 14336 x 4096 49.5 -> 62.5 us,
+                        * 256 x 4096 x 4096 24.2 -> 27.7) */
+#endif
 #ifndef Q_PER_STEP
 #define Q_PER_STEP 2 /* K slices per barrier (1 or 2) */
 #endif
@@ -960,21 +964,26 @@ static void q_launch_quant(const void *x, int m, int k_in, int8_t *xq, float *sx
     k_quant_act<<<(unsigned)grid, 256, 0, st>>>((const glint_u32x4 *)x, nchunk8, (glint_u32x2 *)xq, sx);
 }
 
-/* The narrow form of k_int8_mma_ring (64 x 32 tiles, where 64 x 64 ones would leave CUs
- * idle) over 8 waves: wave w computes rows 16 (w / 2) .. +15, columns 16 (w % 2) .. +15, so
- * each SIMD holds two waves. Per slice each wave issues one DMA (waves 0-3 16 rows of A,
- * waves 4-5 16 rows of B, wave 6 the tile's 64 sx, wave 7 64 sw of which 32 are used), so
- * every wave's wait count is the same and only the 32 W rows the tile uses are staged.
- * Against the 4-wave form (32 x 16 per wave, 64 W rows staged): M 70 N 4096 K 3072 17.4 ->
- * 15.0 us for the whole call (quantization included), bit-identical. Epilogue as
- * k_int8_mma_dma. */
-template <bool ACCUM>
+/* k_int8_mma_ring over 8 waves, two per SIMD: 64 x 32 NB tiles, wave w computes rows
+ * 16 (w / 2) .. +15 and NB 16-column blocks from column 16 NB (w % 2). Every wave issues the
+ * same number of DMAs per slice, so the wait counts are uniform: NB = 1 one (waves 0-3 16
+ * rows of A each, waves 4-5 16 rows of B, wave 6 the tile's 64 sx, wave 7 64 sw of which 32
+ * are used: only the W rows the tile uses are staged); NB = 2 two (waves 0-3 16 rows of A,
+ * waves 4-7 16 rows of B, wave 0 sx, wave 1 sw and the others copies of them into spare
+ * slots). Against the 4-wave form (32 x 16 NB per wave): M 70 N 4096 K 3072 (NB = 1) 17.4 ->
+ * 15.0 us for the whole call (quantization included), bit-identical; at NB = 2 it was slower
+ * (Q_RING8_WIDE). Epilogue as k_int8_mma_dma. */
+template <bool ACCUM, int NB>
 __global__ __launch_bounds__(512) void k_int8_mma_ring8(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
                                                         const float *__restrict__ sx, const float *__restrict__ sw,
                                                         float *__restrict__ y, int M, int N, int K) {
     static_assert(Q_NBUF == 8, "ring slots are declared one by one");
-#define Q_SLOT(i) __shared__ __attribute__((aligned(16))) int8_t sA##i[64 * G2_LDS_ROW], sB##i[32 * G2_LDS_ROW]; \
-    __shared__ __attribute__((aligned(16))) float sS##i[128];
+    static_assert(NB == 1 || NB == 2, "16-column blocks per wave");
+    constexpr int BR = 32 * NB;         /* W rows of a tile */
+    constexpr int ND = NB;              /* DMAs per wave per slice */
+    constexpr int SW = NB == 1 ? 128 : 512; /* scale floats per slot: sx, sw (and the copies) */
+#define Q_SLOT(i) __shared__ __attribute__((aligned(16))) int8_t sA##i[64 * G2_LDS_ROW], sB##i[BR * G2_LDS_ROW]; \
+    __shared__ __attribute__((aligned(16))) float sS##i[SW];
     Q_SLOT(0) Q_SLOT(1) Q_SLOT(2) Q_SLOT(3) Q_SLOT(4) Q_SLOT(5) Q_SLOT(6) Q_SLOT(7)
 #undef Q_SLOT
     auto slotA = [&](int i) -> int8_t * {
@@ -991,54 +1000,64 @@ __global__ __launch_bounds__(512) void k_int8_mma_ring8(const int8_t *__restrict
     };
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 32;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * BR;
     const int nkb = K / 64;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    /* this wave's DMA: source resource, per-lane offset, LDS destination, size */
-    __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t vo;
-    if (wave < 6) {
-        const bool isA = wave < 4;
-        const int rbase = isA ? 16 * wave : 16 * (wave - 4);
-        const int r = rbase + (lane >> 2);
-        const int c = (lane & 3) ^ (((r >> 1) ^ ((r >> 3) & 1)) & 3);
-        rsrc = isA ? __builtin_amdgcn_make_buffer_rsrc((void *)A, (short)0, (int)((uint32_t)M * (uint32_t)K), GLINT_BUF_DWORD3)
-                   : __builtin_amdgcn_make_buffer_rsrc((void *)B, (short)0, (int)((uint32_t)N * (uint32_t)K), GLINT_BUF_DWORD3);
-        vo = (uint32_t)min((isA ? m0 : n0) + r, (isA ? M : N) - 1) * (uint32_t)K + (uint32_t)c * 16u;
-    } else {
-        const bool rows = wave == 6;
-        rsrc = rows ? __builtin_amdgcn_make_buffer_rsrc((void *)sx, (short)0, (int)((uint32_t)M * (uint32_t)nkb * 4u), GLINT_BUF_DWORD3)
-                    : __builtin_amdgcn_make_buffer_rsrc((void *)sw, (short)0, (int)((uint32_t)N * (uint32_t)nkb * 4u), GLINT_BUF_DWORD3);
-        vo = (rows ? (uint32_t)min(m0 + lane, M - 1) : (uint32_t)min(n0 + lane, N - 1)) * (uint32_t)nkb * 4u;
-    }
+    float acc[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            acc[b][i] = 0.0f;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)A, (short)0, (int)((uint32_t)M * (uint32_t)K), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)B, (short)0, (int)((uint32_t)N * (uint32_t)K), GLINT_BUF_DWORD3);
+    /* operand rows: waves 0-3 A rows 16 w, waves 4 .. 4 + BR / 16 - 1 B rows 16 (w - 4) */
+    const bool opA = wave < 4, opB = !opA && wave < 4 + BR / 16;
+    const int r = (opA ? 16 * wave : 16 * (wave - 4)) + (lane >> 2);
+    const int c = (lane & 3) ^ (((r >> 1) ^ ((r >> 3) & 1)) & 3);
+    const uint32_t ovo = opA ? (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)c * 16u
+                             : (uint32_t)min(n0 + r, N - 1) * (uint32_t)K + (uint32_t)c * 16u;
+    /* scales: NB = 1 waves 6 (sx) and 7 (sw); NB = 2 even waves sx, odd waves sw, wave w
+     * into 64-float region w (regions 0 and 1 are the ones read) */
+    const bool srow = NB == 1 ? wave == 6 : (wave & 1) == 0;
+    const __amdgpu_buffer_rsrc_t rs = srow
+        ? __builtin_amdgcn_make_buffer_rsrc((void *)sx, (short)0, (int)((uint32_t)M * (uint32_t)nkb * 4u), GLINT_BUF_DWORD3)
+        : __builtin_amdgcn_make_buffer_rsrc((void *)sw, (short)0, (int)((uint32_t)N * (uint32_t)nkb * 4u), GLINT_BUF_DWORD3);
+    const uint32_t svo = (srow ? (uint32_t)min(m0 + lane, M - 1) : (uint32_t)min(n0 + lane, N - 1)) * (uint32_t)nkb * 4u;
+    const int sreg = NB == 1 ? 64 * (wave - 6) : 64 * wave;
     auto dma = [&](int kb, int buf) {
         const uint32_t kc = (uint32_t)min(kb, nkb - 1);
-        if (wave < 4)
+        if (opA)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rsrc, (__attribute__((address_space(3))) void *)(slotA(buf) + 16 * wave * G2_LDS_ROW), 16, vo, kc * 64u, 0, 0);
-        else if (wave < 6)
+                ra, (__attribute__((address_space(3))) void *)(slotA(buf) + 16 * wave * G2_LDS_ROW), 16, ovo, kc * 64u, 0, 0);
+        else if (opB)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rsrc, (__attribute__((address_space(3))) void *)(slotB(buf) + 16 * (wave - 4) * G2_LDS_ROW), 16, vo, kc * 64u, 0, 0);
-        else
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rsrc, (__attribute__((address_space(3))) void *)(slotS(buf) + 64 * (wave - 6)), 4, vo, kc * 4u, 0, 0);
+                rb, (__attribute__((address_space(3))) void *)(slotB(buf) + 16 * (wave - 4) * G2_LDS_ROW), 16, ovo, kc * 64u,
+                0, 0);
+        if (NB == 2 || (!opA && !opB))
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(slotS(buf) + sreg), 4, svo,
+                                                     kc * 4u, 0, 0);
     };
     const int fr_ofs = g2_lds_ofs(lane & 15, lane >> 4);
     auto slice = [&](int u) {
         const int8_t *ta = slotA(u), *tb = slotB(u);
         const float *ts = slotS(u);
         const glint_i32x4 af = *(const glint_i32x4 *)(ta + (wm * 16) * G2_LDS_ROW + fr_ofs);
-        const glint_i32x4 bf = *(const glint_i32x4 *)(tb + (wn * 16) * G2_LDS_ROW + fr_ofs);
-        const float swv = ts[64 + wn * 16 + (lane & 15)];
         const glint_f32x4 sxv = *(const glint_f32x4 *)(ts + wm * 16 + (lane >> 4) * 4);
-        const glint_i32x4 ic = glint_mfma_i8(af, bf, glint_i32x4{0, 0, 0, 0});
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            acc[i] = __builtin_fmaf((float)ic[i] * sxv[i], swv, acc[i]);
+        for (int b = 0; b < NB; ++b) {
+            const glint_i32x4 bf = *(const glint_i32x4 *)(tb + (wn * 16 * NB + b * 16) * G2_LDS_ROW + fr_ofs);
+            const float swv = ts[64 + wn * 16 * NB + b * 16 + (lane & 15)];
+            const glint_i32x4 ic = glint_mfma_i8(af, bf, glint_i32x4{0, 0, 0, 0});
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[b][i] = __builtin_fmaf((float)ic[i] * sxv[i], swv, acc[b][i]);
+        }
     };
     constexpr int PS = Q_PER_STEP, AHEAD = Q_NBUF - PS;
     auto step = [&](int kb, int u) {
-        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(AHEAD - PS));
+        __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(ND * (AHEAD - PS)));
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
@@ -1066,14 +1085,16 @@ __global__ __launch_bounds__(512) void k_int8_mma_ring8(const int8_t *__restrict
             step(kb + u, u);
     __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int rr = m0 + wm * 16 + (lane >> 4) * 4 + i;
-        const int cc = n0 + wn * 16 + (lane & 15);
-        if (rr < M && cc < N) {
-            float *dst = y + (int64_t)rr * N + cc;
-            *dst = ACCUM ? *dst + acc[i] : acc[i];
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rr = m0 + wm * 16 + (lane >> 4) * 4 + i;
+            const int cc = n0 + wn * 16 * NB + b * 16 + (lane & 15);
+            if (rr < M && cc < N) {
+                float *dst = y + (int64_t)rr * N + cc;
+                *dst = ACCUM ? *dst + acc[b][i] : acc[b][i];
+            }
         }
-    }
 }
 
 /* The W8A8 product: the 256 x 256 DMA-ring kernel where there are enough tiles, else the
@@ -1091,14 +1112,16 @@ static void q_launch_gemm(const int8_t *xq, const float *sx, const int8_t *wq, c
         /* 64 x 32 output tiles (each wave one 16-column block; the loader still stages 64 W
          * rows, half of them unused) where 64 x 64 tiles would leave CUs idle */
         const int64_t tiles64 = (int64_t)((n + Q_BN - 1) / Q_BN) * ((m + Q_BM - 1) / Q_BM);
-        if (Q_NARROW && tiles64 < glint_cu_count()) {
-            if (Q_RING8)
-                k_int8_mma_ring8<ACCUM><<<dim3((n + 31) / 32, (m + Q_BM - 1) / Q_BM), 512, 0, st>>>(xq, wq, sx, sw, y, m,
-                                                                                                   n, k_in);
-            else
-                k_int8_mma_ring<ACCUM, 1><<<dim3((n + 31) / 32, (m + Q_BM - 1) / Q_BM), 256, 0, st>>>(xq, wq, sx, sw, y,
-                                                                                                      m, n, k_in);
-        }
+        const bool narrow = Q_NARROW && tiles64 < glint_cu_count();
+        if (narrow && Q_RING8)
+            k_int8_mma_ring8<ACCUM, 1><<<dim3((n + 31) / 32, (m + Q_BM - 1) / Q_BM), 512, 0, st>>>(xq, wq, sx, sw, y, m,
+                                                                                                  n, k_in);
+        else if (narrow)
+            k_int8_mma_ring<ACCUM, 1><<<dim3((n + 31) / 32, (m + Q_BM - 1) / Q_BM), 256, 0, st>>>(xq, wq, sx, sw, y, m,
+                                                                                                  n, k_in);
+        else if (Q_RING8_WIDE)
+            k_int8_mma_ring8<ACCUM, 2><<<dim3((n + Q_BN - 1) / Q_BN, (m + Q_BM - 1) / Q_BM), 512, 0, st>>>(xq, wq, sx, sw,
+                                                                                                          y, m, n, k_in);
         else
             k_int8_mma_ring<ACCUM, 2><<<dim3((n + Q_BN - 1) / Q_BN, (m + Q_BM - 1) / Q_BM), 256, 0, st>>>(xq, wq, sx, sw,
                                                                                                           y, m, n, k_in);
