@@ -409,7 +409,8 @@ def test_bf16_stream_k(oracle, M, N, K):
 
 
 F32_SHAPES = [(2, 64, 64), (3, 300, 1088), (64, 1024, 4096), (127, 520, 2368), (128, 4096, 576), (300, 1100, 1024),
-              (513, 2048, 4096), (64, 4096, 14336), (100, 14336, 4096)]
+              (513, 2048, 4096), (64, 4096, 14336), (100, 14336, 4096), (24, 1000, 2304), (32, 300, 1152),
+              (48, 777, 640)]
 
 
 @pytest.mark.parametrize("M,N,K", F32_SHAPES)
@@ -417,8 +418,10 @@ def test_f32_prefill_mfma_vs_float64(oracle, M, N, K):
     """The f32-out ABI at M > 1, bs 64 (launch_glint_htile_s3_f32_stream on BF16 MFMA with the
     weights in three exact BF16 planes): against float64, every output within the f32
     summation bound (K + 2) 2^-23 sum|t| and within the reference's 1e-5 (1 + |ref|);
-    ragged M and N (64 x 128 tiles below M = 128, or 64 x 64 where those would leave CUs
-    idle, as at M = 64 on the 4096 x 14336 down shape; 128 x 128 above), split K, odd K steps."""
+    ragged M and N: M <= 64 with K % 128 == 0 on the register-dequantized kernel (one, two or
+    four MFMA row blocks; K split 4 ways on the 4096 x 14336 down shape; half-used last W
+    lines at K = 1152 and 640), 64 x 128 tiles below M = 128 otherwise, 128 x 128 above;
+    split K, odd K steps."""
     torch = torch_cuda()
     print(f"f32 prefill M={M} N={N} K={K}", flush=True)
     hole, plug, am = _encoded_weight(oracle, N, K, 3200 + M)
