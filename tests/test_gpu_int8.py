@@ -126,12 +126,14 @@ def _bands(m, h):
     return sorted({(0, min(h, m)), (max(m // 2 - h // 2, 0), min(m // 2 + h // 2, m)), (max(m - h, 0), m)})
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 24576, 640), (4096, 3100, 1088), (3000, 4100, 64)])
+@pytest.mark.parametrize("m,n,k", [(512, 24576, 640), (4096, 3100, 1088), (3000, 4100, 64), (2048, 6144, 960),
+                                   (4096, 3100, 192)])
 def test_int8_mma_gemm_dma_tiles_match_emulation(oracle, m, n, k):
     """int8_mma_gemm where it takes the 256 x 256 DMA-ring kernel (at least 3/4 as many
-    256 x 256 tiles as CUs on a 256-CU part): ragged N, a ragged slice count (17), a single
-    slice. Activation bytes exact on the whole input; y bit-exact against the oracle's
-    emulation on three 64-row bands (first, middle, last)."""
+    256 x 256 tiles as CUs on a 256-CU part): ragged N; slice counts 10, 17, 1, 15 and 3
+    (its loop runs four slices per pass, so every remainder mod 4 occurs). Activation
+    bytes exact on the whole input; y bit-exact against the oracle's emulation on three
+    64-row bands (first, middle, last)."""
     print(f"int8_mma_gemm dma m={m} n={n} k={k}", flush=True)
     rng = np.random.default_rng(m + n + k)
     x = bf16_bits(rng.normal(0, 1, m * k).astype(np.float32))
