@@ -165,6 +165,131 @@ def bench_gemv(torch, H, steps, warmup, headline_only=False):
     }, pins, x
 
 
+def _gemv_cu_plan(N: int, K: int, cus: int):
+    """k_htile_gemv_cu's launch plan (glint_htile.hip htile_launch_gemv_cu): workgroups and
+    waves per workgroup for an M = 1 GEMV with K % 2048 == 0."""
+    S = K // 2048
+    narrow = S <= 2
+    G = (8 if narrow else 16) // S
+    wgs = cus * (2 if narrow else 1)
+    rows = -(-N // wgs)
+    return -(-N // rows), S * G, rows
+
+
+def _timeline_summary(a, N: int, K: int, wpg: int, rows: int, nbytes: float) -> list:
+    """Text lines for the per-wave stamps `a` (waves x 8, slots as in glint_htile.hip's
+    GLINT_TIMELINE block) of one k_htile_gemv_cu launch."""
+    import numpy as np
+    a = a.astype(np.int64)
+    nw = a.shape[0]
+    T0 = a[:, 0].min()
+    us = lambda v: (v - T0) / 100.0  # s_memrealtime runs at 100 MHz
+    st, rdy, lend, en = us(a[:, 0]), us(a[:, 3]), us(a[:, 4]), us(a[:, 5])
+    mhz = np.median((a[:, 7] - a[:, 2]) / ((a[:, 5] - a[:, 0]) / 100.0))
+    hw = a[:, 1]
+    xcc, se, sh, cu = (hw >> 32) & 0xF, (hw >> 13) & 0x7, (hw >> 12) & 0x1, (hw >> 8) & 0xF
+    items = a[:, 6]
+    wg = np.arange(nw) // wpg
+    nwg = nw // wpg
+    wst = np.array([st[wg == g].min() for g in range(nwg)])
+    wen = np.array([en[wg == g].max() for g in range(nwg)])
+    wit = np.array([items[wg == g].sum() for g in range(nwg)])
+    key = (xcc * 64 + se * 16 + sh * 8)[::wpg] * 16 + cu[::wpg]
+    gen = np.zeros(nwg, dtype=int)
+    for k in np.unique(key):
+        idx = np.nonzero(key == k)[0]
+        gen[idx[np.argsort(wst[idx], kind="stable")]] = np.arange(idx.size)
+    pct = lambda v, q=(0, 10, 50, 90, 100): " ".join(f"{x:6.2f}" for x in np.percentile(v, q))
+    span = en.max()
+    out = [f"{N}x{K}: {nwg} workgroups x {wpg} waves ({rows} rows each) on {np.unique(key).size} CUs; "
+           f"shader clock {mhz:.0f} MHz (s_memtime against s_memrealtime)",
+           f"  kernel span (first wave start to last wave end) {span:.2f} us: {nbytes / span / 1e3:.0f} GB/s "
+           f"({nbytes / span / 1e3 / HBM_PEAK_GBS:.3f} of 8 TB/s) over the span",
+           "  times in us from the first wave's start      p0     p10    p50    p90    p100",
+           f"  wave start                                  {pct(st)}",
+           f"  first item done (table, x, item 1)          {pct(rdy)}",
+           f"  item loop done                              {pct(lend)}",
+           f"  wave end (after the row stores)             {pct(en)}",
+           f"  workgroup end                               {pct(wen)}",
+           f"  per wave: loop (first item done -> loop done) {pct(lend - rdy)}",
+           f"  per wave: items                             {pct(items)}",
+           ]
+    for g in np.unique(gen):
+        m = gen == g
+        out.append(f"  workgroups dispatched {['first', 'second', 'third', 'fourth'][min(g, 3)]} on their CU "
+                   f"({m.sum()}): start p50 {np.median(wst[m]):.2f}, end p10/p50/p90/max "
+                   f"{pct(wen[m], (10, 50, 90, 100))}, items per workgroup p50 {np.median(wit[m]):.0f}, "
+                   f"{np.mean(np.nonzero(m)[0] < nwg // 2) * 100:.0f}% in the first half of the grid")
+    ends = " ".join(f"{np.median(wen[(xcc[::wpg] == x)]):.2f}/{wen[(xcc[::wpg] == x)].max():.2f}"
+                    for x in np.unique(xcc))
+    out.append(f"  workgroup end median/max per XCD: {ends}")
+    return out
+
+
+def gemv_timeline(torch, H, out_path: str, steps: int) -> None:
+    """Per-wave timeline of the decode GEMV (k_htile_gemv_cu) at the headline shape and the
+    down shape, from libglint_encode_tl.so (the same kernels with stamps compiled in): the
+    same rotated pins and timed loop as the headline; the stamps are the loop's last launch."""
+    import ctypes
+    import numpy as np
+    from glint_amd import glint_hip
+    path = glint_hip.LIB_DIR / "libglint_encode_tl.so"
+    if not path.is_file():
+        raise RuntimeError("libglint_encode_tl.so not built: run `python -m glint_amd.build`")
+    tl = ctypes.CDLL(str(path))
+    VP, I = ctypes.c_void_p, ctypes.c_int
+    for name in ("launch_glint_htile_bf16_stream",):
+        getattr(tl, name).argtypes = [VP, VP, VP, VP, VP, I, I, I, I, VP]
+        getattr(tl, name).restype = I
+    tl.glint_timeline_fetch.argtypes = [VP, ctypes.c_size_t]
+    tl.glint_timeline_fetch.restype = I
+    plain = H.encode_lib()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    st = stream_handle(torch)
+    lines = [f"# per-wave timeline of k_htile_gemv_cu (M = 1, bs 64, BF16 out) on {torch.cuda.get_device_name(0)}",
+             "", "command (repo root):", f"  python3 bench.py --timeline {out_path} --steps {steps}", "",
+             "libglint_encode_tl.so is libglint_encode.so built with -DGLINT_TIMELINE: lane 0 of each wave stores",
+             "s_memrealtime (100 MHz) stamps at entry, after its first item (cell table, x and item 1 in),",
+             "after its item loop and after the row stores, plus XCC_ID/HW_ID, its item count and",
+             "s_memtime. The stamps are those of the last launch of a timed loop of back-to-back launches",
+             "over rotated pins (the headline loop's setup). A launch's algorithmic bytes over its span",
+             "exclude the gap between launches, which the per-launch HIP-event time includes.", ""]
+    for N, K in ((GEMV_N, GEMV_K), (4096, 14336)):
+        per = gemv_bytes(N, K)
+        copies = max(17, int(1.05 * 2 ** 30 / per) + 1)
+        g = torch.Generator(device="cuda").manual_seed(2002)
+        pins = []
+        for _ in range(copies):
+            w = (torch.randn(N * K, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+            pins.append(H.encode_bf16(w, 64))
+            del w
+        x = torch.randn(K, device="cuda", generator=g).to(torch.bfloat16)
+        y = torch.empty(N, dtype=torch.bfloat16, device="cuda")
+        f_pl = [bound(plain.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, y, 1, N, K, 64, st) for p in pins]
+        f_tl = [bound(tl.launch_glint_htile_bf16_stream, p[0], p[1], p[2], x, y, 1, N, K, 64, st) for p in pins]
+        settle(torch, f_pl, 0.2)
+        ms_pl = timed(torch, f_pl, steps, 100)
+        settle(torch, f_tl, 0.05)
+        ms_tl = timed(torch, f_tl, steps, 100)
+        grid, wpg, rows = _gemv_cu_plan(N, K, cus)
+        buf = np.zeros(grid * wpg * 8, dtype=np.uint64)
+        rc = tl.glint_timeline_fetch(buf.ctypes.data_as(VP), buf.nbytes)
+        if rc != 0:
+            raise RuntimeError(f"glint_timeline_fetch rc={rc}")
+        a = buf.reshape(grid * wpg, 8)
+        if not (a[:, 0] > 0).all():
+            raise RuntimeError("timeline: waves without stamps (launch plan differs)")
+        lines.append(f"{N}x{K}: {steps} back-to-back launches, HIP events per launch: plain {ms_pl * 1e3:.2f} us "
+                     f"({per / ms_pl / 1e6 / HBM_PEAK_GBS:.3f} of 8 TB/s), instrumented {ms_tl * 1e3:.2f} us")
+        lines += _timeline_summary(a, N, K, wpg, rows, per)
+        lines.append("")
+        del pins
+        torch.cuda.empty_cache()
+    text = "\n".join(lines)
+    Path(out_path).write_text(text)
+    print(text)
+
+
 def bench_gemv_pair(torch, H, steps, warmup):
     """Beside the headline, not instead of it (opt-in: --parts gemvpair, so the default run's
     kernel trace holds only the headline's dispatches of its kernel): a decode step's gate
@@ -1034,6 +1159,8 @@ def main() -> int:
                     help="run the fixed hot-kernel workload for the rocprofv3 counter passes, write its manifest")
     ap.add_argument("--summarize-counters", nargs="+", metavar="ARG",
                     help="MANIFEST tag=DB ... (tags fetch, write, util, inst, trace): write the counter summary")
+    ap.add_argument("--timeline", metavar="OUT",
+                    help="write the per-wave timeline summary of the decode GEMV (libglint_encode_tl.so) to OUT")
     ap.add_argument("--summarize-trace", nargs="+", metavar="DB",
                     help="print the per-kernel table of a rocprofv3 --kernel-trace database [and bench JSON]")
     args = ap.parse_args()
@@ -1061,6 +1188,9 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_name(0)}")
     if args.counter_workload:
         counter_workload(torch, H, args.counter_workload)
+        return 0
+    if args.timeline:
+        gemv_timeline(torch, H, args.timeline, args.steps)
         return 0
     if args.calibrate_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)

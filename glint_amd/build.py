@@ -7,6 +7,8 @@ Outputs (git-ignored, shipped with the tree):
     glint_amd/lib/libglint_encode.so   encode / expand / H-TILE (include/glint_encode.h, glint_htile.h)
     glint_amd/lib/libp7_kernels.so     attach ABI: INT8 GEMM (include/int8_mma_gemm.h, p7_attach.h)
     glint_amd/lib/libglint_probe.so    bench.py's HBM read ceiling (measurement only)
+    glint_amd/lib/libglint_encode_tl.so  libglint_encode.so with the decode GEMV's per-wave
+                                       timeline stamps (bench.py --timeline; measurement only)
     oracle/liboracle.so                CPU oracle (tests only)
     tests/native/bin/abi_caller        C++ caller of the C ABI, linked with -lglint_encode (tests only)
 """
@@ -41,7 +43,12 @@ LIBS = {
     "libp7_kernels.so": ["int8_mma_gemm.hip", "int8_tile_gemm.hip", "p7_abi.cpp", "glint_plug_streamer.cpp", "p7_selftest.cpp"],
     # measurement only (bench.py's read ceiling), not part of the GLINT ABI
     "libglint_probe.so": ["hbm_probe.hip"],
+    # measurement only (bench.py --timeline): libglint_encode.so with the decode GEMV's
+    # per-wave stamps compiled in
+    "libglint_encode_tl.so": ["glint_encode.hip", "glint_htile.hip+tl", "glint_select.hip", "glint_noalloc.hip"],
 }
+# source variants: "<file>+<tag>" compiles <file> with these extra flags
+VARIANT_FLAGS = {"tl": ["-DGLINT_TIMELINE=1"]}
 
 
 def _run(cmd, **kw):
@@ -65,16 +72,17 @@ def gen_code_table() -> None:
 
 
 def _compile(src: str) -> Path:
-    obj = BUILD / (src + ".o")
-    lang = ["-x", "hip"] if src.endswith(".hip") else []
-    _run([HIPCC, *HIP_FLAGS, *lang, "-c", str(CSRC / src), "-o", str(obj)])
+    file, _, tag = src.partition("+")
+    obj = BUILD / (file + (f".{tag}" if tag else "") + ".o")
+    lang = ["-x", "hip"] if file.endswith(".hip") else []
+    _run([HIPCC, *HIP_FLAGS, *VARIANT_FLAGS.get(tag, []), *lang, "-c", str(CSRC / file), "-o", str(obj)])
     return obj
 
 
 def build_libs() -> None:
     BUILD.mkdir(exist_ok=True)
     LIB.mkdir(exist_ok=True)
-    srcs = [s for files in LIBS.values() for s in files if (CSRC / s).is_file()]
+    srcs = list(dict.fromkeys(s for files in LIBS.values() for s in files if (CSRC / s.partition("+")[0]).is_file()))
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = dict(zip(srcs, ex.map(_compile, srcs)))
     for lib, files in LIBS.items():

@@ -371,6 +371,28 @@ __global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(GEMV_X_WPE
 #define GEMV_CU_SMAX 16 /* K <= 32768 */
 #define GEMV_CU_DYN_MAX (28 * 1024) /* bytes of dynamic LDS: the partials, 16 S per row */
 
+/* Per-wave timeline of k_htile_gemv_cu, compiled only into the measurement library
+ * libglint_encode_tl.so (-DGLINT_TIMELINE). A wave keeps its stamps in registers and
+ * lane 0 stores them when the wave ends, so each launch overwrites the slots of the one
+ * before it and the last launch's stamps remain. Slots of wave blockIdx.x * waves + w:
+ *   0 s_memrealtime (100 MHz) at entry      1 XCC_ID << 32 | HW_ID
+ *   2 s_memtime (shader clock) at entry     3 s_memrealtime after the first item
+ *   4 s_memrealtime after the item loop     5 s_memrealtime after the row stores
+ *   6 items computed by the wave            7 s_memtime after the row stores */
+#ifdef GLINT_TIMELINE
+#define GLINT_TL_SLOTS 8
+#define GLINT_TL_WAVES 16384
+__device__ unsigned long long g_glint_tl[GLINT_TL_WAVES * GLINT_TL_SLOTS];
+extern "C" __attribute__((visibility("default"))) int glint_timeline_fetch(void *dst, size_t bytes) {
+    if (!dst || bytes > sizeof(g_glint_tl))
+        return (int)hipErrorInvalidValue;
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_glint_tl), bytes, 0, hipMemcpyDeviceToHost);
+}
+#define GEMV_TL(stmt) stmt
+#else
+#define GEMV_TL(stmt)
+#endif
+
 template <bool OUT_BF16, int XC, int NT, int XS, bool XFIRST>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_htile_gemv_cu(
     const uint8_t *__restrict__ hole, const uint8_t *__restrict__ plug, const float *__restrict__ absmax,
@@ -393,6 +415,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 4))) void
     const int s = w % S, g = w / S;
     const int r0 = blockIdx.x * rows_per_wg;
     const int nrows = max(min(rows_per_wg, N - r0), 0);
+    GEMV_TL(const unsigned long long tl_t0 = __builtin_amdgcn_s_memrealtime();
+            const unsigned long long tl_m0 = __builtin_amdgcn_s_memtime();
+            const unsigned long long tl_hw = ((unsigned long long)__builtin_amdgcn_s_getreg(63508) << 32) |
+                                             (unsigned)__builtin_amdgcn_s_getreg(63492);
+            unsigned long long tl_t1 = 0; int tl_items = 0;)
 
     /* the band's rows of each plane and of absmax; offsets at or past num_records load zeros */
     const uint32_t rowb = (uint32_t)K >> 1; /* bytes of a row in each plane */
@@ -492,10 +519,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         const float v = glint_row16_sum(sc);
         if ((lane & 15) == 0)
             red[(item * S + s) * 4 + (lane >> 4)] = v;
+        GEMV_TL(++tl_items;)
     };
     /* first item (landed before the barrier) */
     if (cur < nrows)
         compute(bufA, cur);
+    GEMV_TL(tl_t1 = __builtin_amdgcn_s_memrealtime();)
     /* steady state: wait for the item in `row` (the only one in flight), send the next
      * claimed item's loads into `other` (past the band they are dropped by the buffer range
      * check), compute. Items are claimed in increasing order, so once `nxt` is past the band
@@ -521,6 +550,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         step(bufB, bufA);
         step(bufA, bufB);
     }
+    GEMV_TL(const unsigned long long tl_t2 = __builtin_amdgcn_s_memrealtime();)
     __syncthreads();
 
     for (int t = threadIdx.x; t < nrows; t += blockDim.x) {
@@ -533,6 +563,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 4))) void
         else
             ((float *)y)[row] = sum;
     }
+#ifdef GLINT_TIMELINE
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0); /* the row stores have left the wave */
+    const unsigned long long tl_t3 = __builtin_amdgcn_s_memrealtime(), tl_m1 = __builtin_amdgcn_s_memtime();
+    const int tl_w = (int)blockIdx.x * (int)(blockDim.x >> 6) + w;
+    if (lane == 0 && tl_w < GLINT_TL_WAVES) {
+        unsigned long long *o = g_glint_tl + (size_t)tl_w * GLINT_TL_SLOTS;
+        o[0] = tl_t0; o[1] = tl_hw; o[2] = tl_m0; o[3] = tl_t1;
+        o[4] = tl_t2; o[5] = tl_t3; o[6] = (unsigned long long)tl_items; o[7] = tl_m1;
+    }
+#endif
 }
 
 /* ------------------------------------------------- small-M decode GEMV (BF16 out) */
