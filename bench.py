@@ -599,6 +599,59 @@ def bench_w8a16(torch, H, steps: int, copies: int = 6):
     return out
 
 
+def kmajor_step_graphs(torch, lib, pins, x, y, part, idx, cnt, N, K, ksg, ks, nsel, reps: int = 20):
+    """The K-major decode step over every pin, captured into a HIP graph and replayed
+    (per-step ms, HIP events around `reps` replays). Two graphs: the three calls in order on
+    one stream, and the selection on a second stream beside the fold (it needs only x),
+    joined by events before the correction. The selection of step i + 1 waits for step i's
+    correction, which reads idx and cnt. Both capture streams have a split-K workspace, so
+    the fold and correction add their slices in-kernel as in the eager loop."""
+    import ctypes
+
+    def vp(t):
+        return ctypes.c_void_p(t.data_ptr())
+
+    out = []
+    for beside in (False, True):
+        s, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        hs, hs2 = ctypes.c_void_p(s.cuda_stream), ctypes.c_void_p(s2.cuda_stream)
+        if lib.glint_htile_workspace_reserve(hs) != 0:
+            raise RuntimeError("glint_htile_workspace_reserve failed")
+        s.wait_stream(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for pk in pins:
+                if beside:
+                    s2.wait_stream(s)
+                    rc = lib.glint_select_topk(vp(x), K, nsel, vp(idx), vp(cnt), hs2)
+                    join = torch.cuda.Event()
+                    join.record(s2)
+                else:
+                    rc = lib.glint_select_topk(vp(x), K, nsel, vp(idx), vp(cnt), hs)
+                rc |= lib.glint_gemv_km_fold(vp(pk[0]), vp(pk[2]), vp(x), vp(y), N, K, ksg, vp(part), hs)
+                if beside:
+                    s.wait_event(join)
+                rc |= lib.glint_apply_corr_km(vp(pk[0]), vp(pk[1]), vp(pk[2]), vp(x), vp(idx), vp(cnt), vp(y), N, K,
+                                              ks, vp(part), hs)
+                if rc != 0:
+                    raise RuntimeError(f"k-major step capture rc={rc}")
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(reps):
+                g.replay()
+            e1.record(s)
+        e1.synchronize()
+        out.append(e0.elapsed_time(e1) / (reps * len(pins)))
+        del g
+        lib.glint_htile_workspace_release(hs)
+    return out
+
+
 def bench_kmajor(torch, H, steps: int = 200, copies: int = 20):
     """The K-major decode step at the decode shape (N 14336, K 4096): fold GEMV (HBM bytes:
     hole_k N K / 2 + scales_k N K / 16 + x + y), device selection of 10% of the channels,
@@ -641,6 +694,7 @@ def bench_kmajor(torch, H, steps: int = 200, copies: int = 20):
             corrs[i]()
         return run
     ms_step = timed(torch, [step_of(i) for i in range(copies)], steps, 10)
+    ms_graph, ms_graph2 = kmajor_step_graphs(torch, lib, pins, x, y, part, idx, cnt, N, K, ksg, ks, nsel)
     # the reference's capacity mode: plug_k stays in mapped pinned host memory and the
     # correction reads only the selected channels' rows over the bus
     import ctypes
@@ -663,6 +717,7 @@ def bench_kmajor(torch, H, steps: int = 200, copies: int = 20):
     return {"config": f"N {N} K {K}, fold ksg {ksg}, 10% of channels selected, correction ks {ks}",
             "fold_ms": ms_fold, "fold_gbs": fold_bytes / ms_fold / 1e6, "fold_frac": fold_bytes / ms_fold / 1e6 / HBM_PEAK_GBS,
             "select_ms": ms_sel, "corr_ms": ms_corr, "step_ms": ms_step, "selected": int(cnt.item()),
+            "step_graph_ms": ms_graph, "step_graph_select_beside_fold_ms": ms_graph2,
             "corr_host_plug_ms": ms_corr_host,
             "resident_bytes_per_weight": 0.5 + 4 / 64, "full_gemv_resident_bytes_per_weight": 1 + 4 / 64}
 
