@@ -238,9 +238,8 @@ def gemv_timeline(torch, H, out_path: str, steps: int) -> None:
         raise RuntimeError("libglint_encode_tl.so not built: run `python -m glint_amd.build`")
     tl = ctypes.CDLL(str(path))
     VP, I = ctypes.c_void_p, ctypes.c_int
-    for name in ("launch_glint_htile_bf16_stream",):
-        getattr(tl, name).argtypes = [VP, VP, VP, VP, VP, I, I, I, I, VP]
-        getattr(tl, name).restype = I
+    tl.launch_glint_htile_bf16_stream.argtypes = [VP, VP, VP, VP, VP, I, I, I, I, VP]
+    tl.launch_glint_htile_bf16_stream.restype = I
     tl.glint_timeline_fetch.argtypes = [VP, ctypes.c_size_t]
     tl.glint_timeline_fetch.restype = I
     plain = H.encode_lib()
