@@ -632,6 +632,135 @@ __global__ __launch_bounds__(G3_THREADS) void k_int8_gemm_dma(const int8_t *__re
             }
 }
 
+/* k_int8_gemm_dma with a 5-slot ring and one barrier per two K steps. A per-step timeline
+ * of k_int8_gemm_dma (s_memtime stamps in a timing copy) showed each SIMD's older wave done
+ * issuing its step in about 780 clocks and the younger in about 1320, the older then
+ * waiting at the barrier: per step the MFMA pipe idles through the wait and the barrier
+ * (about 250 clocks) besides the 1024 clocks of MFMAs. Here an even step kb waits for its
+ * own loads of steps up to kb + 2, passes the barrier, and loads steps kb + 4 and kb + 5
+ * into the slots of steps kb - 1 and kb (whose fragments every wave has read); an odd step
+ * only multiplies and reads the next step's fragments, which the even step's barrier
+ * already made visible. Loads still run two steps ahead of the wait that needs them. The
+ * 5 slots are the whole 160 KiB of LDS. */
+template <bool SCALED>
+__global__ __launch_bounds__(512) void k_int8_gemm_dma5(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
+                                                        const float *__restrict__ sa, const float *__restrict__ sb,
+                                                        void *__restrict__ C, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) int8_t sA0[G2_BM * G2_LDS_ROW], sA1[G2_BM * G2_LDS_ROW],
+        sA2[G2_BM * G2_LDS_ROW], sA3[G2_BM * G2_LDS_ROW], sA4[G2_BM * G2_LDS_ROW];
+    __shared__ __attribute__((aligned(16))) int8_t sB0[G2_BN * G2_LDS_ROW], sB1[G2_BN * G2_LDS_ROW],
+        sB2[G2_BN * G2_LDS_ROW], sB3[G2_BN * G2_LDS_ROW], sB4[G2_BN * G2_LDS_ROW];
+    auto bufA = [&](int i) { return i == 0 ? sA0 : (i == 1 ? sA1 : (i == 2 ? sA2 : (i == 3 ? sA3 : sA4))); };
+    auto bufB = [&](int i) { return i == 0 ? sB0 : (i == 1 ? sB1 : (i == 2 ? sB2 : (i == 3 ? sB3 : sB4))); };
+    constexpr int NW = 8, WNW = 4, TM = 8, TN = 4, RPW = 32, QN = 2, NS = 5;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WNW, wn = wave % WNW;
+    const int m0 = blockIdx.y * G2_BM, n0 = blockIdx.x * G2_BN;
+    const int nkb = K / 64;
+    glint_i32x4 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+            acc[a][b] = glint_i32x4{0, 0, 0, 0};
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)A, (short)0, (int)((uint32_t)M * (uint32_t)K), GLINT_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)B, (short)0, (int)((uint32_t)N * (uint32_t)K), GLINT_BUF_DWORD3);
+    uint32_t avo[QN], bvo[QN];
+#pragma unroll
+    for (int q = 0; q < QN; ++q) {
+        const int r = RPW * wave + 16 * q + (lane >> 2);
+        const int c = (lane & 3) ^ (((r >> 1) ^ ((r >> 3) & 1)) & 3);
+        avo[q] = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)c * 16u;
+        bvo[q] = (uint32_t)min(n0 + r, N - 1) * (uint32_t)K + (uint32_t)c * 16u;
+    }
+    auto dma = [&](int kb, int buf) {
+        const uint32_t so = (uint32_t)min(kb, nkb - 1) * 64u;
+#pragma unroll
+        for (int q = 0; q < QN; ++q) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void *)(bufA(buf) + (RPW * wave + 16 * q) * G2_LDS_ROW), 16,
+                avo[q], so, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void *)(bufB(buf) + (RPW * wave + 16 * q) * G2_LDS_ROW), 16,
+                bvo[q], so, 0, 0);
+        }
+    };
+    const int fr_ofs = g2_lds_ofs(lane & 15, lane >> 4);
+    struct Frags {
+        glint_i32x4 a[TM], b[TN];
+    };
+    Frags fr[2];
+    auto read_frags = [&](int u, Frags &f) {
+        const int8_t *ta = bufA(u), *tb = bufB(u);
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+            f.b[b] = *(const glint_i32x4 *)(tb + (wn * TN * 16 + b * 16) * G2_LDS_ROW + fr_ofs);
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+            f.a[a] = *(const glint_i32x4 *)(ta + (wm * 128 + a * 16) * G2_LDS_ROW + fr_ofs);
+    };
+    /* step kb in slot u = kb % NS, fragments in set p = kb % 2 (constants after unrolling) */
+    auto step = [&](int kb, int u, int p) {
+        if (p == 0) {
+            __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(2 * QN)); /* only step kb + 3's remain */
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
+            dma(kb + 4, (u + 4) % NS);
+            dma(kb + 5, u);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        Frags &f = fr[p];
+        read_frags((u + 1) % NS, fr[p ^ 1]); /* past the end: clamped data nobody uses */
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+                acc[a][b] = glint_mfma_i8(f.a[a], f.b[b], acc[a][b]);
+#pragma unroll
+        for (int i = 0; i < TM + TN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); /* LDS read */
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0); /* MFMA */
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        dma(i, i);
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT_LGKM0(2 * QN * 2)); /* steps 0 and 1 landed */
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "global");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "global");
+    read_frags(0, fr[0]);
+    int kb = 0;
+    for (; kb + 2 * NS <= nkb; kb += 2 * NS) {
+#pragma unroll
+        for (int i = 0; i < 2 * NS; ++i)
+            step(kb + i, i % NS, i & 1);
+    }
+#pragma unroll
+    for (int i = 0; i + 1 < 2 * NS; ++i)
+        if (kb + i < nkb)
+            step(kb + i, i % NS, i & 1);
+    __builtin_amdgcn_s_waitcnt(GLINT_WAIT_VMCNT0); /* the ring's last (clamped) loads land first */
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = m0 + wm * 128 + a * 16 + (lane >> 4) * 4 + i;
+                const int c = n0 + wn * TN * 16 + b * 16 + (lane & 15);
+                if (r < M && c < N) {
+                    if (SCALED)
+                        ((uint16_t *)C)[(int64_t)r * N + c] = glint_f32_to_bf16(((float)acc[a][b][i] * sa[r]) * sb[c]);
+                    else
+                        ((int32_t *)C)[(int64_t)r * N + c] = acc[a][b][i];
+                }
+            }
+}
+
 /* The attach ABI's W8A8 GEMM on the same 256 x 256 DMA ring (int8_mma_gemm at the shapes
  * with at least 3/4 as many 256 x 256 tiles as CUs). Per 64-slice kb the wave's 32 MFMAs
  * run with zero C (ic = the slice's exact int32 dot products), and each A tile's 4 results
@@ -934,6 +1063,9 @@ __global__ __launch_bounds__(256) void k_int8_mma_ring(const int8_t *__restrict_
 #ifndef G3_DMA
 #define G3_DMA 1
 #endif
+#ifndef G3_RING5
+#define G3_RING5 1 /* the plain GEMM on k_int8_gemm_dma5 (5-slot ring, a barrier every two steps) */
+#endif
 static inline bool g3_fits(int M, int N, int K) {
     return G3_DMA && (int64_t)M * K < ((int64_t)1 << 31) && (int64_t)N * K < ((int64_t)1 << 31);
 }
@@ -1201,7 +1333,10 @@ GLINT_API int glint_int8_gemm_i32(const int8_t *A, const int8_t *B, int32_t *C, 
     if (!A || !B || !C || M < 1 || N < 1 || K < 64 || (K % 64) != 0 || !glint_aligned(A, 16) || !glint_aligned(B, 16))
         return (int)hipErrorInvalidValue;
     const bool big = g2_pays(M, N);
-    if (big && g3_fits(M, N, K))
+    if (big && g3_fits(M, N, K) && G3_RING5)
+        k_int8_gemm_dma5<false><<<dim3((N + G2_BN - 1) / G2_BN, (M + G2_BM - 1) / G2_BM), 512, 0, (hipStream_t)stream>>>(
+            A, B, nullptr, nullptr, C, M, N, K);
+    else if (big && g3_fits(M, N, K))
         k_int8_gemm_dma<false><<<dim3((N + G2_BN - 1) / G2_BN, (M + G2_BM - 1) / G2_BM), G3_THREADS, 0,
                                              (hipStream_t)stream>>>(
             A, B, nullptr, nullptr, C, M, N, K);
@@ -1220,7 +1355,10 @@ GLINT_API int glint_int8_gemm_scaled_bf16(const int8_t *A, const int8_t *B, cons
         !glint_aligned(B, 16))
         return (int)hipErrorInvalidValue;
     const bool big = g2_pays(M, N);
-    if (big && g3_fits(M, N, K))
+    if (big && g3_fits(M, N, K) && G3_RING5)
+        k_int8_gemm_dma5<true><<<dim3((N + G2_BN - 1) / G2_BN, (M + G2_BM - 1) / G2_BM), 512, 0, (hipStream_t)stream>>>(
+            A, B, sa, sb, out, M, N, K);
+    else if (big && g3_fits(M, N, K))
         k_int8_gemm_dma<true><<<dim3((N + G2_BN - 1) / G2_BN, (M + G2_BM - 1) / G2_BM), G3_THREADS, 0,
                                             (hipStream_t)stream>>>(
             A, B, sa, sb, out, M, N, K);
