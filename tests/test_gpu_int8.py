@@ -86,12 +86,15 @@ def test_int8_gemm_exact(oracle, M, N, K):
     assert np.array_equal(out, oracle.int8_scale_bf16(ref, sa, sb, M, N))
 
 
-@pytest.mark.parametrize("M,N,K", [(4096, 3100, 640), (3000, 4100, 64), (4096, 3100, 128), (3100, 4096, 192)])
+@pytest.mark.parametrize("M,N,K", [(4096, 3100, 640), (3000, 4100, 64), (4096, 3100, 128), (3100, 4096, 192),
+                                   (4096, 3100, 448), (3100, 4096, 1216)])
 def test_int8_gemm_dma_tiles_exact(oracle, M, N, K):
-    """The 256 x 256 kernel whose operands go HBM -> LDS directly (a 4-deep ring of K steps)
-    runs once there are at least 3/4 as many 256 x 256 tiles as CUs: these shapes on a
-    256-CU part, with ragged M and N, 10 K steps (not a multiple of the ring), 1, 2 and 3. Exact int32 against the oracle on the first and last 256-row bands; every row and
-    column through exact int64 row and column sums (sum_n C[m, n] = A[m] . sum_n B[n])."""
+    """The 256 x 256 kernel whose operands go HBM -> LDS directly (a 5-slot ring of K steps,
+    a barrier every two steps, the loop unrolled over 10) runs once there are at least 3/4
+    as many 256 x 256 tiles as CUs: these shapes on a 256-CU part, with ragged M and N and
+    10, 1, 2, 3, 7 and 19 K steps. Exact int32 against the oracle on the first and last
+    256-row bands; every row and column through exact int64 row and column sums
+    (sum_n C[m, n] = A[m] . sum_n B[n])."""
     print(f"int8_gemm dma M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M + 3 * N + K)
     A = rng.integers(-127, 128, (M, K), dtype=np.int8)
